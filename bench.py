@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Reshard-repack benchmark on one MI355X.
+
+Default workload: Llama-2-7B shape (6.74e9 params), bf16 params + fp32 main /
+exp_avg / exp_avg_sq, world 8 simulated on one GPU, distributed optimizer with
+40M-element buckets, TP1 PP1 DP8 -> TP4 PP1 DP2, emitting every target shard.
+
+A step is one execution of the switch's copy plan (one kernel launch) with
+every source shard already resident in HBM.  Inputs are synthetic: seeded
+values ~N(0, 0.02) for bf16 params, main = their exact upcast, exp_avg
+~N(0, 1e-3), exp_avg_sq = |N(0, 1e-6)|.  The destination is checked
+bit-exact against the generator after warm-up.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Prints one JSON line.  ``value`` is payload throughput: bytes of model state
+(bf16 params + fp32 optimizer state) delivered to the target layout per
+second; ``roofline.achieved`` counts HBM traffic (each payload byte read once
+and written once).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "reshard repack GB/s & ms (params+Adam state), Llama-2-7B TP1DP8→TP4DP2, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+SEED = 1234
+
+
+def workloads():
+    from elasticmegatron_amd import ParallelStrategy as PS
+    from elasticmegatron_amd.resharding import model_spec as ms
+
+    return {
+        "llama2-7b-tp1dp8-tp4dp2": ("Llama-2-7B TP1PP1DP8 -> TP4PP1DP2, world 8, 40M buckets",
+                                    ms.llama2_7b, PS(8, 1, 1), PS(8, 4, 1)),
+        "tiny-llama2-tp2dp4-tp1dp8": ("tiny LLaMA-2 (2L h512) TP2DP4 -> TP1DP8, world 8",
+                                      ms.tiny_llama2, PS(8, 2, 1), PS(8, 1, 1)),
+        "tiny-llama2-tp1dp8-tp4dp2": ("tiny LLaMA-2 (2L h512) TP1DP8 -> TP4DP2, world 8",
+                                      ms.tiny_llama2, PS(8, 1, 1), PS(8, 4, 1)),
+        "llama3-8b-tp2pp2dp2-tp4pp1dp2": ("Llama-3-8B GQA TP2PP2DP2 -> TP4PP1DP2, world 8",
+                                          ms.llama3_8b, PS(8, 2, 2), PS(8, 4, 1)),
+        "mixtral-4l-ep4-ep8": ("Mixtral-8x7B 4-layer slice EP4 (EDP2) -> EP8 (EDP1), world 8",
+                               ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4),
+                               PS(8, 1, 1, expert_model_parallel_size=8)),
+        "llama2-7b-dp8-dp6": ("Llama-2-7B world 8 DP8 -> world 6 DP6", ms.llama2_7b, PS(8, 1, 1), PS(6, 1, 1)),
+        "llama2-7b-groupzero-1-2": ("Llama-2-7B Group ZeRO instances 1 -> 2 (world 6 -> 12), fp32 only",
+                                    ms.llama2_7b, PS(6, 1, 1),
+                                    PS(12, 1, 1, num_distributed_optimizer_instances=2)),
+    }
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="llama2-7b-tp1dp8-tp4dp2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--copy-calibration-gib", type=float, default=0.0,
+                    help="time a single contiguous copy of this many GiB instead (traffic calibration)")
+    return ap.parse_args()
+
+
+def cpu_baseline(spec_fn, src, dst, backup):
+    """Oracle-1 (the reference's three-pass executor restated on CPU torch tensors) on layer 0."""
+    import torch
+
+    from oracle import model
+    from oracle import transfer as oracle1
+    from oracle.plan import Strat
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    spec = spec_fn()
+    inv = model.inventory(spec)
+    params = {p["id"] for p in inv if p["layer"] == 0}
+    S, D = Strat.of(src), Strat.of(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED, params)
+    t0 = time.perf_counter()
+    if backup is None:
+        dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
+        payload = sum((i.rng[1] - i.rng[0]) * 12 for infos in dw.values() for i in infos.values())
+        payload += sum(a.size * 2 for a in dbf.values())
+    else:
+        dw = oracle1.redundant_backup(inv, spec, S, D, world, backup)
+        payload = sum((i.rng[1] - i.rng[0]) * 12 for infos in dw.values() for i in infos.values())
+    dt = time.perf_counter() - t0
+    n = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
+    return {"value": round(payload / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"transformer layer 0 ({len(params)} params, {n} elements) of the same switch, "
+                      f"{payload / 1e9:.2f} GB payload in {dt:.2f} s; torch CPU threads={cores}"}
+
+
+def main():
+    args = parse()
+    ws = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or ws != 1:
+        print("bench.py measures one GPU: the reshard is simulated for every rank on a single device; "
+              "run it with --gpus 1 (multi-GPU runs are not part of this build).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _native.load()
+    stream = torch.cuda.current_stream(dev)
+
+    if args.copy_calibration_gib > 0:
+        return copy_calibration(args, dev, stream)
+
+    desc, spec_fn, src, dst = workloads()[args.workload]
+    backup = ParallelStrategy.is_redundant_backup(src, dst)
+    spec = spec_fn()
+    t0 = time.time()
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+    plan = tm.compile(ls, ld, kind)
+    t_plan = time.time() - t0
+    a = TrainingState.allocate(ls, dev)
+    b = TrainingState.allocate(ld, dev, param=a.param if backup is not None else None)
+    a.fill_synthetic(SEED, bf16=True)
+    torch.cuda.synchronize()
+    print(f"[bench] {args.workload}: plan {plan.segments.shape[0]} segments, payload {plan.payload_bytes / 1e9:.2f} GB,"
+          f" planning {t_plan:.2f}s", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        tm.execute(plan, a, b, stream)
+    torch.cuda.synchronize()
+    verified = None
+    if not args.no_verify:
+        bad, first = b.verify_synthetic(SEED, bf16=backup is None)
+        verified = bad == 0
+        if bad:
+            print(f"[bench] verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+            return 3
+
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    events[0].record(stream)
+    for i in range(args.steps):
+        tm.execute(plan, a, b, stream)
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3
+    step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
+    ms = sum(step_ms) / len(step_ms)
+    payload = plan.payload_bytes
+    gbps = payload / (ms / 1e3) / 1e9
+    traffic_gbps = 2 * payload / (ms / 1e3) / 1e9
+
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"{args.workload}.traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16+fp32 (bitwise copy)",
+        "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
+        "config": {"workload": desc, "params": spec.num_params(), "payload_bytes": payload,
+                   "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
+                   "wall_ms_per_step": round(wall_ms / args.steps, 4),
+                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4)},
+        "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
+    }
+    del a, b
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def copy_calibration(args, dev, stream):
+    """One contiguous segment of known size: the reference point for HBM counters."""
+    import numpy as np
+    import torch
+
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
+
+    n = int(args.copy_calibration_gib * (1 << 30)) // 16 * 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty(n, dtype=torch.float32, device=dev)
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0)
+    plan = _native.Plan(t, [n * 4], [n * 4])
+    for _ in range(args.warmup):
+        plan.execute([a.data_ptr()], [b.data_ptr()], stream.cuda_stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        plan.execute([a.data_ptr()], [b.data_ptr()], stream.cuda_stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    print(json.dumps({"copy_bytes": n * 4, "ms": round(ms, 4),
+                      "traffic_GBps": round(2 * n * 4 / (ms / 1e3) / 1e9, 1)}), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

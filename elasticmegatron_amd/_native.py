@@ -1,0 +1,194 @@
+"""ctypes binding of libemrs (include/emrs.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``python -m elasticmegatron_amd.build``) into
+``elasticmegatron_amd/csrc/libemrs.so``.  There is no fallback: when the
+library is missing every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+from .resharding.layout import PIECE_DTYPE, SEGMENT_DTYPE
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "csrc", "libemrs.so")
+
+EMRS_OK = 0
+ERRORS = {
+    -1: "EMRS_ERR_INVALID_ARGUMENT",
+    -2: "EMRS_ERR_OUT_OF_BOUNDS",
+    -3: "EMRS_ERR_MISALIGNED",
+    -4: "EMRS_ERR_OVERLAP",
+    -5: "EMRS_ERR_HIP",
+    -6: "EMRS_ERR_NO_DEVICE",
+    -7: "EMRS_ERR_TOO_MANY_BUFFERS",
+    -8: "EMRS_ERR_ALIAS",
+}
+EMRS_PLAN_CHECK_DISJOINT = 1
+EMRS_MAX_BUFFERS = 128
+
+# Every function include/emrs.h declares.
+EXPORTS = (
+    "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
+    "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
+    "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify",
+)
+
+
+class EmrsError(RuntimeError):
+    def __init__(self, code: int, where: str, msg: str):
+        super().__init__(f"{where}: {ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class PlanStats(ctypes.Structure):
+    _fields_ = [
+        ("n_segments", ctypes.c_uint64), ("n_device_segments", ctypes.c_uint64),
+        ("payload_bytes", ctypes.c_uint64), ("vector_bytes", ctypes.c_uint64),
+        ("scalar_bytes", ctypes.c_uint64), ("n_chunks", ctypes.c_uint64),
+        ("n_src_bufs", ctypes.c_uint32), ("n_dst_bufs", ctypes.c_uint32),
+    ]
+
+
+class Tuning(ctypes.Structure):
+    _fields_ = [("blocks_per_cu", ctypes.c_uint32), ("nontemporal", ctypes.c_uint32),
+                ("xcd_remap", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libemrs; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"libemrs is not built ({path} missing); run __graft_entry__.build() or "
+            "python -m elasticmegatron_amd.build")
+    lib = ctypes.CDLL(path)
+    P, U64, U32, I = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int
+    lib.emrs_last_error.restype = ctypes.c_char_p
+    lib.emrs_last_error.argtypes = []
+    lib.emrs_abi_version.restype = I
+    lib.emrs_device_count.restype = I
+    lib.emrs_plan_create.restype = I
+    lib.emrs_plan_create.argtypes = [P, U64, P, U32, P, U32, U32, ctypes.POINTER(P)]
+    lib.emrs_plan_stats_get.restype = I
+    lib.emrs_plan_stats_get.argtypes = [P, ctypes.POINTER(PlanStats)]
+    lib.emrs_plan_execute.restype = I
+    lib.emrs_plan_execute.argtypes = [P, P, P, P]
+    lib.emrs_plan_destroy.restype = I
+    lib.emrs_plan_destroy.argtypes = [P]
+    lib.emrs_get_tuning.restype = I
+    lib.emrs_get_tuning.argtypes = [ctypes.POINTER(Tuning)]
+    lib.emrs_set_tuning.restype = I
+    lib.emrs_set_tuning.argtypes = [ctypes.POINTER(Tuning)]
+    lib.emrs_synth_fill.restype = I
+    lib.emrs_synth_fill.argtypes = [P, U64, P, P, U32, U64, P]
+    lib.emrs_synth_verify.restype = I
+    lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
+    if lib.emrs_abi_version() != 1:
+        raise RuntimeError("libemrs ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def _check(rc: int, where: str) -> None:
+    if rc != EMRS_OK:
+        raise EmrsError(rc, where, load().emrs_last_error().decode(errors="replace"))
+
+
+def _ptr_array(ptrs: Sequence[int]):
+    arr = (ctypes.c_void_p * max(1, len(ptrs)))()
+    for i, p in enumerate(ptrs):
+        arr[i] = ctypes.c_void_p(int(p))
+    return arr
+
+
+def _u64_array(vals: Sequence[int]):
+    arr = (ctypes.c_uint64 * max(1, len(vals)))()
+    for i, v in enumerate(vals):
+        arr[i] = int(v)
+    return arr
+
+
+def device_count() -> int:
+    return int(load().emrs_device_count())
+
+
+def get_tuning() -> Tuning:
+    t = Tuning()
+    _check(load().emrs_get_tuning(ctypes.byref(t)), "emrs_get_tuning")
+    return t
+
+
+def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = False) -> None:
+    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, 0)
+    _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
+
+
+class Plan:
+    """An uploaded-on-demand copy plan (emrs_plan)."""
+
+    def __init__(self, segments: np.ndarray, src_buf_bytes: Sequence[int], dst_buf_bytes: Sequence[int],
+                 check_disjoint: bool = False):
+        lib = load()
+        segs = np.ascontiguousarray(segments, dtype=SEGMENT_DTYPE)
+        self._handle = ctypes.c_void_p()
+        self.n_src = len(src_buf_bytes)
+        self.n_dst = len(dst_buf_bytes)
+        sb, db = _u64_array(src_buf_bytes), _u64_array(dst_buf_bytes)
+        rc = lib.emrs_plan_create(segs.ctypes.data if len(segs) else None, len(segs), sb, self.n_src,
+                                  db, self.n_dst, EMRS_PLAN_CHECK_DISJOINT if check_disjoint else 0,
+                                  ctypes.byref(self._handle))
+        _check(rc, "emrs_plan_create")
+
+    def stats(self) -> PlanStats:
+        st = PlanStats()
+        _check(load().emrs_plan_stats_get(self._handle, ctypes.byref(st)), "emrs_plan_stats_get")
+        return st
+
+    def execute(self, src_ptrs: Sequence[int], dst_ptrs: Sequence[int], stream: int = 0) -> None:
+        if len(src_ptrs) != self.n_src or len(dst_ptrs) != self.n_dst:
+            raise ValueError("wrong number of base pointers")
+        rc = load().emrs_plan_execute(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
+                                      ctypes.c_void_p(int(stream)))
+        _check(rc, "emrs_plan_execute")
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None):
+            load().emrs_plan_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def synth_fill(pieces: np.ndarray, ptrs: Sequence[int], buf_bytes: Sequence[int], seed: int, stream: int = 0) -> None:
+    pcs = np.ascontiguousarray(pieces, dtype=PIECE_DTYPE)
+    rc = load().emrs_synth_fill(pcs.ctypes.data if len(pcs) else None, len(pcs), _ptr_array(ptrs),
+                                _u64_array(buf_bytes), len(ptrs), int(seed), ctypes.c_void_p(int(stream)))
+    _check(rc, "emrs_synth_fill")
+
+
+def synth_verify(pieces: np.ndarray, ptrs: Sequence[int], buf_bytes: Sequence[int], seed: int,
+                 stream: int = 0):
+    """(mismatching elements, first bad (piece index, element index) or None)."""
+    pcs = np.ascontiguousarray(pieces, dtype=PIECE_DTYPE)
+    bad, first = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    rc = load().emrs_synth_verify(pcs.ctypes.data if len(pcs) else None, len(pcs), _ptr_array(ptrs),
+                                  _u64_array(buf_bytes), len(ptrs), int(seed), ctypes.c_void_p(int(stream)),
+                                  ctypes.byref(bad), ctypes.byref(first))
+    _check(rc, "emrs_synth_verify")
+    f = first.value
+    return int(bad.value), (None if f == 2 ** 64 - 1 else (f >> 40, f & ((1 << 40) - 1)))

@@ -1,0 +1,609 @@
+// Copy-plan executor for the reshard repack on MI355X (gfx950, CDNA4).
+//
+// One launch moves every segment of a plan.  The path is pure data movement
+// (no arithmetic), so the kernel is shaped for HBM streaming: 16-byte vector
+// loads and stores, eight of them in flight per lane before the first store,
+// a persistent grid whose workgroups each own a contiguous run of fixed-size
+// chunks, and a one-time binary search per workgroup for its first segment
+// followed by a forward walk.  Element sizes are irrelevant to the vector
+// path: offsets are converted to 16-byte units when the plan is created, so
+// bf16 parameters and fp32 optimizer state share one launch.
+//
+// The reference performs the same movement as per-parameter slicing plus
+// point-to-point messages (elastic_megatron/transfer/transfer.py:36-101,
+// :143-269; elastic_megatron/transfer/communicator.py:61-96).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "emrs.h"
+#include "internal.h"
+
+namespace {
+thread_local std::string g_last_error;
+}  // namespace
+
+namespace emrs_internal {
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+void clear_error() { g_last_error.clear(); }
+}  // namespace emrs_internal
+
+namespace {
+
+using emrs_internal::fail;
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(EMRS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+constexpr uint32_t kChunkUnits = kThreads * kUnroll;  // units per work chunk
+constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 bits
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct Bases {
+  char *p[EMRS_MAX_BUFFERS];
+};
+
+// Segment as the kernel sees it.  Offsets and strides are in units of
+// (1 << unit_log2) bytes: 16 for the vector path, the element size otherwise.
+struct DevSeg {
+  uint64_t src_off;
+  uint64_t dst_off;
+  uint64_t chunk_begin;  // index of this segment's first chunk
+  uint32_t len;          // units per row
+  uint32_t rows;
+  uint32_t src_stride;
+  uint32_t dst_stride;
+  uint32_t magic;        // row = (t + ((u - t) >> sh1)) >> sh2, t = umulhi(magic, u)
+  uint8_t sh1;
+  uint8_t sh2;
+  uint8_t unit_log2;
+  uint8_t pad0;
+  uint8_t src_buf;
+  uint8_t dst_buf;
+  uint8_t pad1[6];
+};
+static_assert(sizeof(DevSeg) == 56, "DevSeg layout");
+
+// Division by an invariant divisor (Granlund & Montgomery 1994, fig. 4.1).
+void make_magic(uint32_t d, uint32_t *m, uint8_t *sh1, uint8_t *sh2) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  uint64_t num = (uint64_t)(((unsigned __int128)1 << 32) * (((unsigned __int128)1 << l) - d) / d) + 1;
+  *m = (uint32_t)num;
+  *sh1 = l < 1 ? (uint8_t)l : 1;
+  *sh2 = l > 1 ? (uint8_t)(l - 1) : 0;
+}
+
+__host__ __device__ __forceinline__ uint32_t umulhi32(uint32_t a, uint32_t b) {
+  return (uint32_t)(((uint64_t)a * b) >> 32);
+}
+
+__host__ __device__ __forceinline__ uint32_t magic_div(uint32_t n, uint32_t m, uint32_t sh1,
+                                                       uint32_t sh2) {
+  uint32_t t = umulhi32(m, n);
+  return (t + ((n - t) >> sh1)) >> sh2;
+}
+
+struct Tuning {
+  std::atomic<uint32_t> blocks_per_cu{0};  // 0: as many as can be resident
+  std::atomic<uint32_t> nontemporal{1};
+  std::atomic<uint32_t> xcd_remap{0};
+};
+Tuning g_tuning;
+
+// ---------------------------------------------------------------------------
+// Copy kernel
+// ---------------------------------------------------------------------------
+
+template <typename T, bool kNT>
+__device__ __forceinline__ T ld(const T *p) {
+  if constexpr (kNT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <typename T, bool kNT>
+__device__ __forceinline__ void st(T *p, T v) {
+  if constexpr (kNT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Copy units [u0, u_end) of segment s, 0 < u_end - u0 <= kChunkUnits.  In a
+// partial chunk, lanes past the end load the last unit again (in bounds) so
+// that every load is unconditional; only their stores are masked off.
+template <typename T, bool kNT>
+__device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, char *dbase,
+                                           uint32_t u0, uint32_t u_end) {
+  const T *src = reinterpret_cast<const T *>(sbase);
+  T *dst = reinterpret_cast<T *>(dbase);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n = u_end - u0;
+  T v[kUnroll];
+  if (s.rows == 1) {
+    const T *sp = src + s.src_off + u0;
+    T *dp = dst + s.dst_off + u0;
+    if (n == kChunkUnits) {
+#pragma unroll
+      for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + j * kThreads + tid);
+#pragma unroll
+      for (int j = 0; j < kUnroll; ++j) st<T, kNT>(dp + j * kThreads + tid, v[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + min(j * kThreads + tid, n - 1));
+#pragma unroll
+      for (int j = 0; j < kUnroll; ++j)
+        if (j * kThreads + tid < n) st<T, kNT>(dp + j * kThreads + tid, v[j]);
+    }
+    return;
+  }
+  uint64_t dof[kUnroll];
+#pragma unroll
+  for (int j = 0; j < kUnroll; ++j) {
+    const uint32_t u = u0 + min(j * kThreads + tid, n - 1);
+    const uint32_t row = magic_div(u, s.magic, s.sh1, s.sh2);
+    const uint32_t col = u - row * s.len;
+    v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row * s.src_stride + col);
+    dof[j] = s.dst_off + (uint64_t)row * s.dst_stride + col;
+  }
+#pragma unroll
+  for (int j = 0; j < kUnroll; ++j)
+    if (j * kThreads + tid < n) st<T, kNT>(dst + dof[j], v[j]);
+}
+
+template <bool kNT>
+__global__ __launch_bounds__(kThreads) void copy_plan_kernel(
+    const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
+    uint64_t chunks_per_block, uint32_t xcd_stride, Bases src, Bases dst) {
+  uint64_t b = blockIdx.x;
+  if (xcd_stride) b = (b & 7) * xcd_stride + (b >> 3);  // one contiguous slice per XCD
+  uint64_t c = b * chunks_per_block;
+  if (c >= n_chunks) return;
+  const uint64_t c_end = min(c + chunks_per_block, n_chunks);
+
+  // Last segment whose first chunk is <= c.
+  uint32_t lo = 0, hi = n_segs - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (segs[mid].chunk_begin <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  uint32_t si = lo;
+  DevSeg s = segs[si];
+  uint64_t s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+
+  for (; c < c_end; ++c) {
+    while (c >= s_end) {
+      ++si;
+      s = segs[si];
+      s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+    }
+    const uint32_t total = s.len * s.rows;
+    const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
+    const uint32_t u_end = min(u0 + kChunkUnits, total);
+    const char *sb = src.p[s.src_buf];
+    char *db = dst.p[s.dst_buf];
+    switch (s.unit_log2) {
+      case 4: copy_chunk<u32x4, kNT>(s, sb, db, u0, u_end); break;
+      case 3: copy_chunk<uint64_t, kNT>(s, sb, db, u0, u_end); break;
+      case 2: copy_chunk<uint32_t, kNT>(s, sb, db, u0, u_end); break;
+      case 1: copy_chunk<uint16_t, kNT>(s, sb, db, u0, u_end); break;
+      default: copy_chunk<uint8_t, kNT>(s, sb, db, u0, u_end); break;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Device bookkeeping
+// ---------------------------------------------------------------------------
+
+struct DeviceProps {
+  int cus = 0;
+  int resident_blocks[2] = {0, 0};  // copy_plan_kernel<false/true> blocks per CU
+};
+
+std::mutex g_dev_mu;
+std::vector<DeviceProps> g_dev_props;
+
+template <bool kNT>
+void copy_plan_kernel_occupancy(int *out) {
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, copy_plan_kernel<kNT>, kThreads, 0) != hipSuccess || v <= 0) {
+    (void)hipGetLastError();
+    v = 4;
+  }
+  *out = v;
+}
+
+int current_device(int *dev, int *cus, int *resident_nt, int *resident_t) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    return fail(EMRS_ERR_NO_DEVICE, "no HIP device is visible");
+  }
+  e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if ((int)g_dev_props.size() < n) g_dev_props.resize(n);
+  if (g_dev_props[*dev].cus == 0) {
+    int v = 0;
+    e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, *dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    g_dev_props[*dev].cus = v > 0 ? v : 1;
+    copy_plan_kernel_occupancy<false>(&g_dev_props[*dev].resident_blocks[0]);
+    copy_plan_kernel_occupancy<true>(&g_dev_props[*dev].resident_blocks[1]);
+  }
+  *cus = g_dev_props[*dev].cus;
+  *resident_t = g_dev_props[*dev].resident_blocks[0];
+  *resident_nt = g_dev_props[*dev].resident_blocks[1];
+  return EMRS_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Plan
+// ---------------------------------------------------------------------------
+
+struct emrs_plan {
+  std::vector<DevSeg> segs;
+  uint64_t n_chunks = 0;
+  std::vector<uint64_t> src_bytes, dst_bytes;
+  emrs_plan_stats stats{};
+  std::mutex mu;
+  std::vector<DevSeg *> dev_tables;  // per device, uploaded on first use
+};
+
+namespace {
+
+struct Builder {
+  std::vector<DevSeg> out;
+  uint64_t chunks = 0;
+  uint64_t vec_bytes = 0, scalar_bytes = 0;
+
+  // Emit a segment in units of (1 << ul) bytes; splits to the 32-bit limits.
+  int emit(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint64_t len,
+           uint64_t rows, uint64_t ss, uint64_t ds) {
+    if (len == 0 || rows == 0) return EMRS_OK;
+    if (rows > 1 && ss == len && ds == len) {  // contiguous on both sides
+      len *= rows;
+      rows = 1;
+    }
+    const uint64_t bytes = (len * rows) << ul;
+    (ul == 4 ? vec_bytes : scalar_bytes) += bytes;
+    if (rows == 1) {
+      for (uint64_t off = 0; off < len; off += kMaxUnitsPerSeg) {
+        const uint64_t n = std::min<uint64_t>(kMaxUnitsPerSeg, len - off);
+        push(sbuf, dbuf, ul, so + off, dof + off, (uint32_t)n, 1, 0, 0);
+      }
+      return EMRS_OK;
+    }
+    if (len >= kMaxUnitsPerSeg || ss > 0xffffffffull || ds > 0xffffffffull) {
+      for (uint64_t r = 0; r < rows; ++r) {
+        for (uint64_t off = 0; off < len; off += kMaxUnitsPerSeg) {
+          const uint64_t n = std::min<uint64_t>(kMaxUnitsPerSeg, len - off);
+          push(sbuf, dbuf, ul, so + r * ss + off, dof + r * ds + off, (uint32_t)n, 1, 0, 0);
+        }
+      }
+      return EMRS_OK;
+    }
+    const uint64_t rows_per = std::max<uint64_t>(1, kMaxUnitsPerSeg / len);
+    for (uint64_t r = 0; r < rows; r += rows_per) {
+      const uint64_t n = std::min<uint64_t>(rows_per, rows - r);
+      push(sbuf, dbuf, ul, so + r * ss, dof + r * ds, (uint32_t)len, (uint32_t)n, (uint32_t)ss,
+           (uint32_t)ds);
+    }
+    return EMRS_OK;
+  }
+
+  void push(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint32_t len,
+            uint32_t rows, uint32_t ss, uint32_t ds) {
+    DevSeg d{};
+    d.src_off = so;
+    d.dst_off = dof;
+    d.chunk_begin = chunks;
+    d.len = len;
+    d.rows = rows;
+    d.src_stride = rows > 1 ? ss : 0;
+    d.dst_stride = rows > 1 ? ds : 0;
+    make_magic(len, &d.magic, &d.sh1, &d.sh2);
+    d.unit_log2 = (uint8_t)ul;
+    d.src_buf = (uint8_t)sbuf;
+    d.dst_buf = (uint8_t)dbuf;
+    const uint64_t units = (uint64_t)len * rows;
+    chunks += (units + kChunkUnits - 1) / kChunkUnits;
+    out.push_back(d);
+  }
+};
+
+int log2_of(uint32_t eb) {
+  switch (eb) {
+    case 1: return 0;
+    case 2: return 1;
+    case 4: return 2;
+    case 8: return 3;
+    default: return -1;
+  }
+}
+
+// Byte extent end of a strided segment; false on overflow.
+bool extent_end(uint64_t off, uint64_t len, uint64_t rows, uint64_t stride, uint32_t eb,
+                unsigned __int128 *end) {
+  unsigned __int128 e = (unsigned __int128)off + (unsigned __int128)(rows - 1) * stride + len;
+  e *= eb;
+  *end = e;
+  return true;
+}
+
+int check_disjoint(const std::vector<emrs_segment> &segs, uint32_t n_dst) {
+  struct Iv {
+    uint32_t buf;
+    uint64_t b, e;
+  };
+  std::vector<Iv> iv;
+  uint64_t total_rows = 0;
+  for (const auto &s : segs) total_rows += s.len ? s.rows : 0;
+  if (total_rows > (1ull << 27))
+    return fail(EMRS_ERR_INVALID_ARGUMENT, "disjointness check: too many rows to check");
+  iv.reserve(total_rows);
+  for (const auto &s : segs) {
+    if (!s.len) continue;
+    for (uint64_t r = 0; r < s.rows; ++r) {
+      const uint64_t b = (s.dst_off + r * s.dst_stride) * s.elem_bytes;
+      iv.push_back({s.dst_buf, b, b + s.len * s.elem_bytes});
+    }
+  }
+  std::sort(iv.begin(), iv.end(), [](const Iv &a, const Iv &b) {
+    return a.buf != b.buf ? a.buf < b.buf : a.b < b.b;
+  });
+  for (size_t i = 1; i < iv.size(); ++i) {
+    if (iv[i].buf == iv[i - 1].buf && iv[i].b < iv[i - 1].e) {
+      char msg[160];
+      snprintf(msg, sizeof msg, "destination ranges overlap in buffer %u at byte %llu", iv[i].buf,
+               (unsigned long long)iv[i].b);
+      return fail(EMRS_ERR_OVERLAP, msg);
+    }
+  }
+  (void)n_dst;
+  return EMRS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *emrs_last_error(void) { return g_last_error.c_str(); }
+
+int emrs_abi_version(void) { return EMRS_ABI_VERSION; }
+
+int emrs_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *src_buf_bytes,
+                     uint32_t n_src_bufs, const uint64_t *dst_buf_bytes, uint32_t n_dst_bufs,
+                     uint32_t flags, emrs_plan **out_plan) {
+  g_last_error.clear();
+  if (!out_plan) return fail(EMRS_ERR_INVALID_ARGUMENT, "out_plan is NULL");
+  *out_plan = nullptr;
+  if (n_segs && !segs) return fail(EMRS_ERR_INVALID_ARGUMENT, "segs is NULL");
+  if (n_src_bufs > EMRS_MAX_BUFFERS || n_dst_bufs > EMRS_MAX_BUFFERS)
+    return fail(EMRS_ERR_TOO_MANY_BUFFERS, "more than EMRS_MAX_BUFFERS buffers on one side");
+  if ((n_src_bufs && !src_buf_bytes) || (n_dst_bufs && !dst_buf_bytes))
+    return fail(EMRS_ERR_INVALID_ARGUMENT, "buffer size array is NULL");
+  if (flags & ~EMRS_PLAN_CHECK_DISJOINT) return fail(EMRS_ERR_INVALID_ARGUMENT, "unknown flags");
+
+  Builder bld;
+  bld.out.reserve(n_segs);
+  uint64_t payload = 0;
+  for (uint64_t i = 0; i < n_segs; ++i) {
+    const emrs_segment &s = segs[i];
+    char where[64];
+    snprintf(where, sizeof where, "segment %llu: ", (unsigned long long)i);
+    const int lg = log2_of(s.elem_bytes);
+    if (lg < 0) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "elem_bytes must be 1, 2, 4 or 8");
+    if (s.flags) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "flags must be 0");
+    if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs)
+      return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "buffer id out of range");
+    if (s.rows == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "rows must be >= 1");
+    if (s.len == 0) continue;
+    if (s.rows > 1 && s.dst_stride < s.len)
+      return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "dst_stride < len makes rows overlap");
+    unsigned __int128 se, de;
+    extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes, &se);
+    extent_end(s.dst_off, s.len, s.rows, s.rows > 1 ? s.dst_stride : 0, s.elem_bytes, &de);
+    if (se > src_buf_bytes[s.src_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, std::string(where) + "source range exceeds its buffer");
+    if (de > dst_buf_bytes[s.dst_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, std::string(where) + "destination range exceeds its buffer");
+    payload += s.len * s.rows * s.elem_bytes;
+
+    const uint64_t eb = s.elem_bytes;
+    const uint64_t so = s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
+    const uint64_t ss = s.rows > 1 ? s.src_stride * eb : 0, ds = s.rows > 1 ? s.dst_stride * eb : 0;
+    const bool rows1 = s.rows == 1 || (ss == lb && ds == lb);
+    if (rows1) {
+      const uint64_t L = lb * s.rows;  // contiguous bytes
+      if (so % 16 == 0 && dof % 16 == 0 && L % 16 == 0) {
+        bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, L / 16, 1, 0, 0);
+      } else if (so % 16 == dof % 16) {
+        const uint64_t head = std::min<uint64_t>((16 - so % 16) % 16, L);
+        const uint64_t body = (L - head) / 16 * 16;
+        const uint64_t tail = L - head - body;
+        bld.emit(s.src_buf, s.dst_buf, lg, so / eb, dof / eb, head / eb, 1, 0, 0);
+        bld.emit(s.src_buf, s.dst_buf, 4, (so + head) / 16, (dof + head) / 16, body / 16, 1, 0, 0);
+        bld.emit(s.src_buf, s.dst_buf, lg, (so + head + body) / eb, (dof + head + body) / eb,
+                 tail / eb, 1, 0, 0);
+      } else {
+        bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, L / eb, 1, 0, 0);
+      }
+    } else if (so % 16 == 0 && dof % 16 == 0 && lb % 16 == 0 && ss % 16 == 0 && ds % 16 == 0) {
+      bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, lb / 16, s.rows, ss / 16, ds / 16);
+    } else {
+      bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, s.len, s.rows, s.src_stride,
+               s.dst_stride);
+    }
+  }
+  if (flags & EMRS_PLAN_CHECK_DISJOINT) {
+    std::vector<emrs_segment> v(segs, segs + n_segs);
+    int rc = check_disjoint(v, n_dst_bufs);
+    if (rc) return rc;
+  }
+
+  emrs_plan *p = new (std::nothrow) emrs_plan;
+  if (!p) return fail(EMRS_ERR_INVALID_ARGUMENT, "out of host memory");
+  p->segs = std::move(bld.out);
+  p->n_chunks = bld.chunks;
+  p->src_bytes.assign(src_buf_bytes, src_buf_bytes + n_src_bufs);
+  p->dst_bytes.assign(dst_buf_bytes, dst_buf_bytes + n_dst_bufs);
+  p->stats.n_segments = n_segs;
+  p->stats.n_device_segments = p->segs.size();
+  p->stats.payload_bytes = payload;
+  p->stats.vector_bytes = bld.vec_bytes;
+  p->stats.scalar_bytes = bld.scalar_bytes;
+  p->stats.n_chunks = bld.chunks;
+  p->stats.n_src_bufs = n_src_bufs;
+  p->stats.n_dst_bufs = n_dst_bufs;
+  *out_plan = p;
+  return EMRS_OK;
+}
+
+int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out) {
+  if (!plan || !out) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = plan->stats;
+  return EMRS_OK;
+}
+
+int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
+                      void *stream) {
+  g_last_error.clear();
+  if (!plan) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
+  if ((ns && !src_bases) || (nd && !dst_bases))
+    return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
+  Bases sb{}, db{};
+  for (uint32_t i = 0; i < ns; ++i) {
+    sb.p[i] = static_cast<char *>(src_bases[i]);
+    if (!sb.p[i] && plan->src_bytes[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
+    if (reinterpret_cast<uintptr_t>(sb.p[i]) % 16)
+      return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
+  }
+  for (uint32_t i = 0; i < nd; ++i) {
+    db.p[i] = static_cast<char *>(dst_bases[i]);
+    if (!db.p[i] && plan->dst_bytes[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
+    if (reinterpret_cast<uintptr_t>(db.p[i]) % 16)
+      return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
+  }
+  for (uint32_t i = 0; i < ns; ++i) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(sb.p[i]), a1 = a0 + plan->src_bytes[i];
+    for (uint32_t j = 0; j < nd; ++j) {
+      const uintptr_t b0 = reinterpret_cast<uintptr_t>(db.p[j]), b1 = b0 + plan->dst_bytes[j];
+      if (a0 < b1 && b0 < a1 && a1 > a0 && b1 > b0)
+        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
+    }
+  }
+  for (uint32_t j = 0; j < nd; ++j) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(db.p[j]), a1 = a0 + plan->dst_bytes[j];
+    for (uint32_t k = j + 1; k < nd; ++k) {
+      const uintptr_t b0 = reinterpret_cast<uintptr_t>(db.p[k]), b1 = b0 + plan->dst_bytes[k];
+      if (a0 < b1 && b0 < a1 && a1 > a0 && b1 > b0)
+        return fail(EMRS_ERR_ALIAS, "two destination buffers overlap");
+    }
+  }
+  if (plan->n_chunks == 0) return EMRS_OK;
+
+  int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
+  int rc = current_device(&dev, &cus, &resident_nt, &resident_t);
+  if (rc) return rc;
+  DevSeg *table = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(plan->mu);
+    if ((int)plan->dev_tables.size() <= dev) plan->dev_tables.resize(dev + 1, nullptr);
+    if (!plan->dev_tables[dev]) {
+      const size_t bytes = plan->segs.size() * sizeof(DevSeg);
+      hipError_t e = hipMalloc(&plan->dev_tables[dev], bytes);
+      if (e != hipSuccess) {
+        plan->dev_tables[dev] = nullptr;
+        return hip_fail(e, "hipMalloc(plan table)");
+      }
+      e = hipMemcpy(plan->dev_tables[dev], plan->segs.data(), bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy(plan table)");
+    }
+    table = plan->dev_tables[dev];
+  }
+
+  const bool nt = g_tuning.nontemporal.load() != 0;
+  const uint32_t bpc = g_tuning.blocks_per_cu.load();
+  const uint64_t max_blocks = (uint64_t)cus * (bpc ? bpc : (uint32_t)(nt ? resident_nt : resident_t));
+  uint64_t blocks = std::min<uint64_t>(plan->n_chunks, max_blocks);
+  const bool remap = g_tuning.xcd_remap.load() != 0;
+  if (remap) blocks = (blocks + 7) / 8 * 8;
+  const uint64_t cpb = (plan->n_chunks + blocks - 1) / blocks;
+  if (!remap) blocks = (plan->n_chunks + cpb - 1) / cpb;
+  const uint32_t xcd_stride = remap ? (uint32_t)(blocks / 8) : 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (nt)
+    hipLaunchKernelGGL(copy_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
+                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, sb, db);
+  else
+    hipLaunchKernelGGL(copy_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
+                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, sb, db);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "copy_plan_kernel launch");
+  return EMRS_OK;
+}
+
+int emrs_plan_destroy(emrs_plan *plan) {
+  if (!plan) return EMRS_OK;
+  for (size_t d = 0; d < plan->dev_tables.size(); ++d) {
+    if (plan->dev_tables[d]) {
+      int prev = 0;
+      (void)hipGetDevice(&prev);
+      (void)hipSetDevice((int)d);
+      (void)hipFree(plan->dev_tables[d]);
+      (void)hipSetDevice(prev);
+    }
+  }
+  delete plan;
+  return EMRS_OK;
+}
+
+int emrs_get_tuning(emrs_tuning *out) {
+  if (!out) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  out->blocks_per_cu = g_tuning.blocks_per_cu.load();
+  out->nontemporal = g_tuning.nontemporal.load();
+  out->xcd_remap = g_tuning.xcd_remap.load();
+  out->reserved = 0;
+  return EMRS_OK;
+}
+
+int emrs_set_tuning(const emrs_tuning *t) {
+  if (!t) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (t->blocks_per_cu > 64) return fail(EMRS_ERR_INVALID_ARGUMENT, "blocks_per_cu must be in [0, 64]");
+  g_tuning.blocks_per_cu.store(t->blocks_per_cu);
+  g_tuning.nontemporal.store(t->nontemporal ? 1 : 0);
+  g_tuning.xcd_remap.store(t->xcd_remap ? 1 : 0);
+  return EMRS_OK;
+}
+
+}  // extern "C"

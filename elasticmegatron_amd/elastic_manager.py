@@ -1,0 +1,131 @@
+"""Public façade: ``ElasticMegatronManager.reshard(new_parallel_strategy=...)``.
+
+Mirrors elastic_megatron/elastic_manager.py:30-265.  The reference's manager
+wraps a live Megatron model, optimizer and process groups; this one wraps a
+:class:`~.megatron_manager.training_state.TrainingState` holding every rank's
+state on one device.  ``reshard`` keeps the reference's control flow:
+
+1. pick the destination strategy (elastic_manager.py:189-258);
+2. Group-ZeRO instance switches take the redundant-backup path, everything
+   else plans and transfers (elastic_manager.py:106-141,
+   parallel_strategy.py:234-263);
+3. the transfer is timed with a device-synchronised timer around the executor
+   only (elastic_manager.py:119-120);
+4. the source optimizer state is released and the perf line is logged in the
+   reference's format (elastic_manager.py:158-178).
+
+Process-group rebuild, learning-rate broadcast and dataloader rebuild have no
+counterpart on one device and are not performed.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Dict, List, Optional, Union
+
+import torch
+
+from .megatron_manager.parallel_strategy import ParallelStrategy
+from .megatron_manager.training_state import TrainingState
+from .resharding.model_spec import ModelSpec
+from .resharding.util import Timer
+from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
+from .transfer.transfer import TransferManager
+
+StrategyLike = Union[ParallelStrategy, Dict[str, int]]
+
+
+def _as_strategy(s: StrategyLike) -> ParallelStrategy:
+    return s if isinstance(s, ParallelStrategy) else ParallelStrategy(**s)
+
+
+class ElasticMegatronManager:
+    def __init__(self, parallel_strategy_list: List[StrategyLike], model_spec: ModelSpec,
+                 training_state: Optional[TrainingState] = None, device=None,
+                 release_source: bool = True):
+        if not parallel_strategy_list:
+            raise ValueError("parallel_strategy_list is empty")
+        self.parallel_strategy_list = [_as_strategy(s) for s in parallel_strategy_list]
+        self.model_spec = model_spec
+        self.virtual_param_space: VirtualParamSpace = build_virtual_model(model_spec)
+        for s in self.parallel_strategy_list:
+            self.virtual_param_space.build_model_virtual_params(s)
+        self.transfer_manager = TransferManager()
+        self.release_source = release_source
+        self.last_transfer_ms = 0.0
+        cur = self.parallel_strategy_list[0]
+        if training_state is None:
+            training_state = TrainingState.allocate(self.virtual_param_space.layout(cur), device)
+        elif training_state.parallel_strategy != cur:
+            raise ValueError("training_state does not use the first strategy of the list")
+        self.training_state = training_state
+
+    @property
+    def parallel_strategy(self) -> ParallelStrategy:
+        return self.training_state.parallel_strategy
+
+    def transfer_params(self, src: TrainingState, dst: TrainingState) -> float:
+        """Plan (cached) and move the state; returns the executor's time in ms."""
+        self.virtual_param_space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
+        self.virtual_param_space.src_state, self.virtual_param_space.dst_state = src, dst
+        plan = self.transfer_manager.compile(src.layout, dst.layout)
+        with Timer() as t:
+            self.transfer_manager.execute(plan, src, dst)
+        return t.elapsed
+
+    def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool) -> float:
+        plan = self.transfer_manager.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
+        with Timer() as t:
+            self.transfer_manager.execute(plan, src, dst)
+        return t.elapsed
+
+    def log_communication_info(self, transfer_time: float, logger: Optional[logging.Logger] = None) -> str:
+        gib = self.transfer_manager.get_communication_bytes()
+        bw = 1000 * gib / transfer_time if transfer_time > 0 else float("inf")
+        msg = (f"[ElasticMegatron-Perf] : transfer time: {transfer_time:.2f} ms, "
+               f"communication bytes: {gib:.2f} GB, bandwidth: {bw:.2f} GB/s")
+        if logger is not None:
+            logger.info(msg)
+        return msg
+
+    def reshard(self, new_parallel_strategy: StrategyLike, logger: Optional[logging.Logger] = None,
+                is_meta_device: bool = False, save_ckpt: bool = False) -> Optional[TrainingState]:
+        """Switch every rank's state to ``new_parallel_strategy``; returns the new state.
+
+        ``is_meta_device=True`` builds and caches the plan without touching
+        device memory and returns None (the reference's meta-device
+        pre-build, elastic_manager.py:268-304).
+        """
+        if is_meta_device and save_ckpt:
+            raise AssertionError("Can't save checkpoint in meta device")
+        if save_ckpt:
+            raise NotImplementedError("checkpoint saving is not part of the reshard data path")
+        dst_strategy = _as_strategy(new_parallel_strategy)
+        src_state = self.training_state
+        src_strategy = src_state.parallel_strategy
+        space = self.virtual_param_space
+        backup = ParallelStrategy.is_redundant_backup(src_strategy, dst_strategy)
+        dst_layout = space.layout(dst_strategy)
+        if backup is None:
+            space.register_reshard(src_strategy, dst_strategy)
+            plan = self.transfer_manager.compile(src_state.layout, dst_layout)
+        else:
+            plan = self.transfer_manager.compile(src_state.layout, dst_layout,
+                                                 "backup_up" if backup else "backup_down")
+        if is_meta_device:
+            return None
+        if backup is None:
+            dst_state = TrainingState.allocate(dst_layout, src_state.device)
+            elapsed = self.transfer_params(src_state, dst_state)
+        else:
+            # Model-parallel shards are unchanged, so the bf16 params carry over as they are.
+            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=src_state.param)
+            elapsed = self.redundant_backup(src_state, dst_state, backup)
+        self.last_transfer_ms = elapsed
+        if self.release_source:
+            src_state.release_optimizer()
+        self.training_state = dst_state
+        msg = self.log_communication_info(elapsed, logger)
+        if logger is None and torch.distributed.is_available() and not torch.distributed.is_initialized():
+            print(msg)
+        return dst_state

@@ -1,0 +1,118 @@
+"""Device-resident training state of every rank of one parallel strategy.
+
+Stands in for the reference's ``TrainingState`` and ``OptimizerTensorInfo``
+(elastic_megatron/megatron_manager/training_state.py:35-366,
+elastic_megatron/resharding/resharding_metadata.py:19-96): instead of one
+Megatron model and optimizer per process, it owns the four arenas of a
+:class:`~elasticmegatron_amd.resharding.layout.StrategyLayout` on one device
+(fp32 main / exp_avg / exp_avg_sq of every rank, bf16 params of every
+model-parallel shard) and hands out per-(rank, parameter) views with the
+reference's names.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+
+from .. import _native
+from ..resharding.layout import ARENA_NAMES, StrategyLayout
+from ..resharding.util import Range
+
+
+@dataclass
+class OptimizerTensorInfo:
+    """Views of one rank's piece of one parameter (resharding_metadata.py:19-40)."""
+
+    main_weight: torch.Tensor
+    exp_avg: torch.Tensor
+    exp_avg_sq: torch.Tensor
+    optimizer_tensor_range_in_model_param: Range   # param-local flat range this rank owns
+    model_param_shape: Tuple[int, ...]             # TP-local shape
+
+    @property
+    def optimizer_tensors(self) -> List[torch.Tensor]:
+        return [self.main_weight, self.exp_avg, self.exp_avg_sq]
+
+
+class TrainingState:
+    def __init__(self, layout: StrategyLayout, main: torch.Tensor, exp_avg: torch.Tensor,
+                 exp_avg_sq: torch.Tensor, param: torch.Tensor):
+        self.layout = layout
+        self.main = main
+        self.exp_avg = exp_avg
+        self.exp_avg_sq = exp_avg_sq
+        self.param = param
+
+    @property
+    def parallel_strategy(self):
+        return self.layout.strategy
+
+    @classmethod
+    def allocate(cls, layout: StrategyLayout, device=None, param: Optional[torch.Tensor] = None) -> "TrainingState":
+        """Uninitialised arenas for ``layout``; ``param`` may alias an existing bf16 arena."""
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        f32 = [torch.empty(layout.fp32_numel, dtype=torch.float32, device=dev) for _ in range(3)]
+        if param is None:
+            param = torch.empty(layout.bf16_numel, dtype=torch.bfloat16, device=dev)
+        elif param.numel() != layout.bf16_numel or param.dtype != torch.bfloat16:
+            raise ValueError("aliased param arena does not match the layout")
+        return cls(layout, f32[0], f32[1], f32[2], param)
+
+    # ----- arenas -----
+    def arenas(self) -> List[torch.Tensor]:
+        return [self.main, self.exp_avg, self.exp_avg_sq, self.param]
+
+    def arena_ptrs(self) -> List[int]:
+        return [t.data_ptr() for t in self.arenas()]
+
+    def arena_bytes(self) -> List[int]:
+        return [t.numel() * t.element_size() for t in self.arenas()]
+
+    @property
+    def device(self) -> torch.device:
+        return self.main.device
+
+    def release_optimizer(self) -> None:
+        """Drop the fp32 arenas (training_state.py:313-315)."""
+        empty = torch.empty(0, dtype=torch.float32, device=self.device)
+        self.main = self.exp_avg = self.exp_avg_sq = empty
+
+    # ----- per-(rank, parameter) views -----
+    def optimizer_tensor_info(self, vp, rank: int) -> Optional[OptimizerTensorInfo]:
+        for h in self.layout.fp32_holders(vp):
+            if h.rank == rank:
+                sl = slice(h.offset, h.offset + h.hi - h.lo)
+                return OptimizerTensorInfo(self.main[sl], self.exp_avg[sl], self.exp_avg_sq[sl],
+                                           Range(h.lo, h.hi), vp.local_shape(self.layout.strategy))
+        return None
+
+    def model_param(self, vp, tp_rank: int = 0) -> Optional[torch.Tensor]:
+        """bf16 TP-local tensor of ``vp`` held by TP rank ``tp_rank`` of its stage."""
+        for h in self.layout.bf16_holders(vp):
+            if h.tp_rank == tp_rank:
+                return self.param[h.offset:h.offset + h.hi - h.lo].view(vp.local_shape(self.layout.strategy))
+        return None
+
+    # ----- synthetic workload -----
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def fill_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True) -> None:
+        """Write the seeded synthetic values of every stored element (see csrc/synth.hip)."""
+        pcs = self.layout.pieces(params, include_bf16=bf16, include_fp32=fp32)
+        with torch.cuda.device(self.device):
+            _native.synth_fill(pcs, self.arena_ptrs(), self.arena_bytes(), seed, self._stream())
+
+    def verify_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True):
+        """(mismatching elements, first bad element) against the seeded synthetic values."""
+        pcs = self.layout.pieces(params, include_bf16=bf16, include_fp32=fp32)
+        with torch.cuda.device(self.device):
+            bad, first = _native.synth_verify(pcs, self.arena_ptrs(), self.arena_bytes(), seed, self._stream())
+        if first is not None:
+            p = pcs[first[0]]
+            first = dict(arena=ARENA_NAMES[int(p["buf"])], param_id=int(p["param_id"]), kind=int(p["kind"]),
+                         element=int(first[1]), piece_offset=int(p["buf_off"]))
+        return bad, first

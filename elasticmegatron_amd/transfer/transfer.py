@@ -1,0 +1,110 @@
+"""Executor of a reshard: one native copy-plan launch.
+
+Replaces ``TransferManager`` of the reference
+(elastic_megatron/transfer/transfer.py:23-388).  The reference runs three
+Python passes over all parameters with blocking point-to-point messages
+(DP gather + SwiGLU shuffle, TP/PP/EP exchange, SwiGLU unshuffle + DP
+scatter) and relies on a FIFO for rank-local self copies
+(transfer.py:143-269, communicator.py:38-96).  Here the whole switch is
+lowered once to a segment table (cached per strategy pair, like the
+reference's per-parameter plan cache, virtual_param.py:174-188) and executed
+as one launch on the caller's stream.  Rank-local copies and cross-rank
+messages are the same operation on one device.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+from .. import _native
+from ..megatron_manager.parallel_strategy import ParallelStrategy
+from ..megatron_manager.training_state import TrainingState
+from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes
+from ..resharding.layout import StrategyLayout
+
+
+@dataclass
+class CompiledPlan:
+    segments: np.ndarray
+    native: _native.Plan
+    payload_bytes: int
+    src: ParallelStrategy
+    dst: ParallelStrategy
+
+
+class TransferManager:
+    """Builds, caches and runs copy plans between device-resident training states."""
+
+    def __init__(self, check_disjoint: bool = False):
+        self._plans: Dict[Tuple, CompiledPlan] = {}
+        self.check_disjoint = check_disjoint
+        self.fake_transfer = False
+        self._payload_bytes = 0
+
+    def set_fake_transfer(self, fake: bool) -> None:
+        """Plan without moving data (transfer.py:32-34)."""
+        self.fake_transfer = fake
+
+    def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
+                include_bf16: bool = True) -> CompiledPlan:
+        key = (src.strategy, dst.strategy, kind, include_bf16)
+        cp = self._plans.get(key)
+        if cp is not None:
+            return cp
+        if kind == "transfer":
+            table = lower_transfer(src, dst, include_bf16=include_bf16)
+        elif kind in ("backup_up", "backup_down"):
+            table = lower_redundant_backup(src, dst, scale_up=kind == "backup_up")
+        else:
+            raise ValueError(kind)
+        sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
+        db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
+        cp = CompiledPlan(table, _native.Plan(table, sb, db, self.check_disjoint), payload_bytes(table),
+                          src.strategy, dst.strategy)
+        self._plans[key] = cp
+        return cp
+
+    def execute(self, plan: CompiledPlan, src: TrainingState, dst: TrainingState,
+                stream: Optional[torch.cuda.Stream] = None) -> None:
+        if self.fake_transfer:
+            return
+        if src.layout.strategy != plan.src or dst.layout.strategy != plan.dst:
+            raise ValueError("training states do not match the plan's strategies")
+        if src.device != dst.device:
+            raise ValueError("source and destination states must be on the same device")
+        st = stream if stream is not None else torch.cuda.current_stream(src.device)
+        with torch.cuda.device(src.device):
+            plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)
+        self._payload_bytes += plan.payload_bytes
+
+    def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
+                                   dst: Optional[TrainingState] = None, include_bf16: bool = True,
+                                   stream=None) -> CompiledPlan:
+        """Move fp32 optimizer state and bf16 params from ``src`` to ``dst`` (transfer.py:291-341).
+
+        The bf16 params are copied directly: with main = upcast(param) the
+        reference's cast of the new main shards back to bf16 plus DP
+        all-gather (training_state.py:176-197) yields the same bits.
+        """
+        src = src if src is not None else virtual_param_space.src_state
+        dst = dst if dst is not None else virtual_param_space.dst_state
+        plan = self.compile(src.layout, dst.layout, "transfer", include_bf16)
+        self.execute(plan, src, dst, stream)
+        return plan
+
+    def redundant_backup(self, is_scale_up: bool, src: TrainingState, dst: TrainingState,
+                         stream=None) -> CompiledPlan:
+        """Group-ZeRO switch (transfer.py:343-388): fp32 shards replicated or dropped."""
+        plan = self.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
+        self.execute(plan, src, dst, stream)
+        return plan
+
+    def get_communication_bytes(self) -> float:
+        """Payload bytes moved since the last call, in GiB (communicator.py:118-122 units)."""
+        b = self._payload_bytes
+        self._payload_bytes = 0
+        return b / 1024 ** 3

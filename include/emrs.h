@@ -1,0 +1,202 @@
+/*
+ * emrs.h - C ABI of the reshard-repack copy-plan executor for MI355X (gfx950).
+ *
+ * The reference moves optimizer state with a Python executor that slices
+ * per-parameter tensors and exchanges them over injectable send/recv/broadcast
+ * callables:
+ *   TransferManager(send_fn, recv_fn, broadcast_fn)
+ *       elastic_megatron/transfer/transfer.py:23-34
+ *   TransferManager.transfer_optimizer_tensors(virtual_param_space)
+ *       elastic_megatron/transfer/transfer.py:291-341
+ *   TransferManager._send_optimizer_tensors / _recv_optimizer_tensors
+ *       elastic_megatron/transfer/transfer.py:36-101
+ *   TransferManager.redundant_backup (Group-ZeRO replication)
+ *       elastic_megatron/transfer/transfer.py:343-388
+ *   Communicator.send / recv (self-copy FIFO, pack/unpack copies)
+ *       elastic_megatron/transfer/communicator.py:61-96
+ *
+ * Here the whole transfer is one precomputed plan of copy segments executed
+ * by one kernel launch over device-resident buffers.  Every segment copies
+ * `rows` rows of `len` elements of `elem_bytes` bytes each, bit for bit:
+ *
+ *   for r in [0, rows):
+ *     dst[dst_buf][dst_off + r*dst_stride + i] = src[src_buf][src_off + r*src_stride + i],
+ *     i in [0, len)
+ *
+ * Conventions
+ *   - All offsets, lengths and strides are in elements of the segment's
+ *     elem_bytes (1, 2, 4 or 8).  Mixed element sizes may share one plan.
+ *   - Buffers are caller-owned device allocations; the library never
+ *     allocates or frees caller memory.  A plan owns only its own segment
+ *     table in device memory.
+ *   - Every function returns EMRS_OK (0) or a negative EMRS_ERR_* code and
+ *     never throws across the ABI; emrs_last_error() returns a description
+ *     of the last failure on the calling thread.
+ *   - Work is enqueued on the caller's stream (a hipStream_t passed as
+ *     void*; NULL is the null stream).  Execution is asynchronous.
+ *   - A plan may be executed concurrently on several streams; it holds no
+ *     mutable state after its first upload to a device.
+ */
+#ifndef EMRS_H
+#define EMRS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMRS_ABI_VERSION 1
+
+#define EMRS_OK 0
+#define EMRS_ERR_INVALID_ARGUMENT (-1)
+#define EMRS_ERR_OUT_OF_BOUNDS (-2)
+#define EMRS_ERR_MISALIGNED (-3)
+#define EMRS_ERR_OVERLAP (-4)
+#define EMRS_ERR_HIP (-5)
+#define EMRS_ERR_NO_DEVICE (-6)
+#define EMRS_ERR_TOO_MANY_BUFFERS (-7)
+#define EMRS_ERR_ALIAS (-8)
+
+/* Maximum number of source (and, separately, destination) buffers. */
+#define EMRS_MAX_BUFFERS 128
+
+/* emrs_plan_create flags */
+#define EMRS_PLAN_CHECK_DISJOINT 1u /* reject plans whose destination ranges overlap */
+
+/* One strided copy.  Units: elements of elem_bytes bytes. */
+typedef struct emrs_segment {
+  uint32_t src_buf;    /* index into the src_bases passed at execution */
+  uint32_t dst_buf;    /* index into the dst_bases passed at execution */
+  uint32_t elem_bytes; /* 1, 2, 4 or 8 */
+  uint32_t flags;      /* must be 0 */
+  uint64_t src_off;    /* first element of row 0 in the source buffer */
+  uint64_t dst_off;    /* first element of row 0 in the destination buffer */
+  uint64_t len;        /* elements per row */
+  uint64_t rows;       /* number of rows (>= 1) */
+  uint64_t src_stride; /* elements between source row starts (rows > 1) */
+  uint64_t dst_stride; /* elements between destination row starts (rows > 1), >= len */
+} emrs_segment;
+
+typedef struct emrs_plan emrs_plan;
+
+typedef struct emrs_plan_stats {
+  uint64_t n_segments;      /* segments as given */
+  uint64_t n_device_segments; /* after alignment splitting */
+  uint64_t payload_bytes;   /* bytes copied per execution (read once, written once) */
+  uint64_t vector_bytes;    /* part of payload moved with 16-byte accesses */
+  uint64_t scalar_bytes;    /* part of payload moved element by element */
+  uint64_t n_chunks;        /* work chunks per execution */
+  uint32_t n_src_bufs;
+  uint32_t n_dst_bufs;
+} emrs_plan_stats;
+
+/* Description of the last failure on this thread ("" if none). */
+const char *emrs_last_error(void);
+
+/* EMRS_ABI_VERSION of the loaded library. */
+int emrs_abi_version(void);
+
+/* Number of visible HIP devices (0 when none); never fails. */
+int emrs_device_count(void);
+
+/*
+ * Validate segments and build a plan.  Host-only: no device work is done
+ * here (the table is uploaded on first execution).
+ *   src_buf_bytes[i]: capacity in bytes of source buffer i (bounds check)
+ *   dst_buf_bytes[i]: capacity in bytes of destination buffer i
+ * Errors: INVALID_ARGUMENT (bad elem_bytes, rows == 0, dst_stride < len,
+ * unknown buffer id, nonzero flags), OUT_OF_BOUNDS (a row leaves its
+ * buffer), TOO_MANY_BUFFERS, OVERLAP (with EMRS_PLAN_CHECK_DISJOINT).
+ */
+int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs,
+                     const uint64_t *src_buf_bytes, uint32_t n_src_bufs,
+                     const uint64_t *dst_buf_bytes, uint32_t n_dst_bufs,
+                     uint32_t flags, emrs_plan **out_plan);
+
+int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
+
+/*
+ * Enqueue the plan on `stream`.  src_bases / dst_bases hold n_src_bufs /
+ * n_dst_bufs device pointers, each aligned to 16 bytes.  Source and
+ * destination buffers must not overlap (EMRS_ERR_ALIAS): the copy is out of
+ * place.  Replaces one call of TransferManager.transfer_optimizer_tensors
+ * (transfer.py:291-341) together with the bf16 rebuild of
+ * TrainingState.update_model_weight (training_state.py:176-197).
+ */
+int emrs_plan_execute(emrs_plan *plan, void *const *src_bases,
+                      void *const *dst_bases, void *stream);
+
+int emrs_plan_destroy(emrs_plan *plan);
+
+/*
+ * Launch-shape knobs of emrs_plan_execute, process-wide.  Results never
+ * depend on them; only speed does.
+ */
+typedef struct emrs_tuning {
+  uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
+                             0 (default): as many as can be resident at once */
+  uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
+  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 0) */
+  uint32_t reserved;
+} emrs_tuning;
+
+int emrs_get_tuning(emrs_tuning *out);
+int emrs_set_tuning(const emrs_tuning *t);
+
+/*
+ * Synthetic workload support (not on the reshard path).
+ *
+ * A piece is a run of one parameter's elements stored contiguously in a
+ * buffer.  Element i of the piece is element (local_start + i) of the
+ * parameter's TP-local tensor, laid out row-major with local_cols columns;
+ * local (r, c) maps to the full tensor at
+ *   row = (r < band_rows || band_rows == 0) ? r + row_off : r - band_rows + row_off2
+ *   col = c + col_off
+ * and full flat index row * full_cols + col.  band_rows splits the local rows
+ * into two bands (fused SwiGLU [W; V]); 0 means one band.
+ *
+ * kind selects the value stream and storage type:
+ *   0 param      bf16, ~N(0, 0.02)
+ *   1 main       fp32, exact upcast of the kind-0 value
+ *   2 exp_avg    fp32, ~N(0, 1e-3)
+ *   3 exp_avg_sq fp32, |N(0, 1e-6)|
+ * Every value is a pure function of (seed, param_id, kind, full flat index).
+ */
+typedef struct emrs_piece {
+  uint32_t buf;
+  uint32_t param_id;
+  uint32_t kind;
+  uint32_t reserved;
+  uint64_t buf_off;     /* elements of the piece's storage type */
+  uint64_t len;
+  uint64_t local_start;
+  uint64_t local_cols;
+  uint64_t full_cols;
+  uint64_t band_rows;
+  uint64_t row_off;
+  uint64_t row_off2;
+  uint64_t col_off;
+} emrs_piece;
+
+/* Write the synthetic values of every piece into its buffer. */
+int emrs_synth_fill(const emrs_piece *pieces, uint64_t n_pieces,
+                    void *const *bases, const uint64_t *buf_bytes,
+                    uint32_t n_bufs, uint64_t seed, void *stream);
+
+/*
+ * Compare every piece with its synthetic values.  Synchronous: waits for
+ * `stream`.  *mismatches receives the number of differing elements and
+ * *first_bad the smallest (piece index << 40 | element index) that differs
+ * (UINT64_MAX when none).
+ */
+int emrs_synth_verify(const emrs_piece *pieces, uint64_t n_pieces,
+                      void *const *bases, const uint64_t *buf_bytes,
+                      uint32_t n_bufs, uint64_t seed, void *stream,
+                      uint64_t *mismatches, uint64_t *first_bad);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMRS_H */

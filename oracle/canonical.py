@@ -1,0 +1,73 @@
+"""Oracle-2: destination pieces regenerated from full-tensor indices (test infrastructure).
+
+Independent of any plan: a TP-local element's full-tensor index follows from
+Megatron's partitioning (contiguous chunks along the partition dim; a fused
+SwiGLU fc1 holds [W_t; V_t], resharding_metadata.py:98-178), and its value
+from the seeded generator.
+"""
+
+import numpy as np
+
+from . import synth
+from .plan import dp_distributions, local_shape, stage, ep_rank, global_rank, tp_size, Strat
+
+
+def full_index(p, T, t, local_idx):
+    idx = np.asarray(local_idx, dtype=np.int64)
+    if not p["tp"] or T == 1:
+        return idx
+    shape = p["shape"]
+    if len(shape) == 1:
+        return t * (shape[0] // T) + idx
+    R, C = shape
+    if p["pdim"] == 0:
+        rl = R // T
+        r, c = np.divmod(idx, C)
+        if p["swiglu"]:
+            half, F = rl // 2, R // 2
+            fr = np.where(r < half, t * half + r, F + t * half + (r - half))
+        else:
+            fr = t * rl + r
+        return fr * C + c
+    cl = C // T
+    r, c = np.divmod(idx, cl)
+    return r * C + t * cl + c
+
+
+def piece_values(seed, p, T, t, lo, hi):
+    """{kind: array} for local elements [lo, hi) of TP rank t at TP size T."""
+    f = full_index(p, T, t, np.arange(lo, hi))
+    return {k: synth.values(seed, p["id"], k, f) for k in ("main", "exp_avg", "exp_avg_sq")}
+
+
+def shard_key(p, strat, hp, t):
+    s = stage(p, strat.pp, hp.num_layers)
+    if p["expert"] is None:
+        return ("dense", s, t)
+    return ("expert", s, ep_rank(p, strat, hp.num_experts), t)
+
+
+def world(inv, hp, strat, seed, params=None):
+    """({(rank, pid): {kind: array}}, {(shard key, pid): bf16 bits}) of a layout."""
+    dist = dp_distributions(inv, strat, hp)
+    fp32, bf16 = {}, {}
+    for p in inv:
+        if params is not None and p["id"] not in params:
+            continue
+        if p["id"] not in dist:
+            continue
+        s = stage(p, strat.pp, hp.num_layers)
+        T = tp_size(strat, p)
+        e = ep_rank(p, strat, hp.num_experts) if p["expert"] is not None else None
+        for t in range(T):
+            for r, (lo, hi) in dist[p["id"]].items():
+                for inst in range(strat.inst):
+                    if e is None:
+                        g = s * (strat.dp * strat.cp * strat.tp) + (inst * strat.pdp + r) * strat.tp + t
+                    else:
+                        g = global_rank(strat, s, r, e, t)
+                    fp32[(g, p["id"])] = piece_values(seed, p, T, t, lo, hi)
+            n = int(np.prod(local_shape(p, T)))
+            bf16[(shard_key(p, strat, hp, t), p["id"])] = synth.values(
+                seed, p["id"], "param", full_index(p, T, t, np.arange(n)))
+    return fp32, bf16

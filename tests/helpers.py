@@ -1,0 +1,128 @@
+"""Shared test utilities: small model shapes, numpy executors and comparisons."""
+
+from dataclasses import replace
+
+import numpy as np
+
+from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
+from elasticmegatron_amd.resharding import model_spec as ms
+from elasticmegatron_amd.resharding.layout import ARENA_PARAM, PIECE_DTYPE
+from oracle import synth
+from oracle.plan import Strat
+
+SEED = 1234
+
+
+# Small models with the structure of each reshard workload (GQA, MoE, buckets, PP).
+def small_llama2():
+    return ms.ModelSpec(name="small-llama2", num_layers=4, hidden_size=256, num_attention_heads=4,
+                        ffn_hidden_size=688, padded_vocab_size=1024, ddp_bucket_size=150_000,
+                        overlap_grad_reduce=True)
+
+
+def small_llama3():
+    return ms.ModelSpec(name="small-llama3", num_layers=4, hidden_size=256, num_attention_heads=8,
+                        num_query_groups=2, kv_channels=32, ffn_hidden_size=896, padded_vocab_size=2048,
+                        ddp_bucket_size=200_000, overlap_grad_reduce=True)
+
+
+def small_mixtral():
+    return ms.ModelSpec(name="small-mixtral", num_layers=2, hidden_size=256, num_attention_heads=8,
+                        num_query_groups=2, kv_channels=32, ffn_hidden_size=512, padded_vocab_size=1024,
+                        num_experts=8, moe_ffn_hidden_size=512, ddp_bucket_size=300_000,
+                        overlap_grad_reduce=True)
+
+
+# (name, spec factory, [strategies]) -- consecutive strategies are switched.
+SMALL_CASES = [
+    ("tiny_tp2dp4_tp1dp8_tp4dp2", ms.tiny_llama2, [PS(8, 2, 1), PS(8, 1, 1), PS(8, 4, 1)]),
+    ("llama2_tp1dp8_tp4dp2", small_llama2, [PS(8, 1, 1), PS(8, 4, 1)]),
+    ("llama3_tp2pp2dp2_tp4pp1dp2", small_llama3, [PS(8, 2, 2), PS(8, 4, 1)]),
+    ("mixtral_ep4_ep8", small_mixtral, [PS(8, 1, 1, expert_model_parallel_size=4),
+                                        PS(8, 1, 1, expert_model_parallel_size=8)]),
+    ("llama2_dp8_dp6", small_llama2, [PS(8, 1, 1), PS(6, 1, 1)]),
+    ("llama2_pp4_tp2", small_llama2, [PS(8, 1, 4), PS(8, 2, 1), PS(8, 2, 2)]),
+    ("llama3_tp4_tp1pp2", small_llama3, [PS(8, 4, 1), PS(8, 1, 2)]),
+]
+
+
+def piece_fill_numpy(pieces, arenas, seed):
+    """Restatement of emrs_synth_fill on numpy arenas (uint32 fp32 bits / uint16 bf16 bits)."""
+    for p in pieces:
+        n = int(p["len"])
+        if n == 0:
+            continue
+        li = int(p["local_start"]) + np.arange(n, dtype=np.int64)
+        r, c = np.divmod(li, int(p["local_cols"]))
+        br = int(p["band_rows"])
+        if br:
+            row = np.where(r < br, r + int(p["row_off"]), r - br + int(p["row_off2"]))
+        else:
+            row = r + int(p["row_off"])
+        f = row * int(p["full_cols"]) + c + int(p["col_off"])
+        kind = int(p["kind"])
+        name = ("param", "main", "exp_avg", "exp_avg_sq")[kind]
+        v = synth.values(seed, int(p["param_id"]), name, f)
+        off = int(p["buf_off"])
+        arenas[int(p["buf"])][off:off + n] = v.view(np.uint16) if kind == 0 else v.view(np.uint32)
+
+
+def new_arenas(layout, fill=0xFFFFFFFF):
+    f32 = [np.full(layout.fp32_numel, fill, dtype=np.uint32) for _ in range(3)]
+    return f32 + [np.full(layout.bf16_numel, fill & 0xFFFF, dtype=np.uint16)]
+
+
+def execute_numpy(table, src, dst):
+    """Reference semantics of emrs_plan_execute on numpy arenas."""
+    for s in table:
+        a, b = src[int(s["src_buf"])], dst[int(s["dst_buf"])]
+        so, do, n, rows = int(s["src_off"]), int(s["dst_off"]), int(s["len"]), int(s["rows"])
+        if rows == 1:
+            b[do:do + n] = a[so:so + n]
+            continue
+        ss, ds = int(s["src_stride"]), int(s["dst_stride"])
+        sv = np.lib.stride_tricks.as_strided(a[so:], shape=(rows, n), strides=(ss * a.itemsize, a.itemsize))
+        dv = np.lib.stride_tricks.as_strided(b[do:], shape=(rows, n), strides=(ds * b.itemsize, b.itemsize))
+        dv[...] = sv
+
+
+def extract(layout, arenas, params=None):
+    """({(rank, pid): {kind: uint32 bits}}, {(shard key, pid): uint16 bits}) from product arenas."""
+    space = layout.space
+    fp32, bf16 = {}, {}
+    vps = [space.all_virtual_params[g] for g in sorted(layout.place)]
+    for vp in vps:
+        if params is not None and vp.global_index not in params:
+            continue
+        for h in layout.fp32_holders(vp):
+            n = h.hi - h.lo
+            fp32[(h.rank, vp.global_index)] = {
+                k: arenas[i][h.offset:h.offset + n] for i, k in enumerate(("main", "exp_avg", "exp_avg_sq"))}
+        for h in layout.bf16_holders(vp):
+            n = h.hi - h.lo
+            bf16[(layout.shard_keys[h.rank], vp.global_index)] = arenas[ARENA_PARAM][h.offset:h.offset + n]
+    return fp32, bf16
+
+
+def compare(got32, gotbf, want32, wantbf):
+    """Returns a list of mismatch descriptions (empty when bit-exact and complete)."""
+    errs = []
+    if set(got32) != set(want32):
+        errs.append(f"fp32 piece keys differ: {sorted(set(got32) ^ set(want32))[:5]}")
+    for k in set(got32) & set(want32):
+        for kind in ("main", "exp_avg", "exp_avg_sq"):
+            g = np.asarray(got32[k][kind]).view(np.uint32)
+            w = np.asarray(want32[k][kind]).view(np.uint32)
+            if g.shape != w.shape or not np.array_equal(g, w):
+                bad = np.flatnonzero(g != w) if g.shape == w.shape else []
+                errs.append(f"fp32 {k} {kind}: {len(bad)} differ, first {bad[:3]}")
+    if set(gotbf) != set(wantbf):
+        errs.append(f"bf16 keys differ: {sorted(set(gotbf) ^ set(wantbf))[:5]}")
+    for k in set(gotbf) & set(wantbf):
+        if not np.array_equal(np.asarray(gotbf[k]).view(np.uint16), np.asarray(wantbf[k]).view(np.uint16)):
+            errs.append(f"bf16 {k} differs")
+    return errs
+
+
+def strat(ps):
+    return Strat.of(ps)

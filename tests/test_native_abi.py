@@ -1,0 +1,107 @@
+"""The C ABI: the library loads, exports what include/emrs.h declares, and
+validates plans on the host (no GPU needed)."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from elasticmegatron_amd import _native
+from elasticmegatron_amd.resharding.layout import PIECE_DTYPE, SEGMENT_DTYPE
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "emrs.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*\s*|int\s+)(emrs_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol():
+    lib = _native.load()
+    declared = _declared()
+    assert set(declared) == set(_native.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.emrs_abi_version() == 1
+
+
+def test_record_layouts_match_header():
+    class Seg(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_uint32) for n in ("src_buf", "dst_buf", "elem_bytes", "flags")] + \
+                   [(n, ctypes.c_uint64) for n in ("src_off", "dst_off", "len", "rows", "src_stride", "dst_stride")]
+
+    assert ctypes.sizeof(Seg) == SEGMENT_DTYPE.itemsize == 64
+    for name, (dt, off) in SEGMENT_DTYPE.fields.items():
+        assert getattr(Seg, name).offset == off
+    assert PIECE_DTYPE.itemsize == 88
+
+
+def _seg(**kw):
+    row = dict(src_buf=0, dst_buf=0, elem_bytes=4, flags=0, src_off=0, dst_off=0, len=16, rows=1,
+               src_stride=0, dst_stride=0)
+    row.update(kw)
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    for k, v in row.items():
+        t[0][k] = v
+    return t
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(elem_bytes=3), -1),
+    (dict(rows=0), -1),
+    (dict(flags=1), -1),
+    (dict(dst_buf=1), -1),
+    (dict(rows=2, len=16, src_stride=16, dst_stride=8), -1),
+    (dict(src_off=250, len=16), -2),
+    (dict(dst_off=1, len=256), -2),
+    (dict(rows=3, len=10, src_stride=200, dst_stride=10), -2),
+])
+def test_plan_create_rejects(kw, code):
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(_seg(**kw), [1024], [1024])
+    assert e.value.code == code
+
+
+def test_plan_create_overlap_check():
+    t = np.concatenate([_seg(dst_off=0, len=10), _seg(src_off=20, dst_off=9, len=4)])
+    _native.Plan(t, [1024], [1024])  # allowed without the check
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(t, [1024], [1024], check_disjoint=True)
+    assert e.value.code == -4
+
+
+def test_too_many_buffers():
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(_seg(), [64] * 129, [64])
+    assert e.value.code == -7
+
+
+def test_plan_stats_classify_alignment():
+    rows = [
+        (0, 0, 4, 0, 0, 0, 64, 1, 0, 0),      # vector: 256 bytes
+        (0, 0, 4, 0, 1, 1, 12, 1, 0, 0),      # co-aligned, 4 B off: 3 head + 8 body + 1 tail elements
+        (0, 0, 4, 0, 1, 2, 8, 1, 0, 0),       # not co-aligned: scalar
+        (0, 0, 2, 0, 0, 0, 8, 4, 16, 8),      # strided bf16 rows of 16 bytes: vector
+        (0, 0, 2, 0, 0, 64, 3, 4, 8, 5),      # strided, odd: scalar
+    ]
+    t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
+    t[:] = rows
+    st = _native.Plan(t, [4096], [4096]).stats()
+    assert st.payload_bytes == 256 + 48 + 32 + 64 + 24
+    assert st.vector_bytes == 256 + 32 + 64
+    assert st.scalar_bytes == 16 + 32 + 24
+    assert st.n_segments == 5
+
+
+def test_empty_plan_and_no_device_errors():
+    plan = _native.Plan(np.zeros(0, dtype=SEGMENT_DTYPE), [16], [16])
+    assert plan.stats().payload_bytes == 0
+    if _native.device_count() == 0:
+        # Host-side checks happen before any device work; a real execution needs a GPU.
+        t = _native.Plan(_seg(), [1024], [1024])
+        with pytest.raises(_native.EmrsError) as e:
+            t.execute([0x10000], [0x20000], 0)
+        assert e.value.code == -6
