@@ -129,7 +129,7 @@ def get_tuning() -> Tuning:
     return t
 
 
-def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = False) -> None:
+def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True) -> None:
     t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, 0)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 

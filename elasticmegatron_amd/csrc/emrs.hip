@@ -103,7 +103,7 @@ __host__ __device__ __forceinline__ uint32_t magic_div(uint32_t n, uint32_t m, u
 struct Tuning {
   std::atomic<uint32_t> blocks_per_cu{0};  // 0: as many as can be resident
   std::atomic<uint32_t> nontemporal{1};
-  std::atomic<uint32_t> xcd_remap{0};
+  std::atomic<uint32_t> xcd_remap{1};
 };
 Tuning g_tuning;
 
@@ -264,6 +264,7 @@ struct emrs_plan {
   std::vector<DevSeg> segs;
   uint64_t n_chunks = 0;
   std::vector<uint64_t> src_bytes, dst_bytes;
+  std::vector<uint8_t> src_used, dst_used;  // buffers referenced by a non-empty segment
   emrs_plan_stats stats{};
   std::mutex mu;
   std::vector<DevSeg *> dev_tables;  // per device, uploaded on first use
@@ -416,6 +417,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   Builder bld;
   bld.out.reserve(n_segs);
   uint64_t payload = 0;
+  std::vector<uint8_t> src_used(n_src_bufs, 0), dst_used(n_dst_bufs, 0);
   for (uint64_t i = 0; i < n_segs; ++i) {
     const emrs_segment &s = segs[i];
     char where[64];
@@ -437,6 +439,8 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     if (de > dst_buf_bytes[s.dst_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, std::string(where) + "destination range exceeds its buffer");
     payload += s.len * s.rows * s.elem_bytes;
+    src_used[s.src_buf] = 1;
+    dst_used[s.dst_buf] = 1;
 
     const uint64_t eb = s.elem_bytes;
     const uint64_t so = s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
@@ -476,6 +480,8 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   p->n_chunks = bld.chunks;
   p->src_bytes.assign(src_buf_bytes, src_buf_bytes + n_src_bufs);
   p->dst_bytes.assign(dst_buf_bytes, dst_buf_bytes + n_dst_bufs);
+  p->src_used = std::move(src_used);
+  p->dst_used = std::move(dst_used);
   p->stats.n_segments = n_segs;
   p->stats.n_device_segments = p->segs.size();
   p->stats.payload_bytes = payload;
@@ -501,34 +507,35 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
   if ((ns && !src_bases) || (nd && !dst_bases))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
+  // Only buffers that some segment references are checked: an unreferenced
+  // buffer may be NULL or alias anything.
   Bases sb{}, db{};
   for (uint32_t i = 0; i < ns; ++i) {
     sb.p[i] = static_cast<char *>(src_bases[i]);
-    if (!sb.p[i] && plan->src_bytes[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
+    if (!plan->src_used[i]) continue;
+    if (!sb.p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
     if (reinterpret_cast<uintptr_t>(sb.p[i]) % 16)
       return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
   }
   for (uint32_t i = 0; i < nd; ++i) {
     db.p[i] = static_cast<char *>(dst_bases[i]);
-    if (!db.p[i] && plan->dst_bytes[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
+    if (!plan->dst_used[i]) continue;
+    if (!db.p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
     if (reinterpret_cast<uintptr_t>(db.p[i]) % 16)
       return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
   }
-  for (uint32_t i = 0; i < ns; ++i) {
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(sb.p[i]), a1 = a0 + plan->src_bytes[i];
-    for (uint32_t j = 0; j < nd; ++j) {
-      const uintptr_t b0 = reinterpret_cast<uintptr_t>(db.p[j]), b1 = b0 + plan->dst_bytes[j];
-      if (a0 < b1 && b0 < a1 && a1 > a0 && b1 > b0)
-        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
-    }
-  }
+  auto overlap = [](uintptr_t a0, uint64_t an, uintptr_t b0, uint64_t bn) {
+    return an && bn && a0 < b0 + bn && b0 < a0 + an;
+  };
   for (uint32_t j = 0; j < nd; ++j) {
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(db.p[j]), a1 = a0 + plan->dst_bytes[j];
-    for (uint32_t k = j + 1; k < nd; ++k) {
-      const uintptr_t b0 = reinterpret_cast<uintptr_t>(db.p[k]), b1 = b0 + plan->dst_bytes[k];
-      if (a0 < b1 && b0 < a1 && a1 > a0 && b1 > b0)
+    if (!plan->dst_used[j]) continue;
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(db.p[j]);
+    for (uint32_t i = 0; i < ns; ++i)
+      if (plan->src_used[i] && overlap(reinterpret_cast<uintptr_t>(sb.p[i]), plan->src_bytes[i], d0, plan->dst_bytes[j]))
+        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
+    for (uint32_t k = j + 1; k < nd; ++k)
+      if (plan->dst_used[k] && overlap(d0, plan->dst_bytes[j], reinterpret_cast<uintptr_t>(db.p[k]), plan->dst_bytes[k]))
         return fail(EMRS_ERR_ALIAS, "two destination buffers overlap");
-    }
   }
   if (plan->n_chunks == 0) return EMRS_OK;
 

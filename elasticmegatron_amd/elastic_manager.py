@@ -80,10 +80,19 @@ class ElasticMegatronManager:
         return t.elapsed
 
     def log_communication_info(self, transfer_time: float, logger: Optional[logging.Logger] = None) -> str:
+        """The reference's perf line (elastic_manager.py:158-178) plus this build's HBM payload.
+
+        ``communication bytes`` keeps the reference's definition (GiB a rank
+        would exchange with other ranks, max over ranks); ``payload`` is the
+        decimal GB of state written on the device.
+        """
         gib = self.transfer_manager.get_communication_bytes()
+        payload = self.transfer_manager.get_payload_bytes()
         bw = 1000 * gib / transfer_time if transfer_time > 0 else float("inf")
+        pbw = payload / transfer_time / 1e6 if transfer_time > 0 else float("inf")
         msg = (f"[ElasticMegatron-Perf] : transfer time: {transfer_time:.2f} ms, "
-               f"communication bytes: {gib:.2f} GB, bandwidth: {bw:.2f} GB/s")
+               f"communication bytes: {gib:.2f} GB, bandwidth: {bw:.2f} GB/s "
+               f"(payload {payload / 1e9:.2f} GB at {pbw:.1f} GB/s)")
         if logger is not None:
             logger.info(msg)
         return msg

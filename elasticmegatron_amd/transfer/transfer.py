@@ -23,6 +23,7 @@ import torch
 from .. import _native
 from ..megatron_manager.parallel_strategy import ParallelStrategy
 from ..megatron_manager.training_state import TrainingState
+from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes
 from ..resharding.layout import StrategyLayout
 
@@ -34,6 +35,7 @@ class CompiledPlan:
     payload_bytes: int
     src: ParallelStrategy
     dst: ParallelStrategy
+    reference_comm_bytes: int = 0   # the reference's per-rank cross-rank volume, max over ranks
 
 
 class TransferManager:
@@ -44,6 +46,7 @@ class TransferManager:
         self.check_disjoint = check_disjoint
         self.fake_transfer = False
         self._payload_bytes = 0
+        self._comm_bytes = 0
 
     def set_fake_transfer(self, fake: bool) -> None:
         """Plan without moving data (transfer.py:32-34)."""
@@ -63,8 +66,14 @@ class TransferManager:
             raise ValueError(kind)
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
+        if kind == "transfer":
+            comm = max(reference_comm_bytes(src.space, src.strategy, dst.strategy).values(), default=0)
+        elif kind == "backup_up":  # every rank joins the broadcast of its whole shard (transfer.py:377-388)
+            comm = max(dst.rank_numel) * FP32_TENSORS_BYTES
+        else:  # param_migrate is a local copy (training_state.py:40-60)
+            comm = 0
         cp = CompiledPlan(table, _native.Plan(table, sb, db, self.check_disjoint), payload_bytes(table),
-                          src.strategy, dst.strategy)
+                          src.strategy, dst.strategy, comm)
         self._plans[key] = cp
         return cp
 
@@ -80,6 +89,7 @@ class TransferManager:
         with torch.cuda.device(src.device):
             plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)
         self._payload_bytes += plan.payload_bytes
+        self._comm_bytes += plan.reference_comm_bytes
 
     def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
                                    dst: Optional[TrainingState] = None, include_bf16: bool = True,
@@ -104,7 +114,17 @@ class TransferManager:
         return plan
 
     def get_communication_bytes(self) -> float:
-        """Payload bytes moved since the last call, in GiB (communicator.py:118-122 units)."""
+        """The reference's communication figure since the last call, in GiB, then reset.
+
+        Max over ranks of fp32 bytes sent to or received from other ranks
+        (communicator.py:118-122); see :mod:`..resharding.comm_stats`.
+        """
+        b = self._comm_bytes
+        self._comm_bytes = 0
+        return b / 1024 ** 3
+
+    def get_payload_bytes(self) -> int:
+        """Bytes of state written to the destination since the last call (each read once), then reset."""
         b = self._payload_bytes
         self._payload_bytes = 0
-        return b / 1024 ** 3
+        return b

@@ -118,9 +118,11 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
 
 /*
  * Enqueue the plan on `stream`.  src_bases / dst_bases hold n_src_bufs /
- * n_dst_bufs device pointers, each aligned to 16 bytes.  Source and
- * destination buffers must not overlap (EMRS_ERR_ALIAS): the copy is out of
- * place.  Replaces one call of TransferManager.transfer_optimizer_tensors
+ * n_dst_bufs device pointers.  Every buffer that a segment references must
+ * be 16-byte aligned (EMRS_ERR_MISALIGNED) and must not overlap a referenced
+ * buffer of the other side or another referenced destination buffer
+ * (EMRS_ERR_ALIAS): the copy is out of place.  Unreferenced buffers are not
+ * checked and may be NULL.  Replaces one call of TransferManager.transfer_optimizer_tensors
  * (transfer.py:291-341) together with the bf16 rebuild of
  * TrainingState.update_model_weight (training_state.py:176-197).
  */
@@ -137,7 +139,7 @@ typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
                              0 (default): as many as can be resident at once */
   uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
-  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 0) */
+  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 1) */
   uint32_t reserved;
 } emrs_tuning;
 

@@ -178,6 +178,13 @@ def test_execute_errors(gpu_device):
     assert e.value.code == -3
     empty = _native.Plan(np.zeros(0, dtype=SEGMENT_DTYPE), [1024], [1024])
     empty.execute([buf.data_ptr()], [other.data_ptr()], 0)
+    # A buffer no segment references may alias anything (a shared bf16 arena, say) or be NULL.
+    buf.copy_((torch.arange(1024, device=gpu_device) % 251).to(torch.uint8))
+    two = _native.Plan(t, [1024, 1024], [1024, 1024])
+    two.execute([buf.data_ptr(), other.data_ptr()], [other.data_ptr() + 1024, other.data_ptr()], 0)
+    two.execute([buf.data_ptr(), 0], [other.data_ptr() + 1024, 0], 0)
+    torch.cuda.synchronize()
+    assert torch.equal(other[1024:1088], buf[:64])
 
 
 def test_manager_sequence(gpu_device):

@@ -1,0 +1,81 @@
+"""ParallelStrategy sizes and rank arithmetic
+(megatron_manager/parallel_strategy.py:10-147, :234-263; resharding/resharding.py:19-51)."""
+
+import itertools
+
+import pytest
+
+from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS, global_rank_of
+from oracle.plan import Strat, global_rank as oracle_global_rank
+
+
+def _enumerate(order_sizes):
+    """Ranks in Megatron's generator order: the first dimension varies fastest."""
+    names = [n for n, _ in order_sizes]
+    sizes = [s for _, s in order_sizes]
+    out = {}
+    rank = 0
+    for coords in itertools.product(*[range(s) for s in reversed(sizes)]):
+        out[tuple(reversed(coords))] = rank
+        rank += 1
+    return names, out
+
+
+@pytest.mark.parametrize("W,tp,pp,cp", [(8, 2, 2, 1), (8, 1, 1, 1), (16, 2, 2, 2), (12, 1, 3, 2), (8, 4, 2, 1)])
+def test_dense_rank_order_tp_cp_dp_pp(W, tp, pp, cp):
+    s = PS(W, tp, pp, context_parallel_size=cp)
+    dp = W // (tp * pp * cp)
+    assert s.data_parallel_size == dp and s.optimizer_data_parallel_size == dp * cp
+    _, ranks = _enumerate([("tp", tp), ("cp", cp), ("dp", dp), ("pp", pp)])
+    for (t, c, d, p), g in ranks.items():
+        dpcp = d * cp + c  # the DP-CP group enumerates cp fastest
+        assert global_rank_of(s, p, dpcp, None, t) == g
+        assert oracle_global_rank(Strat.of(s), p, dpcp, None, t) == g
+        assert s.dense_rank_coords(g) == (p, dpcp, t)
+
+
+@pytest.mark.parametrize("W,ep,pp", [(8, 4, 1), (8, 8, 1), (16, 2, 2), (8, 2, 2)])
+def test_expert_rank_order_etp_ep_dp_pp(W, ep, pp):
+    s = PS(W, 1, pp, expert_model_parallel_size=ep)
+    edp = W // (ep * pp)
+    assert s.expert_data_parallel_size == edp
+    _, ranks = _enumerate([("etp", 1), ("ep", ep), ("edp", edp), ("pp", pp)])
+    for (t, e, d, p), g in ranks.items():
+        assert global_rank_of(s, p, d, e, t) == g
+        assert oracle_global_rank(Strat.of(s), p, d, e, t) == g
+        assert s.expert_rank_coords(g) == (p, d, e, t)
+
+
+def test_sizes_and_validation():
+    s = PS(12, 1, 1, num_distributed_optimizer_instances=2)
+    assert s.data_parallel_size == 12 and s.optimizer_data_parallel_size == 6
+    assert s.expert_tensor_parallel_size == 1 and s.sequence_parallel is False
+    assert PS(8, 2, 1).sequence_parallel is True
+    with pytest.raises(ValueError):
+        PS(8, 3, 1)
+    with pytest.raises(ValueError):
+        PS(8, 1, 1, sequence_parallel=True)
+    with pytest.raises(ValueError):
+        PS(6, 1, 1, num_distributed_optimizer_instances=4)
+    with pytest.raises(RuntimeError):
+        PS(6, 1, 1, expert_model_parallel_size=4)
+    with pytest.raises(AssertionError):
+        PS(8, 1, 2).validate_for(num_layers=3, num_experts=None)
+    with pytest.raises(AssertionError):
+        PS(8, 2, 1).validate_for(4, num_experts=8)  # ETP defaults to TP and must be 1 with experts
+    PS(8, 2, 1, expert_tensor_parallel_size=1).validate_for(4, 8)
+    assert PS(8, 1, 1) == PS(8, 1, 1, sequence_parallel=False) and hash(PS(8, 1, 1)) == hash(PS(8, 1, 1))
+
+
+def test_is_redundant_backup():
+    a = PS(6, 1, 1)
+    b = PS(12, 1, 1, num_distributed_optimizer_instances=2)
+    assert PS.is_redundant_backup(a, b) is True
+    assert PS.is_redundant_backup(b, a) is False
+    assert PS.is_redundant_backup(a, PS(8, 1, 1)) is None
+    with pytest.raises(ValueError):
+        PS.is_redundant_backup(b, b)
+    with pytest.raises(AssertionError):
+        PS.is_redundant_backup(PS(6, 2, 1), b)
+    with pytest.raises(AssertionError):
+        PS.is_redundant_backup(PS(8, 1, 1), b)
