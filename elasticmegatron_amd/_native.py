@@ -49,7 +49,7 @@ class EmrsError(RuntimeError):
 class PlanStats(ctypes.Structure):
     _fields_ = [
         ("n_segments", ctypes.c_uint64), ("n_device_segments", ctypes.c_uint64),
-        ("payload_bytes", ctypes.c_uint64), ("vector_bytes", ctypes.c_uint64),
+        ("payload_bytes", ctypes.c_uint64), ("read_bytes", ctypes.c_uint64), ("vector_bytes", ctypes.c_uint64),
         ("scalar_bytes", ctypes.c_uint64), ("n_chunks", ctypes.c_uint64),
         ("n_src_bufs", ctypes.c_uint32), ("n_dst_bufs", ctypes.c_uint32),
     ]

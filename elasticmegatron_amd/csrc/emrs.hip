@@ -23,6 +23,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "emrs.h"
@@ -48,8 +49,14 @@ int hip_fail(hipError_t e, const char *what) {
   return fail(EMRS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 8;
+#ifndef EMRS_COPY_THREADS
+#define EMRS_COPY_THREADS 256  // lanes per workgroup
+#endif
+#ifndef EMRS_COPY_UNROLL
+#define EMRS_COPY_UNROLL 8  // 16-byte loads in flight per lane
+#endif
+constexpr int kThreads = EMRS_COPY_THREADS;
+constexpr int kUnroll = EMRS_COPY_UNROLL;
 constexpr uint32_t kChunkUnits = kThreads * kUnroll;  // units per work chunk
 constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 bits
 
@@ -61,24 +68,29 @@ struct Bases {
 
 // Segment as the kernel sees it.  Offsets and strides are in units of
 // (1 << unit_log2) bytes: 16 for the vector path, the element size otherwise.
+// A cast segment (fp32 only) also writes bf16 copies to aux, whose offset and
+// stride are in units of half that size (8 bytes, or one bf16).
 struct DevSeg {
   uint64_t src_off;
   uint64_t dst_off;
   uint64_t chunk_begin;  // index of this segment's first chunk
+  uint64_t aux_off;
   uint32_t len;          // units per row
   uint32_t rows;
   uint32_t src_stride;
   uint32_t dst_stride;
+  uint32_t aux_stride;
   uint32_t magic;        // row = (t + ((u - t) >> sh1)) >> sh2, t = umulhi(magic, u)
   uint8_t sh1;
   uint8_t sh2;
   uint8_t unit_log2;
-  uint8_t pad0;
+  uint8_t cast;          // 1: also write bf16 to aux
   uint8_t src_buf;
   uint8_t dst_buf;
-  uint8_t pad1[6];
+  uint8_t aux_buf;
+  uint8_t pad;
 };
-static_assert(sizeof(DevSeg) == 56, "DevSeg layout");
+static_assert(sizeof(DevSeg) == 64, "DevSeg layout");
 
 // Division by an invariant divisor (Granlund & Montgomery 1994, fig. 4.1).
 void make_magic(uint32_t d, uint32_t *m, uint8_t *sh1, uint8_t *sh2) {
@@ -123,46 +135,84 @@ __device__ __forceinline__ void st(T *p, T v) {
   else *p = v;
 }
 
-// Copy units [u0, u_end) of segment s, 0 < u_end - u0 <= kChunkUnits.  In a
-// partial chunk, lanes past the end load the last unit again (in bounds) so
-// that every load is unconditional; only their stores are masked off.
-template <typename T, bool kNT>
-__device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, char *dbase,
+// fp32 -> bf16 rounded to nearest even; NaN becomes the quiet NaN 0x7FC0
+// (the rounding torch applies in float -> bfloat16 conversions).
+__device__ __forceinline__ uint32_t bf16_rne(uint32_t u) {
+  return (u & 0x7fffffffu) > 0x7f800000u ? 0x7fc0u : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <typename T>
+struct CastOf;  // bf16 image of one unit
+template <>
+struct CastOf<u32x4> {
+  typedef unsigned int type __attribute__((ext_vector_type(2)));
+  __device__ static type cast(u32x4 v) {
+    type r;
+    r.x = bf16_rne(v.x) | (bf16_rne(v.y) << 16);
+    r.y = bf16_rne(v.z) | (bf16_rne(v.w) << 16);
+    return r;
+  }
+};
+template <>
+struct CastOf<uint32_t> {
+  typedef uint16_t type;
+  __device__ static type cast(uint32_t v) { return (uint16_t)bf16_rne(v); }
+};
+
+// Copy units [u0, u_end) of segment s, 0 < u_end - u0 <= kChunkUnits; with
+// kCast also store each unit's bf16 image to aux.  In a partial chunk, lanes
+// past the end load the last unit again (in bounds) so that every load is
+// unconditional; only their stores are masked off.
+template <typename T, bool kNT, bool kCast>
+__device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, char *dbase, char *abase,
                                            uint32_t u0, uint32_t u_end) {
+  typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
   const T *src = reinterpret_cast<const T *>(sbase);
   T *dst = reinterpret_cast<T *>(dbase);
+  A *aux = reinterpret_cast<A *>(abase);
   const uint32_t tid = threadIdx.x;
   const uint32_t n = u_end - u0;
   T v[kUnroll];
   if (s.rows == 1) {
     const T *sp = src + s.src_off + u0;
     T *dp = dst + s.dst_off + u0;
+    A *ap = aux + s.aux_off + u0;
     if (n == kChunkUnits) {
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + j * kThreads + tid);
 #pragma unroll
-      for (int j = 0; j < kUnroll; ++j) st<T, kNT>(dp + j * kThreads + tid, v[j]);
+      for (int j = 0; j < kUnroll; ++j) {
+        st<T, kNT>(dp + j * kThreads + tid, v[j]);
+        if constexpr (kCast) st<A, kNT>(ap + j * kThreads + tid, C::cast(v[j]));
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + min(j * kThreads + tid, n - 1));
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j)
-        if (j * kThreads + tid < n) st<T, kNT>(dp + j * kThreads + tid, v[j]);
+        if (j * kThreads + tid < n) {
+          st<T, kNT>(dp + j * kThreads + tid, v[j]);
+          if constexpr (kCast) st<A, kNT>(ap + j * kThreads + tid, C::cast(v[j]));
+        }
     }
     return;
   }
-  uint64_t dof[kUnroll];
+  uint32_t row[kUnroll], col[kUnroll];
 #pragma unroll
   for (int j = 0; j < kUnroll; ++j) {
     const uint32_t u = u0 + min(j * kThreads + tid, n - 1);
-    const uint32_t row = magic_div(u, s.magic, s.sh1, s.sh2);
-    const uint32_t col = u - row * s.len;
-    v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row * s.src_stride + col);
-    dof[j] = s.dst_off + (uint64_t)row * s.dst_stride + col;
+    row[j] = magic_div(u, s.magic, s.sh1, s.sh2);
+    col[j] = u - row[j] * s.len;
+    v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row[j] * s.src_stride + col[j]);
   }
 #pragma unroll
   for (int j = 0; j < kUnroll; ++j)
-    if (j * kThreads + tid < n) st<T, kNT>(dst + dof[j], v[j]);
+    if (j * kThreads + tid < n) {
+      st<T, kNT>(dst + s.dst_off + (uint64_t)row[j] * s.dst_stride + col[j], v[j]);
+      if constexpr (kCast)
+        st<A, kNT>(aux + s.aux_off + (uint64_t)row[j] * s.aux_stride + col[j], C::cast(v[j]));
+    }
 }
 
 template <bool kNT>
@@ -197,12 +247,18 @@ __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
     const uint32_t u_end = min(u0 + kChunkUnits, total);
     const char *sb = src.p[s.src_buf];
     char *db = dst.p[s.dst_buf];
+    char *ab = dst.p[s.aux_buf];
+    if (s.cast) {
+      if (s.unit_log2 == 4) copy_chunk<u32x4, kNT, true>(s, sb, db, ab, u0, u_end);
+      else copy_chunk<uint32_t, kNT, true>(s, sb, db, ab, u0, u_end);
+      continue;
+    }
     switch (s.unit_log2) {
-      case 4: copy_chunk<u32x4, kNT>(s, sb, db, u0, u_end); break;
-      case 3: copy_chunk<uint64_t, kNT>(s, sb, db, u0, u_end); break;
-      case 2: copy_chunk<uint32_t, kNT>(s, sb, db, u0, u_end); break;
-      case 1: copy_chunk<uint16_t, kNT>(s, sb, db, u0, u_end); break;
-      default: copy_chunk<uint8_t, kNT>(s, sb, db, u0, u_end); break;
+      case 4: copy_chunk<u32x4, kNT, false>(s, sb, db, ab, u0, u_end); break;
+      case 3: copy_chunk<uint64_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
+      case 2: copy_chunk<uint32_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
+      case 1: copy_chunk<uint16_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
+      default: copy_chunk<uint8_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
     }
   }
 }
@@ -272,48 +328,55 @@ struct emrs_plan {
 
 namespace {
 
+// Optional bf16 image of a segment: buffer, offset and row stride in units
+// of half the segment's unit.
+struct Aux {
+  bool on = false;
+  uint32_t buf = 0;
+  uint64_t off = 0, stride = 0;
+};
+
 struct Builder {
   std::vector<DevSeg> out;
   uint64_t chunks = 0;
   uint64_t vec_bytes = 0, scalar_bytes = 0;
 
-  // Emit a segment in units of (1 << ul) bytes; splits to the 32-bit limits.
-  int emit(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint64_t len,
-           uint64_t rows, uint64_t ss, uint64_t ds) {
-    if (len == 0 || rows == 0) return EMRS_OK;
-    if (rows > 1 && ss == len && ds == len) {  // contiguous on both sides
+  // A copy in units of (1 << ul) bytes, optionally with its bf16 image.
+  // Splits to the kernel's 32-bit limits.
+  void emit(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint64_t len,
+            uint64_t rows, uint64_t ss, uint64_t ds, Aux ax = Aux()) {
+    if (len == 0 || rows == 0) return;
+    if (rows > 1 && ss == len && ds == len && (!ax.on || ax.stride == len)) {  // contiguous
       len *= rows;
       rows = 1;
     }
-    const uint64_t bytes = (len * rows) << ul;
-    (ul == 4 ? vec_bytes : scalar_bytes) += bytes;
+    (ul == 4 ? vec_bytes : scalar_bytes) += (len * rows) << ul;
     if (rows == 1) {
       for (uint64_t off = 0; off < len; off += kMaxUnitsPerSeg) {
         const uint64_t n = std::min<uint64_t>(kMaxUnitsPerSeg, len - off);
-        push(sbuf, dbuf, ul, so + off, dof + off, (uint32_t)n, 1, 0, 0);
+        push(sbuf, dbuf, ul, so + off, dof + off, (uint32_t)n, 1, 0, 0, ax, ax.off + off, 0);
       }
-      return EMRS_OK;
+      return;
     }
-    if (len >= kMaxUnitsPerSeg || ss > 0xffffffffull || ds > 0xffffffffull) {
-      for (uint64_t r = 0; r < rows; ++r) {
+    if (len >= kMaxUnitsPerSeg || ss > 0xffffffffull || ds > 0xffffffffull || ax.stride > 0xffffffffull) {
+      for (uint64_t r = 0; r < rows; ++r)
         for (uint64_t off = 0; off < len; off += kMaxUnitsPerSeg) {
           const uint64_t n = std::min<uint64_t>(kMaxUnitsPerSeg, len - off);
-          push(sbuf, dbuf, ul, so + r * ss + off, dof + r * ds + off, (uint32_t)n, 1, 0, 0);
+          push(sbuf, dbuf, ul, so + r * ss + off, dof + r * ds + off, (uint32_t)n, 1, 0, 0, ax,
+               ax.off + r * ax.stride + off, 0);
         }
-      }
-      return EMRS_OK;
+      return;
     }
     const uint64_t rows_per = std::max<uint64_t>(1, kMaxUnitsPerSeg / len);
     for (uint64_t r = 0; r < rows; r += rows_per) {
       const uint64_t n = std::min<uint64_t>(rows_per, rows - r);
-      push(sbuf, dbuf, ul, so + r * ss, dof + r * ds, (uint32_t)len, (uint32_t)n, (uint32_t)ss,
-           (uint32_t)ds);
+      push(sbuf, dbuf, ul, so + r * ss, dof + r * ds, (uint32_t)len, (uint32_t)n, (uint32_t)ss, (uint32_t)ds,
+           ax, ax.off + r * ax.stride, (uint32_t)ax.stride);
     }
-    return EMRS_OK;
   }
 
-  void push(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint32_t len,
-            uint32_t rows, uint32_t ss, uint32_t ds) {
+  void push(uint32_t sbuf, uint32_t dbuf, uint32_t ul, uint64_t so, uint64_t dof, uint32_t len, uint32_t rows,
+            uint32_t ss, uint32_t ds, const Aux &ax, uint64_t aoff, uint32_t astride) {
     DevSeg d{};
     d.src_off = so;
     d.dst_off = dof;
@@ -326,6 +389,10 @@ struct Builder {
     d.unit_log2 = (uint8_t)ul;
     d.src_buf = (uint8_t)sbuf;
     d.dst_buf = (uint8_t)dbuf;
+    d.cast = ax.on ? 1 : 0;
+    d.aux_buf = (uint8_t)(ax.on ? ax.buf : dbuf);
+    d.aux_off = ax.on ? aoff : 0;
+    d.aux_stride = ax.on && rows > 1 ? astride : 0;
     const uint64_t units = (uint64_t)len * rows;
     chunks += (units + kChunkUnits - 1) / kChunkUnits;
     out.push_back(d);
@@ -342,36 +409,36 @@ int log2_of(uint32_t eb) {
   }
 }
 
-// Byte extent end of a strided segment; false on overflow.
-bool extent_end(uint64_t off, uint64_t len, uint64_t rows, uint64_t stride, uint32_t eb,
-                unsigned __int128 *end) {
-  unsigned __int128 e = (unsigned __int128)off + (unsigned __int128)(rows - 1) * stride + len;
-  e *= eb;
-  *end = e;
-  return true;
+// Byte extent end of a strided segment (128-bit: cannot overflow).
+unsigned __int128 extent_end(uint64_t off, uint64_t len, uint64_t rows, uint64_t stride, uint32_t eb) {
+  return ((unsigned __int128)off + (unsigned __int128)(rows - 1) * stride + len) * eb;
 }
 
-int check_disjoint(const std::vector<emrs_segment> &segs, uint32_t n_dst) {
+int check_disjoint(const emrs_segment *segs, uint64_t n_segs) {
   struct Iv {
     uint32_t buf;
     uint64_t b, e;
   };
-  std::vector<Iv> iv;
   uint64_t total_rows = 0;
-  for (const auto &s : segs) total_rows += s.len ? s.rows : 0;
+  for (uint64_t i = 0; i < n_segs; ++i)
+    if (segs[i].len) total_rows += segs[i].rows * ((segs[i].flags & EMRS_SEG_CAST_BF16) ? 2 : 1);
   if (total_rows > (1ull << 27))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "disjointness check: too many rows to check");
+  std::vector<Iv> iv;
   iv.reserve(total_rows);
-  for (const auto &s : segs) {
+  for (uint64_t i = 0; i < n_segs; ++i) {
+    const emrs_segment &s = segs[i];
     if (!s.len) continue;
     for (uint64_t r = 0; r < s.rows; ++r) {
       const uint64_t b = (s.dst_off + r * s.dst_stride) * s.elem_bytes;
       iv.push_back({s.dst_buf, b, b + s.len * s.elem_bytes});
+      if (s.flags & EMRS_SEG_CAST_BF16) {
+        const uint64_t a = (s.aux_off + r * s.aux_stride) * 2;
+        iv.push_back({s.aux_buf, a, a + s.len * 2});
+      }
     }
   }
-  std::sort(iv.begin(), iv.end(), [](const Iv &a, const Iv &b) {
-    return a.buf != b.buf ? a.buf < b.buf : a.b < b.b;
-  });
+  std::sort(iv.begin(), iv.end(), [](const Iv &a, const Iv &b) { return a.buf != b.buf ? a.buf < b.buf : a.b < b.b; });
   for (size_t i = 1; i < iv.size(); ++i) {
     if (iv[i].buf == iv[i - 1].buf && iv[i].b < iv[i - 1].e) {
       char msg[160];
@@ -380,7 +447,6 @@ int check_disjoint(const std::vector<emrs_segment> &segs, uint32_t n_dst) {
       return fail(EMRS_ERR_OVERLAP, msg);
     }
   }
-  (void)n_dst;
   return EMRS_OK;
 }
 
@@ -416,61 +482,77 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
 
   Builder bld;
   bld.out.reserve(n_segs);
-  uint64_t payload = 0;
+  uint64_t payload = 0, read = 0;
   std::vector<uint8_t> src_used(n_src_bufs, 0), dst_used(n_dst_bufs, 0);
   for (uint64_t i = 0; i < n_segs; ++i) {
     const emrs_segment &s = segs[i];
     char where[64];
     snprintf(where, sizeof where, "segment %llu: ", (unsigned long long)i);
+    const std::string at(where);
     const int lg = log2_of(s.elem_bytes);
-    if (lg < 0) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "elem_bytes must be 1, 2, 4 or 8");
-    if (s.flags) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "flags must be 0");
-    if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs)
-      return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "buffer id out of range");
-    if (s.rows == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "rows must be >= 1");
+    const bool cast = (s.flags & EMRS_SEG_CAST_BF16) != 0;
+    if (lg < 0) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "elem_bytes must be 1, 2, 4 or 8");
+    if ((s.flags & ~EMRS_SEG_CAST_BF16) || s.reserved) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "unknown flags");
+    if (cast && s.elem_bytes != 4) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a bf16 cast needs fp32 elements");
+    if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs || (cast && s.aux_buf >= n_dst_bufs))
+      return fail(EMRS_ERR_INVALID_ARGUMENT, at + "buffer id out of range");
+    if (s.rows == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "rows must be >= 1");
     if (s.len == 0) continue;
-    if (s.rows > 1 && s.dst_stride < s.len)
-      return fail(EMRS_ERR_INVALID_ARGUMENT, std::string(where) + "dst_stride < len makes rows overlap");
-    unsigned __int128 se, de;
-    extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes, &se);
-    extent_end(s.dst_off, s.len, s.rows, s.rows > 1 ? s.dst_stride : 0, s.elem_bytes, &de);
-    if (se > src_buf_bytes[s.src_buf])
-      return fail(EMRS_ERR_OUT_OF_BOUNDS, std::string(where) + "source range exceeds its buffer");
-    if (de > dst_buf_bytes[s.dst_buf])
-      return fail(EMRS_ERR_OUT_OF_BOUNDS, std::string(where) + "destination range exceeds its buffer");
-    payload += s.len * s.rows * s.elem_bytes;
+    if (s.rows > 1 && (s.dst_stride < s.len || (cast && s.aux_stride < s.len)))
+      return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a destination stride < len makes rows overlap");
+    if (extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes) > src_buf_bytes[s.src_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "source range exceeds its buffer");
+    if (extent_end(s.dst_off, s.len, s.rows, s.rows > 1 ? s.dst_stride : 0, s.elem_bytes) > dst_buf_bytes[s.dst_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "destination range exceeds its buffer");
+    if (cast && extent_end(s.aux_off, s.len, s.rows, s.rows > 1 ? s.aux_stride : 0, 2) > dst_buf_bytes[s.aux_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "bf16 range exceeds its buffer");
+    read += s.len * s.rows * s.elem_bytes;
+    payload += s.len * s.rows * (s.elem_bytes + (cast ? 2 : 0));
     src_used[s.src_buf] = 1;
     dst_used[s.dst_buf] = 1;
+    if (cast) dst_used[s.aux_buf] = 1;
 
     const uint64_t eb = s.elem_bytes;
     const uint64_t so = s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
     const uint64_t ss = s.rows > 1 ? s.src_stride * eb : 0, ds = s.rows > 1 ? s.dst_stride * eb : 0;
-    const bool rows1 = s.rows == 1 || (ss == lb && ds == lb);
+    const uint64_t ao = cast ? s.aux_off * 2 : 0, as = cast && s.rows > 1 ? s.aux_stride * 2 : 0;
+    Aux ax;
+    ax.on = cast;
+    ax.buf = s.aux_buf;
+    // The bf16 image of a 16-byte unit is 8 bytes: the vector path needs it 8-byte aligned.
+    const bool aux_vec_ok = !cast || (ao % 8 == 0 && as % 8 == 0);
+    const bool rows1 = s.rows == 1 || (ss == lb && ds == lb && (!cast || as == s.len * 2));
     if (rows1) {
       const uint64_t L = lb * s.rows;  // contiguous bytes
-      if (so % 16 == 0 && dof % 16 == 0 && L % 16 == 0) {
-        bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, L / 16, 1, 0, 0);
-      } else if (so % 16 == dof % 16) {
+      if (so % 16 == 0 && dof % 16 == 0 && L % 16 == 0 && aux_vec_ok) {
+        ax.off = ao / 8;
+        bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, L / 16, 1, 0, 0, ax);
+      } else if (so % 16 == dof % 16 && (!cast || (ao % 8) * 2 == so % 16)) {
         const uint64_t head = std::min<uint64_t>((16 - so % 16) % 16, L);
         const uint64_t body = (L - head) / 16 * 16;
         const uint64_t tail = L - head - body;
-        bld.emit(s.src_buf, s.dst_buf, lg, so / eb, dof / eb, head / eb, 1, 0, 0);
-        bld.emit(s.src_buf, s.dst_buf, 4, (so + head) / 16, (dof + head) / 16, body / 16, 1, 0, 0);
-        bld.emit(s.src_buf, s.dst_buf, lg, (so + head + body) / eb, (dof + head + body) / eb,
-                 tail / eb, 1, 0, 0);
+        ax.off = ao / 2;
+        bld.emit(s.src_buf, s.dst_buf, lg, so / eb, dof / eb, head / eb, 1, 0, 0, ax);
+        ax.off = (ao + head / 2) / 8;
+        bld.emit(s.src_buf, s.dst_buf, 4, (so + head) / 16, (dof + head) / 16, body / 16, 1, 0, 0, ax);
+        ax.off = (ao + (head + body) / 2) / 2;
+        bld.emit(s.src_buf, s.dst_buf, lg, (so + head + body) / eb, (dof + head + body) / eb, tail / eb, 1, 0, 0, ax);
       } else {
-        bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, L / eb, 1, 0, 0);
+        ax.off = s.aux_off;
+        bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, L / eb, 1, 0, 0, ax);
       }
-    } else if (so % 16 == 0 && dof % 16 == 0 && lb % 16 == 0 && ss % 16 == 0 && ds % 16 == 0) {
-      bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, lb / 16, s.rows, ss / 16, ds / 16);
+    } else if (so % 16 == 0 && dof % 16 == 0 && lb % 16 == 0 && ss % 16 == 0 && ds % 16 == 0 && aux_vec_ok) {
+      ax.off = ao / 8;
+      ax.stride = as / 8;
+      bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, lb / 16, s.rows, ss / 16, ds / 16, ax);
     } else {
-      bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, s.len, s.rows, s.src_stride,
-               s.dst_stride);
+      ax.off = s.aux_off;
+      ax.stride = s.rows > 1 ? s.aux_stride : 0;
+      bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, s.len, s.rows, s.src_stride, s.dst_stride, ax);
     }
   }
   if (flags & EMRS_PLAN_CHECK_DISJOINT) {
-    std::vector<emrs_segment> v(segs, segs + n_segs);
-    int rc = check_disjoint(v, n_dst_bufs);
+    int rc = check_disjoint(segs, n_segs);
     if (rc) return rc;
   }
 
@@ -485,6 +567,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   p->stats.n_segments = n_segs;
   p->stats.n_device_segments = p->segs.size();
   p->stats.payload_bytes = payload;
+  p->stats.read_bytes = read;
   p->stats.vector_bytes = bld.vec_bytes;
   p->stats.scalar_bytes = bld.scalar_bytes;
   p->stats.n_chunks = bld.chunks;

@@ -8,7 +8,9 @@ elastic_megatron/elastic_manager.py:158-178).  On one device every hop is a
 local copy, so the figure is derived from the plan: the DP gather onto the
 aligned rank of every source TP rank (transfer.py:143-180), the exchange
 between aligned ranks (transfer.py:182-228) and the DP scatter from the
-aligned destination rank (transfer.py:230-269).
+aligned destination rank (transfer.py:230-269), plus, for tied embeddings at
+destination PP > 1, the broadcast of the word embedding's state to the
+output layer over the embedding group (transfer.py:103-141).
 """
 
 from __future__ import annotations
@@ -27,9 +29,16 @@ def reference_comm_bytes(space, src: ParallelStrategy, dst: ParallelStrategy) ->
     per_rank: Dict[int, int] = defaultdict(int)
     for vp in space.all_virtual_params:
         plan = vp.reshard_plan
-        if plan is None or plan.global_send_info is None:
-            continue
         if vp.shared_embedding and vp.param_position_attr.layer_type.value == "output_layer":
+            if dst.pipeline_model_parallel_size > 1:
+                stage = vp.get_model_param_stage_id(dst.pipeline_model_parallel_size)
+                for t in range(vp.tp_size_at(dst)):
+                    for r, rng in vp.get_dp_distribution(dst).items():
+                        n = rng.size * FP32_TENSORS_BYTES
+                        per_rank[global_rank_of(dst, 0, r, None, t)] += n      # first stage sends
+                        per_rank[global_rank_of(dst, stage, r, None, t)] += n  # last stage receives
+            continue
+        if plan is None or plan.global_send_info is None:
             continue
         dpi = plan.data_parallel_resharding_info
         ts, td = vp.tp_size_at(src), vp.tp_size_at(dst)

@@ -46,14 +46,16 @@ SEGMENT_DTYPE = np.dtype([
     ("src_buf", "<u4"), ("dst_buf", "<u4"), ("elem_bytes", "<u4"), ("flags", "<u4"),
     ("src_off", "<u8"), ("dst_off", "<u8"), ("len", "<u8"), ("rows", "<u8"),
     ("src_stride", "<u8"), ("dst_stride", "<u8"),
+    ("aux_buf", "<u4"), ("reserved", "<u4"), ("aux_off", "<u8"), ("aux_stride", "<u8"),
 ])
+SEG_CAST_BF16 = 1
 PIECE_DTYPE = np.dtype([
     ("buf", "<u4"), ("param_id", "<u4"), ("kind", "<u4"), ("reserved", "<u4"),
     ("buf_off", "<u8"), ("len", "<u8"), ("local_start", "<u8"), ("local_cols", "<u8"),
     ("full_cols", "<u8"), ("band_rows", "<u8"), ("row_off", "<u8"), ("row_off2", "<u8"),
     ("col_off", "<u8"),
 ])
-assert SEGMENT_DTYPE.itemsize == 64 and PIECE_DTYPE.itemsize == 88
+assert SEGMENT_DTYPE.itemsize == 88 and PIECE_DTYPE.itemsize == 88
 
 
 def _align(n: int, a: int) -> int:
@@ -269,19 +271,24 @@ class StrategyLayout:
 
     # ----- synthetic-data descriptors -----
     def pieces(self, params=None, include_bf16: bool = True, include_fp32: bool = True) -> np.ndarray:
-        """emrs_piece records covering every stored element of ``params``."""
+        """emrs_piece records covering every stored element of ``params``.
+
+        A tied output layer is described with the word embedding's id: it
+        holds the same values.
+        """
         rows = []
         vps = params if params is not None else [self.space.all_virtual_params[g] for g in sorted(self.place)]
         for vp in vps:
+            vid = self.space.value_source(vp).global_index
             if include_fp32:
                 for h in self.fp32_holders(vp):
                     geo = self.geometry(vp, h.tp_rank)
                     for kind in (1, 2, 3):
-                        rows.append(_piece_row(kind - 1, vp.global_index, kind, h, geo))
+                        rows.append(_piece_row(kind - 1, vid, kind, h, geo))
             if include_bf16:
                 for h in self.bf16_holders(vp):
                     geo = self.geometry(vp, h.tp_rank)
-                    rows.append(_piece_row(ARENA_PARAM, vp.global_index, 0, h, geo))
+                    rows.append(_piece_row(ARENA_PARAM, vid, 0, h, geo))
         arr = np.zeros(len(rows), dtype=PIECE_DTYPE)
         if rows:
             arr[:] = rows

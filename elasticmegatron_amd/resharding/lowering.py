@@ -34,11 +34,11 @@ training_state.py:40-60).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterable, List, Sequence, Tuple
+from typing import Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from .layout import (ARENA_PARAM, Geometry, Holder, SEGMENT_DTYPE, StrategyLayout)
+from .layout import ARENA_PARAM, SEG_CAST_BF16, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout
 
 
 @dataclass(frozen=True)
@@ -104,19 +104,24 @@ def _intersections(src: Sequence[Rect], dst: Sequence[Rect]) -> Iterable[Tuple[i
 
 
 class SegmentBuilder:
+    """Accumulates segment rows, merging a contiguous continuation into the previous row."""
+
     def __init__(self):
         self.rows: List[Tuple] = []
 
-    def add(self, sbuf: int, dbuf: int, eb: int, so: int, do: int, n: int, rows: int, ss: int, ds: int) -> None:
+    def add(self, sbuf: int, dbuf: int, eb: int, so: int, do: int, n: int, rows: int, ss: int, ds: int,
+            aux: Optional[Tuple[int, int, int]] = None) -> None:
         if n <= 0 or rows <= 0:
             return
+        flags, abuf, aoff, astr = (SEG_CAST_BF16, aux[0], aux[1], aux[2]) if aux else (0, 0, 0, 0)
         if self.rows and rows == 1:
             p = self.rows[-1]
-            if (p[0] == sbuf and p[1] == dbuf and p[2] == eb and p[7] == 1
-                    and p[4] + p[6] == so and p[5] + p[6] == do):
-                self.rows[-1] = (p[0], p[1], p[2], 0, p[4], p[5], p[6] + n, 1, 0, 0)
+            if (p[0] == sbuf and p[1] == dbuf and p[2] == eb and p[3] == flags and p[7] == 1
+                    and p[4] + p[6] == so and p[5] + p[6] == do
+                    and (not flags or (p[10] == abuf and p[12] + p[6] == aoff))):
+                self.rows[-1] = p[:6] + (p[6] + n,) + p[7:]
                 return
-        self.rows.append((sbuf, dbuf, eb, 0, so, do, n, rows, ss, ds))
+        self.rows.append((sbuf, dbuf, eb, flags, so, do, n, rows, ss, ds, abuf, 0, aoff, astr if rows > 1 else 0))
 
     def table(self) -> np.ndarray:
         arr = np.zeros(len(self.rows), dtype=SEGMENT_DTYPE)
@@ -133,35 +138,59 @@ def _src_replica(vp, holders: List[Holder]) -> List[Holder]:
 
 
 def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool = True,
-                   include_bf16: bool = True) -> np.ndarray:
+                   include_bf16: bool = True, bf16_source: str = "cast") -> np.ndarray:
     """Segments of a switch between two layouts of the same model.
 
     Buffers 0..2 are the fp32 arenas (main, exp_avg, exp_avg_sq) and buffer 3
-    the bf16 param arena, on both sides.
+    the bf16 param arena, on both sides.  ``bf16_source``:
+
+    * ``"cast"`` (default): the destination bf16 params are the bf16 rounding
+      of the destination main weights, written by the main segments as they
+      copy (the reference's ``_copy_main_params_to_model_params`` + DP
+      all-gather, training_state.py:176-197).  26 bytes of HBM traffic per
+      parameter.
+    * ``"copy"``: the bf16 params are copied from the source bf16 shards.
+      28 bytes per parameter; equal bits when main = upcast(param).
     """
+    if bf16_source not in ("cast", "copy"):
+        raise ValueError(bf16_source)
+    cast = include_bf16 and bf16_source == "cast"
+    if cast and not include_fp32:
+        raise ValueError("the bf16 cast rides on the fp32 main segments")
     space = src.space
     assert dst.space is space
     fp32 = SegmentBuilder()
     bf16 = SegmentBuilder()
     for vp in space.all_virtual_params:
-        if not (src.has_param(vp) and dst.has_param(vp)):
-            continue  # tied output layer at PP 1 (transfer.py:324-330)
+        # A tied output layer is filled from the source word embedding: the
+        # reference broadcasts the new embedding state to it (transfer.py:103-141).
+        sv = space.value_source(vp)
+        if not (src.has_param(sv) and dst.has_param(vp)):
+            continue  # tied output layer at destination PP 1 (transfer.py:324-330)
         if include_fp32:
-            s_rects = [r for h in _src_replica(vp, src.fp32_holders(vp))
-                       for r in holder_rects(h, src.geometry(vp, h.tp_rank))]
+            bf16_base = {h.tp_rank: h.offset for h in dst.bf16_holders(vp)} if cast else {}
+            s_rects = [r for h in _src_replica(sv, src.fp32_holders(sv))
+                       for r in holder_rects(h, src.geometry(sv, h.tp_rank))]
             covered = 0
             want = 0
             for h in dst.fp32_holders(vp):
                 want += h.hi - h.lo
                 d_rects = holder_rects(h, dst.geometry(vp, h.tp_rank))
                 for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
-                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds)
+                    aux = None
+                    if cast and h.instance == 0:
+                        aux = (ARENA_PARAM, bf16_base[h.tp_rank] + do - h.offset + h.lo, ds)
+                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds, aux)
                     covered += n * rows
             if covered != want:
                 raise AssertionError(f"{vp.name}: fp32 plan covers {covered} of {want} elements")
-        if include_bf16:
-            s_rects = [r for h in _src_replica(vp, src.bf16_holders(vp))
-                       for r in holder_rects(h, src.geometry(vp, h.tp_rank))]
+            if cast:
+                main_once = sum(h.hi - h.lo for h in dst.fp32_holders(vp) if h.instance == 0)
+                if main_once != sum(h.hi - h.lo for h in dst.bf16_holders(vp)):
+                    raise AssertionError(f"{vp.name}: bf16 cast would not cover every param element once")
+        if include_bf16 and not cast:
+            s_rects = [r for h in _src_replica(sv, src.bf16_holders(sv))
+                       for r in holder_rects(h, src.geometry(sv, h.tp_rank))]
             covered = 0
             want = 0
             for h in dst.bf16_holders(vp):
@@ -194,16 +223,69 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     return _assemble(b.table(), np.zeros(0, dtype=SEGMENT_DTYPE))
 
 
+# Elements per interleaved piece: 1 MiB of fp32.
+INTERLEAVE_ELEMS = 1 << 18
+
+
+def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
+    """Cut segments into pieces of at most ``max_elems`` elements (whole rows for strided ones)."""
+    out = []
+    for s in table:
+        n, rows = int(s["len"]), int(s["rows"])
+        if n * rows <= max_elems:
+            out.append(s)
+            continue
+        if rows == 1:
+            for o in range(0, n, max_elems):
+                p = s.copy()
+                p["src_off"] += o
+                p["dst_off"] += o
+                p["aux_off"] += o if s["flags"] else 0
+                p["len"] = min(max_elems, n - o)
+                out.append(p)
+            continue
+        step = max(1, max_elems // n)
+        for r in range(0, rows, step):
+            p = s.copy()
+            p["src_off"] += r * int(s["src_stride"])
+            p["dst_off"] += r * int(s["dst_stride"])
+            p["aux_off"] += r * int(s["aux_stride"]) if s["flags"] else 0
+            p["rows"] = min(step, rows - r)
+            out.append(p)
+    return np.array(out, dtype=SEGMENT_DTYPE) if out else np.zeros(0, dtype=SEGMENT_DTYPE)
+
+
 def _assemble(fp32: np.ndarray, bf16: np.ndarray) -> np.ndarray:
-    parts = []
+    """Replicate the fp32 segments over the three optimizer kinds; only main carries the bf16 cast.
+
+    The kinds are interleaved in pieces of about 1 MiB: the kernel hands
+    every workgroup an equal run of chunks, and a main chunk that also writes
+    the bf16 cast costs more than the others, so every run must hold the same
+    mix of kinds.
+    """
+    base = _split(fp32, INTERLEAVE_ELEMS)
+    out = np.zeros(3 * len(base), dtype=SEGMENT_DTYPE)
     for k in range(3):
-        t = fp32.copy()
+        t = out[k::3]
+        t[...] = base
         t["src_buf"] = k
         t["dst_buf"] = k
-        parts.append(t)
-    parts.append(bf16)
-    return np.concatenate(parts)
+        if k:
+            for f in ("flags", "aux_buf", "aux_off", "aux_stride"):
+                t[f] = 0
+    return np.concatenate([out, bf16])
+
+
+def _units(table: np.ndarray) -> np.ndarray:
+    return table["len"].astype(np.uint64) * table["rows"].astype(np.uint64)
 
 
 def payload_bytes(table: np.ndarray) -> int:
-    return int(np.sum(table["len"].astype(np.uint64) * table["rows"] * table["elem_bytes"]))
+    """Bytes written per execution (bf16 casts included)."""
+    cast = (table["flags"] & SEG_CAST_BF16) != 0
+    return int(np.sum(_units(table) * (table["elem_bytes"].astype(np.uint64) + 2 * cast.astype(np.uint64))))
+
+
+def read_bytes(table: np.ndarray) -> int:
+    """Bytes read per execution."""
+    return int(np.sum(_units(table) * table["elem_bytes"].astype(np.uint64)))

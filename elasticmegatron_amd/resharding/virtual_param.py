@@ -138,6 +138,21 @@ class VirtualParamSpace:
         self._built: set = set()
         self._layouts: Dict[ParallelStrategy, "object"] = {}
 
+    @property
+    def tied_embeddings(self) -> bool:
+        return not self.spec.untie_embeddings_and_output_weights
+
+    def value_source(self, vp: VirtualParam) -> VirtualParam:
+        """The parameter whose values ``vp`` carries.
+
+        A tied output layer carries the word embedding: the reference skips it
+        in the transfer and then broadcasts the new word-embedding state to it
+        over the embedding group (transfer.py:103-141, :324-330).
+        """
+        if self.tied_embeddings and vp.param_position_attr.layer_type == LayerType.OUTPUT_LAYER:
+            return self.embedding_layer_virtual_params[0]
+        return vp
+
     def stages(self, pp_size: int) -> List[List[VirtualParam]]:
         """virtual_param.py:295-316."""
         st = self._stages.get(pp_size)

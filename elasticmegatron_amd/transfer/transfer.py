@@ -24,7 +24,7 @@ from .. import _native
 from ..megatron_manager.parallel_strategy import ParallelStrategy
 from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
-from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes
+from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import StrategyLayout
 
 
@@ -32,18 +32,25 @@ from ..resharding.layout import StrategyLayout
 class CompiledPlan:
     segments: np.ndarray
     native: _native.Plan
-    payload_bytes: int
+    payload_bytes: int              # bytes of state written to the destination per execution
+    read_bytes: int                 # bytes read per execution
     src: ParallelStrategy
     dst: ParallelStrategy
     reference_comm_bytes: int = 0   # the reference's per-rank cross-rank volume, max over ranks
+
+    @property
+    def traffic_bytes(self) -> int:
+        """Algorithmic HBM traffic per execution: every byte read once and written once."""
+        return self.payload_bytes + self.read_bytes
 
 
 class TransferManager:
     """Builds, caches and runs copy plans between device-resident training states."""
 
-    def __init__(self, check_disjoint: bool = False):
+    def __init__(self, check_disjoint: bool = False, bf16_source: str = "cast"):
         self._plans: Dict[Tuple, CompiledPlan] = {}
         self.check_disjoint = check_disjoint
+        self.bf16_source = bf16_source
         self.fake_transfer = False
         self._payload_bytes = 0
         self._comm_bytes = 0
@@ -54,12 +61,12 @@ class TransferManager:
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                 include_bf16: bool = True) -> CompiledPlan:
-        key = (src.strategy, dst.strategy, kind, include_bf16)
+        key = (src.strategy, dst.strategy, kind, include_bf16, self.bf16_source)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
         if kind == "transfer":
-            table = lower_transfer(src, dst, include_bf16=include_bf16)
+            table = lower_transfer(src, dst, include_bf16=include_bf16, bf16_source=self.bf16_source)
         elif kind in ("backup_up", "backup_down"):
             table = lower_redundant_backup(src, dst, scale_up=kind == "backup_up")
         else:
@@ -73,7 +80,7 @@ class TransferManager:
         else:  # param_migrate is a local copy (training_state.py:40-60)
             comm = 0
         cp = CompiledPlan(table, _native.Plan(table, sb, db, self.check_disjoint), payload_bytes(table),
-                          src.strategy, dst.strategy, comm)
+                          read_bytes(table), src.strategy, dst.strategy, comm)
         self._plans[key] = cp
         return cp
 
@@ -85,6 +92,8 @@ class TransferManager:
             raise ValueError("training states do not match the plan's strategies")
         if src.device != dst.device:
             raise ValueError("source and destination states must be on the same device")
+        if src.device.type != "cuda":
+            raise RuntimeError("training states must live in GPU memory: the reshard has no CPU path")
         st = stream if stream is not None else torch.cuda.current_stream(src.device)
         with torch.cuda.device(src.device):
             plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)
@@ -94,11 +103,12 @@ class TransferManager:
     def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
                                    dst: Optional[TrainingState] = None, include_bf16: bool = True,
                                    stream=None) -> CompiledPlan:
-        """Move fp32 optimizer state and bf16 params from ``src`` to ``dst`` (transfer.py:291-341).
+        """Move fp32 optimizer state from ``src`` to ``dst`` and rebuild the bf16 params (transfer.py:291-341).
 
-        The bf16 params are copied directly: with main = upcast(param) the
-        reference's cast of the new main shards back to bf16 plus DP
-        all-gather (training_state.py:176-197) yields the same bits.
+        By default the destination bf16 params are the bf16 rounding of the
+        destination main weights, written in the same pass (the reference's
+        cast plus DP all-gather, training_state.py:176-197); with
+        ``bf16_source="copy"`` they are copied from the source bf16 shards.
         """
         src = src if src is not None else virtual_param_space.src_state
         dst = dst if dst is not None else virtual_param_space.dst_state

@@ -64,18 +64,31 @@ extern "C" {
 /* emrs_plan_create flags */
 #define EMRS_PLAN_CHECK_DISJOINT 1u /* reject plans whose destination ranges overlap */
 
+/* emrs_segment flags */
+#define EMRS_SEG_CAST_BF16 1u /* fp32 segment that also writes its values as bf16 to aux */
+
 /* One strided copy.  Units: elements of elem_bytes bytes. */
 typedef struct emrs_segment {
   uint32_t src_buf;    /* index into the src_bases passed at execution */
   uint32_t dst_buf;    /* index into the dst_bases passed at execution */
   uint32_t elem_bytes; /* 1, 2, 4 or 8 */
-  uint32_t flags;      /* must be 0 */
+  uint32_t flags;      /* 0 or EMRS_SEG_CAST_BF16 */
   uint64_t src_off;    /* first element of row 0 in the source buffer */
   uint64_t dst_off;    /* first element of row 0 in the destination buffer */
   uint64_t len;        /* elements per row */
   uint64_t rows;       /* number of rows (>= 1) */
   uint64_t src_stride; /* elements between source row starts (rows > 1) */
   uint64_t dst_stride; /* elements between destination row starts (rows > 1), >= len */
+  /* EMRS_SEG_CAST_BF16 (elem_bytes 4 only): every copied fp32 value is also
+   * written, rounded to bf16 to nearest-even (NaN -> 0x7FC0, the rounding of
+   * torch's float -> bfloat16 conversion), at bf16 element
+   * aux_off + r*aux_stride + i of destination buffer aux_buf.  This is
+   * Megatron's copy of main params into the bf16 model params
+   * (training_state.py:176-197) fused into the reshard. */
+  uint32_t aux_buf;
+  uint32_t reserved;   /* must be 0 */
+  uint64_t aux_off;
+  uint64_t aux_stride; /* bf16 elements between aux row starts (rows > 1), >= len */
 } emrs_segment;
 
 typedef struct emrs_plan emrs_plan;
@@ -83,9 +96,10 @@ typedef struct emrs_plan emrs_plan;
 typedef struct emrs_plan_stats {
   uint64_t n_segments;      /* segments as given */
   uint64_t n_device_segments; /* after alignment splitting */
-  uint64_t payload_bytes;   /* bytes copied per execution (read once, written once) */
-  uint64_t vector_bytes;    /* part of payload moved with 16-byte accesses */
-  uint64_t scalar_bytes;    /* part of payload moved element by element */
+  uint64_t payload_bytes;   /* bytes written per execution, bf16 casts included */
+  uint64_t read_bytes;      /* bytes read per execution */
+  uint64_t vector_bytes;    /* bytes read with 16-byte accesses */
+  uint64_t scalar_bytes;    /* bytes read element by element */
   uint64_t n_chunks;        /* work chunks per execution */
   uint32_t n_src_bufs;
   uint32_t n_dst_bufs;
@@ -105,9 +119,10 @@ int emrs_device_count(void);
  * here (the table is uploaded on first execution).
  *   src_buf_bytes[i]: capacity in bytes of source buffer i (bounds check)
  *   dst_buf_bytes[i]: capacity in bytes of destination buffer i
- * Errors: INVALID_ARGUMENT (bad elem_bytes, rows == 0, dst_stride < len,
- * unknown buffer id, nonzero flags), OUT_OF_BOUNDS (a row leaves its
- * buffer), TOO_MANY_BUFFERS, OVERLAP (with EMRS_PLAN_CHECK_DISJOINT).
+ * Errors: INVALID_ARGUMENT (bad elem_bytes, rows == 0, dst_stride or
+ * aux_stride < len, unknown buffer id, unknown flags, a cast on a non-fp32
+ * segment), OUT_OF_BOUNDS (a row leaves its buffer), TOO_MANY_BUFFERS,
+ * OVERLAP (with EMRS_PLAN_CHECK_DISJOINT; aux writes included).
  */
 int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs,
                      const uint64_t *src_buf_bytes, uint32_t n_src_bufs,

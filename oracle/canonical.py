@@ -34,10 +34,15 @@ def full_index(p, T, t, local_idx):
     return r * C + t * cl + c
 
 
+def value_id(p):
+    """Generator stream of a parameter: a tied output layer carries the word embedding (id 0)."""
+    return 0 if (p["shared"] and p["where"] == "out") else p["id"]
+
+
 def piece_values(seed, p, T, t, lo, hi):
     """{kind: array} for local elements [lo, hi) of TP rank t at TP size T."""
     f = full_index(p, T, t, np.arange(lo, hi))
-    return {k: synth.values(seed, p["id"], k, f) for k in ("main", "exp_avg", "exp_avg_sq")}
+    return {k: synth.values(seed, value_id(p), k, f) for k in ("main", "exp_avg", "exp_avg_sq")}
 
 
 def shard_key(p, strat, hp, t):
@@ -69,5 +74,5 @@ def world(inv, hp, strat, seed, params=None):
                     fp32[(g, p["id"])] = piece_values(seed, p, T, t, lo, hi)
             n = int(np.prod(local_shape(p, T)))
             bf16[(shard_key(p, strat, hp, t), p["id"])] = synth.values(
-                seed, p["id"], "param", full_index(p, T, t, np.arange(n)))
+                seed, value_id(p), "param", full_index(p, T, t, np.arange(n)))
     return fp32, bf16

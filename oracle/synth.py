@@ -54,8 +54,45 @@ def bf16_round(bits: np.ndarray) -> np.ndarray:
     return ((b + 0x7FFF + ((b >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)).astype(np.uint16)
 
 
+_KIND_CODE = {"param": 0, "main": 1, "exp_avg": 2, "exp_avg_sq": 3}
+_clib = None
+
+
+def _c_library():
+    """oracle/build/libsynth_ref.so (oracle/Makefile) when it has been built, else None."""
+    global _clib
+    if _clib is None:
+        import ctypes
+        import os
+
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "build", "libsynth_ref.so")
+        if not os.path.exists(path):
+            _clib = False
+            return None
+        lib = ctypes.CDLL(path)
+        lib.oracle_synth.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                     ctypes.c_uint64, ctypes.c_void_p]
+        _clib = lib
+    return _clib or None
+
+
 def values(seed: int, param_id: int, kind: str, idx: np.ndarray) -> np.ndarray:
-    """kind in {param, main, exp_avg, exp_avg_sq}: bf16 returned as uint16 bits, fp32 as float32."""
+    """kind in {param, main, exp_avg, exp_avg_sq}: bf16 returned as uint16 bits, fp32 as float32.
+
+    Uses the C restatement when it is built (same definition, much faster);
+    tests/test_synth.py checks that the two agree bit for bit.
+    """
+    lib = _c_library()
+    if lib is not None:
+        i = np.ascontiguousarray(idx, dtype=np.uint64)
+        out = np.empty(i.size, dtype=np.uint32)
+        lib.oracle_synth(seed & M64, param_id, _KIND_CODE[kind], i.ctypes.data, i.size, out.ctypes.data)
+        return out.astype(np.uint16) if kind == "param" else out.view(np.float32)
+    return values_numpy(seed, param_id, kind, idx)
+
+
+def values_numpy(seed: int, param_id: int, kind: str, idx: np.ndarray) -> np.ndarray:
+    """The numpy restatement (see ``values``)."""
     if kind in ("param", "main"):
         bf = bf16_round(f32_bits(seed, param_id, 0, idx))
         if kind == "param":

@@ -230,7 +230,36 @@ def transfer(inv, hp, src, dst, src_world, params=None):
             elif g == aligned:
                 info.release_padded()
     assert mb.empty(), "unmatched messages"
+    tie_output_layer(inv, hp, dst, dd, dst_world, tp_of_dst, mb, params)
     return dst_world, rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst), mb
+
+
+def tie_output_layer(inv, hp, dst, dd, dst_world, tp_of_dst, mb, params=None):
+    """Broadcast the word embedding's new state to a tied output layer (transfer.py:103-141).
+
+    Only with tied embeddings and destination PP > 1: in every embedding
+    group (first- and last-stage ranks of one (dp, tp) position) the
+    first-stage rank broadcasts its three optimizer tensors.
+    """
+    out = [p for p in inv if p["shared"] and p["where"] == "out"]
+    if not out or dst.pp == 1:
+        return
+    p_out, p_emb = out[0], inv[0]
+    if (params is not None and p_out["id"] not in params) or p_out["id"] not in dd:
+        return
+    infos = {}
+    for g, t, (lo, hi) in holders(inv, hp, dst, p_out, dd[p_out["id"]]):
+        r = next(r for r, v in dd[p_out["id"]].items() if v == (lo, hi))
+        g0 = global_rank(dst, 0, r, None, t)
+        src_info = dst_world[p_emb["id"]][g0]
+        assert src_info.rng == (lo, hi), "tied parameters must share their DP distribution"
+        info = OptInfo([torch.empty_like(x) for x in src_info.tensors], (lo, hi), src_info.model_shape)
+        for a, b in zip(src_info.tensors, info.tensors):
+            mb.send(g0, g, a)
+            mb.recv(g0, g, b)
+        infos[g] = info
+    dst_world[p_out["id"]] = infos
+    tp_of_dst[p_out["id"]] = {g: t for g, t, _ in holders(inv, hp, dst, p_out, dd[p_out["id"]])}
 
 
 def rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst):
@@ -238,7 +267,6 @@ def rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst):
     out = {}
     for pid, infos in dst_world.items():
         p = inv[pid]
-        plan = plans[pid]
         for g, info in infos.items():
             t = tp_of_dst[pid][g]
             key = (shard_key(p, dst, hp, t), pid)

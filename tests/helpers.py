@@ -72,18 +72,29 @@ def new_arenas(layout, fill=0xFFFFFFFF):
     return f32 + [np.full(layout.bf16_numel, fill & 0xFFFF, dtype=np.uint16)]
 
 
+def bf16_rne_bits(u32):
+    """fp32 bits -> bf16 bits, nearest-even; NaN -> 0x7FC0 (torch's float -> bfloat16 rounding)."""
+    u = u32.astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)).astype(np.uint16)
+    return np.where((u32 & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000), np.uint16(0x7FC0), r)
+
+
+def _view(arr, off, rows, n, stride):
+    if rows == 1:
+        return arr[off:off + n]
+    return np.lib.stride_tricks.as_strided(arr[off:], shape=(rows, n), strides=(stride * arr.itemsize, arr.itemsize))
+
+
 def execute_numpy(table, src, dst):
-    """Reference semantics of emrs_plan_execute on numpy arenas."""
+    """Reference semantics of emrs_plan_execute on numpy arenas (fp32 arenas as uint32 bits)."""
     for s in table:
         a, b = src[int(s["src_buf"])], dst[int(s["dst_buf"])]
         so, do, n, rows = int(s["src_off"]), int(s["dst_off"]), int(s["len"]), int(s["rows"])
-        if rows == 1:
-            b[do:do + n] = a[so:so + n]
-            continue
-        ss, ds = int(s["src_stride"]), int(s["dst_stride"])
-        sv = np.lib.stride_tricks.as_strided(a[so:], shape=(rows, n), strides=(ss * a.itemsize, a.itemsize))
-        dv = np.lib.stride_tricks.as_strided(b[do:], shape=(rows, n), strides=(ds * b.itemsize, b.itemsize))
-        dv[...] = sv
+        vals = _view(a, so, rows, n, int(s["src_stride"])).copy()
+        _view(b, do, rows, n, int(s["dst_stride"]))[...] = vals
+        if int(s["flags"]) & 1:
+            aux = dst[int(s["aux_buf"])]
+            _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"]))[...] = bf16_rne_bits(vals)
 
 
 def extract(layout, arenas, params=None):
@@ -126,3 +137,13 @@ def compare(got32, gotbf, want32, wantbf):
 
 def strat(ps):
     return Strat.of(ps)
+
+
+def small_llama2_tied():
+    return ms.ModelSpec(name="small-llama2-tied", num_layers=4, hidden_size=256, num_attention_heads=4,
+                        ffn_hidden_size=688, padded_vocab_size=1024, ddp_bucket_size=150_000,
+                        overlap_grad_reduce=True, untie_embeddings_and_output_weights=False)
+
+
+SMALL_CASES.append(("llama2_tied_pp1_pp2_pp4_tp2pp1",
+                    small_llama2_tied, [PS(8, 1, 1), PS(8, 1, 2), PS(8, 2, 4), PS(8, 2, 1)]))

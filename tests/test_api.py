@@ -1,0 +1,71 @@
+"""The public API mirrors the reference's (elastic_manager.py:30-265) and fails loudly without a GPU."""
+
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy, TrainingState, tiny_llama2
+from elasticmegatron_amd import _native
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+
+SEQ = [dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1),
+       dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+       dict(world_size=8, tensor_model_parallel_size=4, pipeline_model_parallel_size=1)]
+
+
+def test_meta_device_reshard_plans_without_touching_memory():
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
+    state = mgr.training_state
+    assert mgr.reshard(SEQ[1], is_meta_device=True) is None
+    assert mgr.training_state is state  # nothing switched
+    # The plan is cached for the real switch.
+    assert len(mgr.transfer_manager._plans) == 1
+    plan = next(iter(mgr.transfer_manager._plans.values()))
+    assert plan.payload_bytes == 14 * tiny_llama2().num_params()
+    with pytest.raises(AssertionError):
+        mgr.reshard(SEQ[1], is_meta_device=True, save_ckpt=True)
+    with pytest.raises(NotImplementedError):
+        mgr.reshard(SEQ[1], save_ckpt=True)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a GPU")
+def test_reshard_without_gpu_raises():
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        mgr.reshard(SEQ[1])
+    # The C ABI itself refuses to run without a device.
+    plan = next(iter(mgr.transfer_manager._plans.values()))
+    src = mgr.training_state
+    dst = TrainingState.allocate(mgr.virtual_param_space.layout(ParallelStrategy(**SEQ[1])), "cpu")
+    with pytest.raises(_native.EmrsError) as e:
+        plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), 0)
+    assert e.value.code == -6  # EMRS_ERR_NO_DEVICE
+
+
+def test_training_state_views():
+    spec = tiny_llama2()
+    space = build_virtual_model(spec)
+    lay = space.layout(ParallelStrategy(8, 2, 1))
+    st = TrainingState.allocate(lay, "cpu")
+    vp = space.all_virtual_params[3]  # layer 0 linear_qkv.weight, TP dim 0
+    shapes = []
+    for g in range(8):
+        info = st.optimizer_tensor_info(vp, g)
+        if info is not None:
+            assert info.main_weight.numel() == info.optimizer_tensor_range_in_model_param.size
+            assert info.model_param_shape == (768, 512)
+            shapes.append(info.main_weight.numel())
+    assert sum(shapes) == 2 * 768 * 512  # two TP ranks, each split over its DP ranks
+    assert st.model_param(vp, 1).shape == (768, 512)
+
+
+def test_strategy_list_and_redundant_backup_dispatch():
+    spec = tiny_llama2()
+    mgr = ElasticMegatronManager([dict(world_size=6, tensor_model_parallel_size=1, pipeline_model_parallel_size=1)],
+                                 spec, device="cpu")
+    assert mgr.reshard(dict(world_size=12, tensor_model_parallel_size=1, pipeline_model_parallel_size=1,
+                            num_distributed_optimizer_instances=2), is_meta_device=True) is None
+    (key, plan), = mgr.transfer_manager._plans.items()
+    assert key[2] == "backup_up" and plan.payload_bytes == 24 * spec.num_params()
+    with pytest.raises(ValueError):  # the reference rejects a reshard inside a Group-ZeRO layout
+        ParallelStrategy.is_redundant_backup(ParallelStrategy(12, 1, 1, num_distributed_optimizer_instances=2),
+                                             ParallelStrategy(12, 1, 1, num_distributed_optimizer_instances=2))

@@ -19,7 +19,8 @@ from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.transfer import TransferManager
 from oracle import model
 from oracle import transfer as oracle1
-from tests.helpers import SEED, SMALL_CASES, compare, extract, new_arenas, piece_fill_numpy, strat
+from tests.helpers import (SEED, SMALL_CASES, bf16_rne_bits, compare, extract, new_arenas, piece_fill_numpy,
+                           strat)
 
 pytestmark = pytest.mark.gpu
 
@@ -59,10 +60,12 @@ def _switches():
                                f"{b.pipeline_model_parallel_size}x{b.world_size}")
 
 
-@pytest.mark.parametrize("factory,src,dst", list(_switches()))
-def test_kernel_matches_oracle1(gpu_device, factory, src, dst):
+@pytest.mark.parametrize("factory,src,dst,bf16_source",
+                         [p.values + ("cast",) for p in _switches()] +
+                         [p.values + ("copy",) for p in list(_switches())[:4]])
+def test_kernel_matches_oracle1(gpu_device, factory, src, dst, bf16_source):
     spec = factory()
-    print(f"case {spec.name} {src} -> {dst}", flush=True)
+    print(f"case {spec.name} {src} -> {dst} bf16 {bf16_source}", flush=True)
     space = build_virtual_model(spec)
     ls, ld = space.layout(src), space.layout(dst)
     a = TrainingState.allocate(ls, gpu_device)
@@ -70,7 +73,7 @@ def test_kernel_matches_oracle1(gpu_device, factory, src, dst):
     a.fill_synthetic(SEED)
     for t in b.arenas():
         t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
-    tm = TransferManager(check_disjoint=True)
+    tm = TransferManager(check_disjoint=True, bf16_source=bf16_source)
     tm.transfer_optimizer_tensors(space, a, b)
     got32, gotbf = extract(ld, _host_arenas(b))
 
@@ -102,7 +105,13 @@ def _random_table(rng, n_segs, sizes):
         if rng.random() < 0.5:  # co-aligned offsets exercise the head/body/tail split
             do = do - (do * eb) % 16 // eb + (so * eb) % 16 // eb
             do = max(0, min(do, nb[1] - dst_ext))
-        rows.append((0, 0, eb, 0, so, do, ln, r, ss, ds))
+        cast = eb == 4 and rng.random() < 0.5
+        if cast:  # bf16 image into the second destination buffer
+            aux_s = ln + int(rng.integers(0, 9)) if r > 1 else 0
+            ao = int(rng.integers(0, sizes[1] // 2 - ((r - 1) * aux_s + ln)))
+            rows.append((0, 0, eb, 1, so, do, ln, r, ss, ds, 1, 0, ao, aux_s))
+        else:
+            rows.append((0, 0, eb, 0, so, do, ln, r, ss, ds, 0, 0, 0, 0))
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
     return t
@@ -121,12 +130,14 @@ def test_random_segments_match_numpy(gpu_device, seed):
     src_h = rng.integers(0, 256, nbytes, dtype=np.uint8)
     src = torch.from_numpy(src_h).to(gpu_device)
     dst = torch.zeros(nbytes, dtype=torch.uint8, device=gpu_device)
+    aux = torch.zeros(nbytes, dtype=torch.uint8, device=gpu_device)
     want = np.zeros(nbytes, dtype=np.uint8)
+    want_aux = np.zeros(nbytes, dtype=np.uint8)
     table = _random_table(rng, 40, (nbytes, nbytes))
     for s in table:
         one = np.array([s], dtype=SEGMENT_DTYPE)
-        plan = _native.Plan(one, [nbytes], [nbytes])
-        plan.execute([src.data_ptr()], [dst.data_ptr()], torch.cuda.current_stream().cuda_stream)
+        plan = _native.Plan(one, [nbytes], [nbytes, nbytes])
+        plan.execute([src.data_ptr()], [dst.data_ptr(), aux.data_ptr()], torch.cuda.current_stream().cuda_stream)
         eb = int(s["elem_bytes"])
         a, b = src_h.view({1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[eb]), \
             want.view({1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[eb])
@@ -134,8 +145,41 @@ def test_random_segments_match_numpy(gpu_device, seed):
             so = int(s["src_off"]) + r * int(s["src_stride"])
             do = int(s["dst_off"]) + r * int(s["dst_stride"])
             b[do:do + int(s["len"])] = a[so:so + int(s["len"])]
+            if int(s["flags"]):
+                ao = int(s["aux_off"]) + r * int(s["aux_stride"])
+                want_aux.view(np.uint16)[ao:ao + int(s["len"])] = bf16_rne_bits(a[so:so + int(s["len"])])
     torch.cuda.synchronize()
     assert np.array_equal(dst.cpu().numpy(), want)
+    assert np.array_equal(aux.cpu().numpy(), want_aux)
+
+
+def test_bf16_cast_rounding_special_values(gpu_device):
+    """The fused cast rounds like torch's float -> bfloat16 (nearest-even, NaN -> 0x7FC0, inf kept)."""
+    vals = np.array([0x3F800000, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x7F7FFFFF, 0x7F800000, 0xFF800000,
+                     0x7FC00001, 0xFFFFFFFF, 0x80000000, 0x00000001, 0x807FFFFF, 0x3F7F7FFF, 0x3F7F8000,
+                     0x477FE000, 0xC2F6E979], dtype=np.uint32)
+    n = vals.size * 64
+    host = np.tile(vals, 64)
+    src = torch.from_numpy(host.view(np.int32)).to(gpu_device)
+    dst = torch.zeros(n, dtype=torch.int32, device=gpu_device)
+    aux = torch.zeros(n, dtype=torch.int16, device=gpu_device)
+    t = np.zeros(2, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 1, 0, 0, n // 2, 1, 0, 0, 1, 0, 0, 0)           # vector path
+    t[1] = (0, 0, 4, 1, n // 2, n // 2, n // 2 - 1, 1, 0, 0, 1, 0, n // 2 + 1, 0)  # element path
+    plan = _native.Plan(t, [n * 4], [n * 4, n * 2])
+    assert plan.stats().scalar_bytes > 0 and plan.stats().vector_bytes > 0
+    plan.execute([src.data_ptr()], [dst.data_ptr(), aux.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = aux.cpu().numpy().view(np.uint16)
+    want = np.concatenate([bf16_rne_bits(host[:n // 2]), [0], bf16_rne_bits(host[n // 2:n - 1])]).astype(np.uint16)
+    got[n // 2] = 0
+    assert np.array_equal(got, want)
+    # Finite values and infinities round exactly as torch rounds them.  (torch's CPU kernels turn NaN
+    # into 0xFFFF or 0x7FC0 depending on vectorisation; the cast here always gives 0x7FC0.)
+    finite = (host & 0x7FFFFFFF) <= 0x7F800000
+    torch_bf16 = torch.from_numpy(host.view(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(want[:n // 2][finite[:n // 2]], torch_bf16[:n // 2][finite[:n // 2]])
+    assert (want[~np.concatenate([finite[:n // 2], [True], finite[n // 2:n - 1]])] == 0x7FC0).all()
 
 
 def test_large_multichunk_plan(gpu_device):
@@ -144,9 +188,9 @@ def test_large_multichunk_plan(gpu_device):
     src = torch.arange(n, dtype=torch.int32, device=gpu_device)
     dst = torch.full((n,), -1, dtype=torch.int32, device=gpu_device)
     rows = [
-        (0, 0, 4, 0, 0, 0, 1 << 24, 1, 0, 0),                      # contiguous 64 MiB
-        (0, 0, 4, 0, 1 << 24, (1 << 24) + 4, 1000, 20000, 1000, 1004),  # strided, co-aligned
-        (0, 0, 4, 0, 45_000_000, 45_000_001, 3_000_001, 1, 0, 0),  # misaligned by 4 bytes
+        (0, 0, 4, 0, 0, 0, 1 << 24, 1, 0, 0, 0, 0, 0, 0),                      # contiguous 64 MiB
+        (0, 0, 4, 0, 1 << 24, (1 << 24) + 4, 1000, 20000, 1000, 1004, 0, 0, 0, 0),  # strided, co-aligned
+        (0, 0, 4, 0, 45_000_000, 45_000_001, 3_000_001, 1, 0, 0, 0, 0, 0, 0),  # misaligned by 4 bytes
     ]
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
@@ -166,7 +210,7 @@ def test_large_multichunk_plan(gpu_device):
 
 def test_execute_errors(gpu_device):
     t = np.zeros(1, dtype=SEGMENT_DTYPE)
-    t[0] = (0, 0, 4, 0, 0, 0, 16, 1, 0, 0)
+    t[0] = (0, 0, 4, 0, 0, 0, 16, 1, 0, 0, 0, 0, 0, 0)
     plan = _native.Plan(t, [1024], [1024])
     buf = torch.zeros(1024, dtype=torch.uint8, device=gpu_device)
     with pytest.raises(_native.EmrsError) as e:  # out of place only

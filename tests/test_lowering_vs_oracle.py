@@ -24,7 +24,8 @@ def _switches():
 
 
 @pytest.mark.parametrize("factory,src,dst", list(_switches()))
-def test_plan_matches_oracles(factory, src, dst):
+@pytest.mark.parametrize("bf16_source", ["cast", "copy"])
+def test_plan_matches_oracles(factory, src, dst, bf16_source):
     spec = factory()
     inv = model.inventory(spec)
     S, D = strat(src), strat(dst)
@@ -36,7 +37,7 @@ def test_plan_matches_oracles(factory, src, dst):
 
     space = build_virtual_model(spec)
     ls, ld = space.layout(src), space.layout(dst)
-    table = lower_transfer(ls, ld)
+    table = lower_transfer(ls, ld, bf16_source=bf16_source)
     a_src, a_dst = new_arenas(ls), new_arenas(ld)
     piece_fill_numpy(ls.pieces(), a_src, SEED)
     execute_numpy(table, a_src, a_dst)

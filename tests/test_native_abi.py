@@ -31,9 +31,11 @@ def test_exports_every_declared_symbol():
 def test_record_layouts_match_header():
     class Seg(ctypes.Structure):
         _fields_ = [(n, ctypes.c_uint32) for n in ("src_buf", "dst_buf", "elem_bytes", "flags")] + \
-                   [(n, ctypes.c_uint64) for n in ("src_off", "dst_off", "len", "rows", "src_stride", "dst_stride")]
+                   [(n, ctypes.c_uint64) for n in ("src_off", "dst_off", "len", "rows", "src_stride", "dst_stride")] + \
+                   [("aux_buf", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("aux_off", ctypes.c_uint64),
+                    ("aux_stride", ctypes.c_uint64)]
 
-    assert ctypes.sizeof(Seg) == SEGMENT_DTYPE.itemsize == 64
+    assert ctypes.sizeof(Seg) == SEGMENT_DTYPE.itemsize == 88
     for name, (dt, off) in SEGMENT_DTYPE.fields.items():
         assert getattr(Seg, name).offset == off
     assert PIECE_DTYPE.itemsize == 88
@@ -41,7 +43,7 @@ def test_record_layouts_match_header():
 
 def _seg(**kw):
     row = dict(src_buf=0, dst_buf=0, elem_bytes=4, flags=0, src_off=0, dst_off=0, len=16, rows=1,
-               src_stride=0, dst_stride=0)
+               src_stride=0, dst_stride=0, aux_buf=0, reserved=0, aux_off=0, aux_stride=0)
     row.update(kw)
     t = np.zeros(1, dtype=SEGMENT_DTYPE)
     for k, v in row.items():
@@ -52,12 +54,17 @@ def _seg(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(elem_bytes=3), -1),
     (dict(rows=0), -1),
-    (dict(flags=1), -1),
     (dict(dst_buf=1), -1),
     (dict(rows=2, len=16, src_stride=16, dst_stride=8), -1),
     (dict(src_off=250, len=16), -2),
     (dict(dst_off=1, len=256), -2),
     (dict(rows=3, len=10, src_stride=200, dst_stride=10), -2),
+    (dict(flags=2), -1),
+    (dict(reserved=1), -1),
+    (dict(flags=1, elem_bytes=2), -1),
+    (dict(flags=1, aux_buf=1), -1),
+    (dict(flags=1, aux_off=500, len=16), -2),
+    (dict(flags=1, rows=2, src_stride=16, dst_stride=16, aux_stride=8), -1),
 ])
 def test_plan_create_rejects(kw, code):
     with pytest.raises(_native.EmrsError) as e:
@@ -71,6 +78,12 @@ def test_plan_create_overlap_check():
     with pytest.raises(_native.EmrsError) as e:
         _native.Plan(t, [1024], [1024], check_disjoint=True)
     assert e.value.code == -4
+    # bf16 images count as destination writes too.
+    t = np.concatenate([_seg(dst_off=0, len=8, flags=1, aux_buf=1, aux_off=0), _seg(dst_off=16, len=8, flags=1,
+                                                                                   aux_buf=1, aux_off=4)])
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(t, [1024], [1024, 1024], check_disjoint=True)
+    assert e.value.code == -4
 
 
 def test_too_many_buffers():
@@ -80,20 +93,24 @@ def test_too_many_buffers():
 
 
 def test_plan_stats_classify_alignment():
+    z = (0, 0, 0, 0)
     rows = [
-        (0, 0, 4, 0, 0, 0, 64, 1, 0, 0),      # vector: 256 bytes
-        (0, 0, 4, 0, 1, 1, 12, 1, 0, 0),      # co-aligned, 4 B off: 3 head + 8 body + 1 tail elements
-        (0, 0, 4, 0, 1, 2, 8, 1, 0, 0),       # not co-aligned: scalar
-        (0, 0, 2, 0, 0, 0, 8, 4, 16, 8),      # strided bf16 rows of 16 bytes: vector
-        (0, 0, 2, 0, 0, 64, 3, 4, 8, 5),      # strided, odd: scalar
+        (0, 0, 4, 0, 0, 0, 64, 1, 0, 0) + z,      # vector: 256 bytes
+        (0, 0, 4, 0, 1, 1, 12, 1, 0, 0) + z,      # co-aligned, 4 B off: 3 head + 8 body + 1 tail elements
+        (0, 0, 4, 0, 1, 2, 8, 1, 0, 0) + z,       # not co-aligned: scalar
+        (0, 0, 2, 0, 0, 0, 8, 4, 16, 8) + z,      # strided bf16 rows of 16 bytes: vector
+        (0, 0, 2, 0, 0, 64, 3, 4, 8, 5) + z,      # strided, odd: scalar
+        (0, 0, 4, 1, 256, 256, 32, 1, 0, 0, 1, 0, 8, 0),   # cast, aux 8-byte aligned: vector
+        (0, 0, 4, 1, 320, 320, 32, 1, 0, 0, 1, 0, 50, 0),  # cast, aux 4 bytes off: scalar
     ]
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
-    st = _native.Plan(t, [4096], [4096]).stats()
-    assert st.payload_bytes == 256 + 48 + 32 + 64 + 24
-    assert st.vector_bytes == 256 + 32 + 64
-    assert st.scalar_bytes == 16 + 32 + 24
-    assert st.n_segments == 5
+    st = _native.Plan(t, [4096], [4096, 4096]).stats()
+    assert st.read_bytes == 256 + 48 + 32 + 64 + 24 + 128 + 128
+    assert st.payload_bytes == st.read_bytes + 64 + 64
+    assert st.vector_bytes == 256 + 32 + 64 + 128
+    assert st.scalar_bytes == 16 + 32 + 24 + 128
+    assert st.n_segments == 7
 
 
 def test_empty_plan_and_no_device_errors():

@@ -32,7 +32,9 @@ def test_numpy_matches_c(cgen, kind, ki):
     for seed, pid in [(1234, 0), (1234, 194), (0, 7), (2 ** 64 - 1, 3)]:
         out = np.zeros(idx.size, dtype=np.uint32)
         cgen.oracle_synth(seed, pid, ki, idx.ctypes.data, idx.size, out.ctypes.data)
-        v = synth.values(seed, pid, kind, idx)
+        v = synth.values_numpy(seed, pid, kind, idx)
+        assert np.array_equal(v.view(np.uint16 if kind == "param" else np.uint32),
+                              synth.values(seed, pid, kind, idx).view(np.uint16 if kind == "param" else np.uint32))
         got = v.astype(np.uint32) if kind == "param" else v.view(np.uint32)
         assert np.array_equal(got, out)
 
