@@ -48,6 +48,9 @@ def workloads():
                                       ms.tiny_llama2, PS(8, 1, 1), PS(8, 4, 1)),
         "llama3-8b-tp2pp2dp2-tp4pp1dp2": ("Llama-3-8B GQA TP2PP2DP2 -> TP4PP1DP2, world 8",
                                           ms.llama3_8b, PS(8, 2, 2), PS(8, 4, 1)),
+        "llama3-8b-tp2pp2dp2-tp4pp1dp2-repad": ("Llama-3-8B GQA TP2PP2DP2 -> TP4PP1DP2, world 8, vocabulary "
+                                                "re-padded 128256 -> 128512", ms.llama3_8b, PS(8, 2, 2),
+                                                PS(8, 4, 1), True),
         "mixtral-4l-ep4-ep8": ("Mixtral-8x7B 4-layer slice EP4 (EDP2) -> EP8 (EDP1), world 8",
                                ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4),
                                PS(8, 1, 1, expert_model_parallel_size=8)),
@@ -66,11 +69,14 @@ def parse():
     ap.add_argument("--workload", default="llama2-7b-tp1dp8-tp4dp2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--placement-trials", type=int, default=0,
+                    help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="0: as many as can be resident")
     ap.add_argument("--nontemporal", type=int, default=1)
     ap.add_argument("--xcd-remap", type=int, default=1)
+    ap.add_argument("--run", type=int, default=4, help="0: contiguous chunk run per workgroup; N: round-robin runs of N")
     ap.add_argument("--copy-calibration-gib", type=float, default=0.0,
                     help="time a single contiguous copy of this many GiB instead (traffic calibration)")
     return ap.parse_args()
@@ -133,18 +139,25 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _native.load()
-    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap))
+    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run)
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:
         return copy_calibration(args, dev, stream)
 
-    desc, spec_fn, src, dst = workloads()[args.workload]
+    desc, spec_fn, src, dst, *opt = workloads()[args.workload]
+    repad = bool(opt and opt[0])
     backup = ParallelStrategy.is_redundant_backup(src, dst)
     spec = spec_fn()
     t0 = time.time()
-    space = build_virtual_model(spec)
-    ls, ld = space.layout(src), space.layout(dst)
+    if repad:
+        ls = build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(
+            src.tensor_model_parallel_size))).layout(src)
+        ld = build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(
+            dst.tensor_model_parallel_size))).layout(dst)
+    else:
+        space = build_virtual_model(spec)
+        ls, ld = space.layout(src), space.layout(dst)
     tm = TransferManager(bf16_source=args.bf16_source)
     kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
     plan = tm.compile(ls, ld, kind)
@@ -161,7 +174,8 @@ def main():
     torch.cuda.synchronize()
     verified = None
     if not args.no_verify:
-        bad, first = b.verify_synthetic(SEED, bf16=backup is None)
+        vocab_rows = ls.space.spec.padded_vocab_size if repad else None
+        bad, first = b.verify_synthetic(SEED, bf16=backup is None, vocab_rows=vocab_rows)
         verified = bad == 0
         if bad:
             print(f"[bench] verification FAILED: {bad} elements, first {first}", file=sys.stderr)
@@ -186,7 +200,9 @@ def main():
     tf = os.path.join(ROOT, "profiles", f"{args.workload}.traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            rec = json.load(f)
+        if rec.get("bf16_source", "cast") == (tm.bf16_source if backup is None else None) or backup is not None:
+            traffic = rec.get("hbm_bytes_per_launch")
 
     out = {
         "metric": METRIC,
@@ -205,10 +221,33 @@ def main():
                    "read_bytes": plan.read_bytes, "bf16_source": tm.bf16_source if backup is None else None,
                    "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
                    "wall_ms_per_step": round(wall_ms / args.steps, 4),
-                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4)},
+                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4),
+                   "median_ms": round(sorted(step_ms)[len(step_ms) // 2], 4),
+                   "first_third_ms": round(sum(step_ms[:max(1, len(step_ms) // 3)]) / max(1, len(step_ms) // 3), 4),
+                   "last_third_ms": round(sum(step_ms[-max(1, len(step_ms) // 3):]) / max(1, len(step_ms) // 3), 4)},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
     }
+    if args.placement_trials:
+        import gc
+
+        trials = []
+        for _ in range(args.placement_trials):
+            del b
+            gc.collect()
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            b = TrainingState.allocate(ld, dev, param=a.param if backup is not None else None)
+            for _ in range(2):
+                tm.execute(plan, a, b, stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(5):
+                tm.execute(plan, a, b, stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            trials.append(round(e0.elapsed_time(e1) / 5, 3))
+        out["config"]["placement_trials_ms"] = trials
     del a, b
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:

@@ -57,7 +57,7 @@ class PlanStats(ctypes.Structure):
 
 class Tuning(ctypes.Structure):
     _fields_ = [("blocks_per_cu", ctypes.c_uint32), ("nontemporal", ctypes.c_uint32),
-                ("xcd_remap", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("xcd_remap", ctypes.c_uint32), ("run", ctypes.c_uint32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -129,8 +129,8 @@ def get_tuning() -> Tuning:
     return t
 
 
-def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True) -> None:
-    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, 0)
+def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True, run: int = 4) -> None:
+    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 
 

@@ -84,7 +84,7 @@ struct DevSeg {
   uint8_t sh1;
   uint8_t sh2;
   uint8_t unit_log2;
-  uint8_t cast;          // 1: also write bf16 to aux
+  uint8_t cast;          // bit 0: also write bf16 to aux; bit 1: write zeros, read nothing
   uint8_t src_buf;
   uint8_t dst_buf;
   uint8_t aux_buf;
@@ -116,6 +116,7 @@ struct Tuning {
   std::atomic<uint32_t> blocks_per_cu{0};  // 0: as many as can be resident
   std::atomic<uint32_t> nontemporal{1};
   std::atomic<uint32_t> xcd_remap{1};
+  std::atomic<uint32_t> run{4};  // round-robin runs of 4 chunks
 };
 Tuning g_tuning;
 
@@ -163,7 +164,7 @@ struct CastOf<uint32_t> {
 // kCast also store each unit's bf16 image to aux.  In a partial chunk, lanes
 // past the end load the last unit again (in bounds) so that every load is
 // unconditional; only their stores are masked off.
-template <typename T, bool kNT, bool kCast>
+template <typename T, bool kNT, bool kCast, bool kZero = false>
 __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, char *dbase, char *abase,
                                            uint32_t u0, uint32_t u_end) {
   typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
@@ -178,9 +179,14 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
     const T *sp = src + s.src_off + u0;
     T *dp = dst + s.dst_off + u0;
     A *ap = aux + s.aux_off + u0;
+    if constexpr (kZero) {
+#pragma unroll
+      for (int j = 0; j < kUnroll; ++j) v[j] = T{};
+    }
     if (n == kChunkUnits) {
 #pragma unroll
-      for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + j * kThreads + tid);
+      for (int j = 0; j < kUnroll; ++j)
+        if constexpr (!kZero) v[j] = ld<T, kNT>(sp + j * kThreads + tid);
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j) {
         st<T, kNT>(dp + j * kThreads + tid, v[j]);
@@ -188,7 +194,8 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < kUnroll; ++j) v[j] = ld<T, kNT>(sp + min(j * kThreads + tid, n - 1));
+      for (int j = 0; j < kUnroll; ++j)
+        if constexpr (!kZero) v[j] = ld<T, kNT>(sp + min(j * kThreads + tid, n - 1));
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j)
         if (j * kThreads + tid < n) {
@@ -204,7 +211,8 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
     const uint32_t u = u0 + min(j * kThreads + tid, n - 1);
     row[j] = magic_div(u, s.magic, s.sh1, s.sh2);
     col[j] = u - row[j] * s.len;
-    v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row[j] * s.src_stride + col[j]);
+    if constexpr (kZero) v[j] = T{};
+    else v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row[j] * s.src_stride + col[j]);
   }
 #pragma unroll
   for (int j = 0; j < kUnroll; ++j)
@@ -215,16 +223,10 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
     }
 }
 
+// Copy chunks [c, c_end), starting from the segment that contains chunk c.
 template <bool kNT>
-__global__ __launch_bounds__(kThreads) void copy_plan_kernel(
-    const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
-    uint64_t chunks_per_block, uint32_t xcd_stride, Bases src, Bases dst) {
-  uint64_t b = blockIdx.x;
-  if (xcd_stride) b = (b & 7) * xcd_stride + (b >> 3);  // one contiguous slice per XCD
-  uint64_t c = b * chunks_per_block;
-  if (c >= n_chunks) return;
-  const uint64_t c_end = min(c + chunks_per_block, n_chunks);
-
+__device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
+                                               uint64_t c, uint64_t c_end, const Bases &src, const Bases &dst) {
   // Last segment whose first chunk is <= c.
   uint32_t lo = 0, hi = n_segs - 1;
   while (lo < hi) {
@@ -248,6 +250,21 @@ __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
     const char *sb = src.p[s.src_buf];
     char *db = dst.p[s.dst_buf];
     char *ab = dst.p[s.aux_buf];
+    if (s.cast & 2) {  // zero fill, with or without the bf16 image
+      if (s.cast & 1) {
+        if (s.unit_log2 == 4) copy_chunk<u32x4, kNT, true, true>(s, sb, db, ab, u0, u_end);
+        else copy_chunk<uint32_t, kNT, true, true>(s, sb, db, ab, u0, u_end);
+      } else {
+        switch (s.unit_log2) {
+          case 4: copy_chunk<u32x4, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
+          case 3: copy_chunk<uint64_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
+          case 2: copy_chunk<uint32_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
+          case 1: copy_chunk<uint16_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
+          default: copy_chunk<uint8_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
+        }
+      }
+      continue;
+    }
     if (s.cast) {
       if (s.unit_log2 == 4) copy_chunk<u32x4, kNT, true>(s, sb, db, ab, u0, u_end);
       else copy_chunk<uint32_t, kNT, true>(s, sb, db, ab, u0, u_end);
@@ -261,6 +278,26 @@ __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
       default: copy_chunk<uint8_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
     }
   }
+}
+
+// Persistent grid.  With run == 0 every workgroup takes one contiguous run of
+// chunks_per_block chunks (xcd_stride != 0: each XCD's workgroups cover one
+// contiguous slice).  With run > 0 the chunks are dealt out round-robin in
+// runs of `run` chunks, so all workgroups sweep the plan together.
+template <bool kNT>
+__global__ __launch_bounds__(kThreads) void copy_plan_kernel(
+    const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
+    uint64_t chunks_per_block, uint32_t xcd_stride, uint32_t run, Bases src, Bases dst) {
+  if (run) {
+    for (uint64_t c = (uint64_t)blockIdx.x * run; c < n_chunks; c += (uint64_t)gridDim.x * run)
+      copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + run, n_chunks), src, dst);
+    return;
+  }
+  uint64_t b = blockIdx.x;
+  if (xcd_stride) b = (b & 7) * xcd_stride + (b >> 3);  // one contiguous slice per XCD
+  const uint64_t c = b * chunks_per_block;
+  if (c >= n_chunks) return;
+  copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + chunks_per_block, n_chunks), src, dst);
 }
 
 // ---------------------------------------------------------------------------
@@ -332,6 +369,7 @@ namespace {
 // of half the segment's unit.
 struct Aux {
   bool on = false;
+  bool zero = false;  // the segment writes zeros (EMRS_SEG_ZERO_FILL)
   uint32_t buf = 0;
   uint64_t off = 0, stride = 0;
 };
@@ -389,7 +427,7 @@ struct Builder {
     d.unit_log2 = (uint8_t)ul;
     d.src_buf = (uint8_t)sbuf;
     d.dst_buf = (uint8_t)dbuf;
-    d.cast = ax.on ? 1 : 0;
+    d.cast = (ax.on ? 1 : 0) | (ax.zero ? 2 : 0);
     d.aux_buf = (uint8_t)(ax.on ? ax.buf : dbuf);
     d.aux_off = ax.on ? aoff : 0;
     d.aux_stride = ax.on && rows > 1 ? astride : 0;
@@ -491,8 +529,10 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     const std::string at(where);
     const int lg = log2_of(s.elem_bytes);
     const bool cast = (s.flags & EMRS_SEG_CAST_BF16) != 0;
+    const bool zero = (s.flags & EMRS_SEG_ZERO_FILL) != 0;
     if (lg < 0) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "elem_bytes must be 1, 2, 4 or 8");
-    if ((s.flags & ~EMRS_SEG_CAST_BF16) || s.reserved) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "unknown flags");
+    if ((s.flags & ~(EMRS_SEG_CAST_BF16 | EMRS_SEG_ZERO_FILL)) || s.reserved)
+      return fail(EMRS_ERR_INVALID_ARGUMENT, at + "unknown flags");
     if (cast && s.elem_bytes != 4) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a bf16 cast needs fp32 elements");
     if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs || (cast && s.aux_buf >= n_dst_bufs))
       return fail(EMRS_ERR_INVALID_ARGUMENT, at + "buffer id out of range");
@@ -500,24 +540,27 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     if (s.len == 0) continue;
     if (s.rows > 1 && (s.dst_stride < s.len || (cast && s.aux_stride < s.len)))
       return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a destination stride < len makes rows overlap");
-    if (extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes) > src_buf_bytes[s.src_buf])
+    if (!zero && extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes) >
+                     src_buf_bytes[s.src_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "source range exceeds its buffer");
     if (extent_end(s.dst_off, s.len, s.rows, s.rows > 1 ? s.dst_stride : 0, s.elem_bytes) > dst_buf_bytes[s.dst_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "destination range exceeds its buffer");
     if (cast && extent_end(s.aux_off, s.len, s.rows, s.rows > 1 ? s.aux_stride : 0, 2) > dst_buf_bytes[s.aux_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "bf16 range exceeds its buffer");
-    read += s.len * s.rows * s.elem_bytes;
+    if (!zero) read += s.len * s.rows * s.elem_bytes;
     payload += s.len * s.rows * (s.elem_bytes + (cast ? 2 : 0));
-    src_used[s.src_buf] = 1;
+    if (!zero) src_used[s.src_buf] = 1;
     dst_used[s.dst_buf] = 1;
     if (cast) dst_used[s.aux_buf] = 1;
 
     const uint64_t eb = s.elem_bytes;
-    const uint64_t so = s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
-    const uint64_t ss = s.rows > 1 ? s.src_stride * eb : 0, ds = s.rows > 1 ? s.dst_stride * eb : 0;
+    // A zero fill has no source: align its phantom source with the destination.
+    const uint64_t so = zero ? s.dst_off * eb : s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
+    const uint64_t ds = s.rows > 1 ? s.dst_stride * eb : 0, ss = zero ? ds : (s.rows > 1 ? s.src_stride * eb : 0);
     const uint64_t ao = cast ? s.aux_off * 2 : 0, as = cast && s.rows > 1 ? s.aux_stride * 2 : 0;
     Aux ax;
     ax.on = cast;
+    ax.zero = zero;
     ax.buf = s.aux_buf;
     // The bf16 image of a 16-byte unit is 8 bytes: the vector path needs it 8-byte aligned.
     const bool aux_vec_ok = !cast || (ao % 8 == 0 && as % 8 == 0);
@@ -539,7 +582,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
         bld.emit(s.src_buf, s.dst_buf, lg, (so + head + body) / eb, (dof + head + body) / eb, tail / eb, 1, 0, 0, ax);
       } else {
         ax.off = s.aux_off;
-        bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, L / eb, 1, 0, 0, ax);
+        bld.emit(s.src_buf, s.dst_buf, lg, so / eb, s.dst_off, L / eb, 1, 0, 0, ax);
       }
     } else if (so % 16 == 0 && dof % 16 == 0 && lb % 16 == 0 && ss % 16 == 0 && ds % 16 == 0 && aux_vec_ok) {
       ax.off = ao / 8;
@@ -548,7 +591,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     } else {
       ax.off = s.aux_off;
       ax.stride = s.rows > 1 ? s.aux_stride : 0;
-      bld.emit(s.src_buf, s.dst_buf, lg, s.src_off, s.dst_off, s.len, s.rows, s.src_stride, s.dst_stride, ax);
+      bld.emit(s.src_buf, s.dst_buf, lg, so / eb, s.dst_off, s.len, s.rows, ss / eb, s.dst_stride, ax);
     }
   }
   if (flags & EMRS_PLAN_CHECK_DISJOINT) {
@@ -646,18 +689,25 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint32_t bpc = g_tuning.blocks_per_cu.load();
   const uint64_t max_blocks = (uint64_t)cus * (bpc ? bpc : (uint32_t)(nt ? resident_nt : resident_t));
   uint64_t blocks = std::min<uint64_t>(plan->n_chunks, max_blocks);
-  const bool remap = g_tuning.xcd_remap.load() != 0;
+  uint32_t run = g_tuning.run.load();
+  if (run) {
+    // Round-robin runs: at most a quarter of each workgroup's share, so that
+    // small plans still spread over the whole grid.
+    run = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(run, plan->n_chunks / (blocks * 4)));
+    blocks = std::min<uint64_t>(blocks, (plan->n_chunks + run - 1) / run);
+  }
+  const bool remap = !run && g_tuning.xcd_remap.load() != 0;
   if (remap) blocks = (blocks + 7) / 8 * 8;
   const uint64_t cpb = (plan->n_chunks + blocks - 1) / blocks;
-  if (!remap) blocks = (plan->n_chunks + cpb - 1) / cpb;
+  if (!remap && !run) blocks = (plan->n_chunks + cpb - 1) / cpb;
   const uint32_t xcd_stride = remap ? (uint32_t)(blocks / 8) : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (nt)
     hipLaunchKernelGGL(copy_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
-                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, sb, db);
+                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, run, sb, db);
   else
     hipLaunchKernelGGL(copy_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
-                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, sb, db);
+                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, run, sb, db);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "copy_plan_kernel launch");
   return EMRS_OK;
@@ -683,7 +733,7 @@ int emrs_get_tuning(emrs_tuning *out) {
   out->blocks_per_cu = g_tuning.blocks_per_cu.load();
   out->nontemporal = g_tuning.nontemporal.load();
   out->xcd_remap = g_tuning.xcd_remap.load();
-  out->reserved = 0;
+  out->run = g_tuning.run.load();
   return EMRS_OK;
 }
 
@@ -693,6 +743,7 @@ int emrs_set_tuning(const emrs_tuning *t) {
   g_tuning.blocks_per_cu.store(t->blocks_per_cu);
   g_tuning.nontemporal.store(t->nontemporal ? 1 : 0);
   g_tuning.xcd_remap.store(t->xcd_remap ? 1 : 0);
+  g_tuning.run.store(t->run);
   return EMRS_OK;
 }
 

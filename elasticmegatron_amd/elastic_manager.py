@@ -16,6 +16,11 @@ state on one device.  ``reshard`` keeps the reference's control flow:
 
 Process-group rebuild, learning-rate broadcast and dataloader rebuild have no
 counterpart on one device and are not performed.
+
+The padded vocabulary stays fixed across switches, as in the reference
+(virtual_param.py:480-481).  With ``repad_vocab=True`` it follows Megatron's
+padding rule for each strategy's TP size instead: the true vocabulary rows
+are carried over and new padding rows are zero in all four tensors.
 """
 
 from __future__ import annotations
@@ -42,23 +47,44 @@ def _as_strategy(s: StrategyLike) -> ParallelStrategy:
 class ElasticMegatronManager:
     def __init__(self, parallel_strategy_list: List[StrategyLike], model_spec: ModelSpec,
                  training_state: Optional[TrainingState] = None, device=None,
-                 release_source: bool = True):
+                 release_source: bool = True, repad_vocab: bool = False):
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
+        if repad_vocab and model_spec.vocab_size is None:
+            raise ValueError("repad_vocab needs model_spec.vocab_size")
         self.parallel_strategy_list = [_as_strategy(s) for s in parallel_strategy_list]
         self.model_spec = model_spec
-        self.virtual_param_space: VirtualParamSpace = build_virtual_model(model_spec)
+        self.repad_vocab = repad_vocab
+        self._spaces: Dict[int, VirtualParamSpace] = {}
         for s in self.parallel_strategy_list:
-            self.virtual_param_space.build_model_virtual_params(s)
+            self.space_for(s).build_model_virtual_params(s)
         self.transfer_manager = TransferManager()
         self.release_source = release_source
         self.last_transfer_ms = 0.0
         cur = self.parallel_strategy_list[0]
         if training_state is None:
-            training_state = TrainingState.allocate(self.virtual_param_space.layout(cur), device)
+            training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device)
         elif training_state.parallel_strategy != cur:
             raise ValueError("training_state does not use the first strategy of the list")
+        elif training_state.layout.space is not self.space_for(cur):
+            raise ValueError("training_state was laid out for another model")
         self.training_state = training_state
+
+    def space_for(self, strategy: ParallelStrategy) -> VirtualParamSpace:
+        """The virtual model a strategy's state is laid out in (one per padded vocabulary size)."""
+        pv = (self.model_spec.padded_vocab_for_tp(strategy.tensor_model_parallel_size) if self.repad_vocab
+              else self.model_spec.padded_vocab_size)
+        space = self._spaces.get(pv)
+        if space is None:
+            spec = self.model_spec if pv == self.model_spec.padded_vocab_size else \
+                self.model_spec.with_padded_vocab(pv)
+            space = self._spaces[pv] = build_virtual_model(spec)
+        return space
+
+    @property
+    def virtual_param_space(self) -> VirtualParamSpace:
+        """The virtual model of the current state."""
+        return self.training_state.layout.space
 
     @property
     def parallel_strategy(self) -> ParallelStrategy:
@@ -66,8 +92,10 @@ class ElasticMegatronManager:
 
     def transfer_params(self, src: TrainingState, dst: TrainingState) -> float:
         """Plan (cached) and move the state; returns the executor's time in ms."""
-        self.virtual_param_space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
-        self.virtual_param_space.src_state, self.virtual_param_space.dst_state = src, dst
+        space = src.layout.space
+        if space is dst.layout.space:
+            space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
+        space.src_state, space.dst_state = src, dst
         plan = self.transfer_manager.compile(src.layout, dst.layout)
         with Timer() as t:
             self.transfer_manager.execute(plan, src, dst)
@@ -112,11 +140,13 @@ class ElasticMegatronManager:
         dst_strategy = _as_strategy(new_parallel_strategy)
         src_state = self.training_state
         src_strategy = src_state.parallel_strategy
-        space = self.virtual_param_space
+        space = src_state.layout.space
         backup = ParallelStrategy.is_redundant_backup(src_strategy, dst_strategy)
-        dst_layout = space.layout(dst_strategy)
+        dst_space = self.space_for(dst_strategy)
+        dst_layout = dst_space.layout(dst_strategy)
         if backup is None:
-            space.register_reshard(src_strategy, dst_strategy)
+            if dst_space is space:
+                space.register_reshard(src_strategy, dst_strategy)
             plan = self.transfer_manager.compile(src_state.layout, dst_layout)
         else:
             plan = self.transfer_manager.compile(src_state.layout, dst_layout,

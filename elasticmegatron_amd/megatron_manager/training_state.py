@@ -18,7 +18,7 @@ from typing import List, Optional, Tuple
 import torch
 
 from .. import _native
-from ..resharding.layout import ARENA_NAMES, StrategyLayout
+from ..resharding.layout import ARENA_NAMES, StrategyLayout, split_vocab_rows
 from ..resharding.util import Range
 
 
@@ -106,11 +106,24 @@ class TrainingState:
         with torch.cuda.device(self.device):
             _native.synth_fill(pcs, self.arena_ptrs(), self.arena_bytes(), seed, self._stream())
 
-    def verify_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True):
-        """(mismatching elements, first bad element) against the seeded synthetic values."""
+    def verify_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True,
+                         vocab_rows: Optional[int] = None):
+        """(mismatching elements, first bad element) against the seeded synthetic values.
+
+        ``vocab_rows``: vocabulary rows at and past it must be zero instead
+        (new padding rows after a switch to a larger padded vocabulary).
+        """
         pcs = self.layout.pieces(params, include_bf16=bf16, include_fp32=fp32)
+        zero = []
+        if vocab_rows is not None:
+            pcs, zero = split_vocab_rows(self.layout, pcs, vocab_rows)
         with torch.cuda.device(self.device):
             bad, first = _native.synth_verify(pcs, self.arena_ptrs(), self.arena_bytes(), seed, self._stream())
+            arenas = self.arenas()
+            for buf, off, n in zero:
+                a = arenas[buf]
+                bits = a.view(torch.int16 if a.dtype == torch.bfloat16 else torch.int32)[off:off + n]
+                bad += int(torch.count_nonzero(bits))
         if first is not None:
             p = pcs[first[0]]
             first = dict(arena=ARENA_NAMES[int(p["buf"])], param_id=int(p["param_id"]), kind=int(p["kind"]),

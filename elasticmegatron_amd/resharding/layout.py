@@ -49,6 +49,7 @@ SEGMENT_DTYPE = np.dtype([
     ("aux_buf", "<u4"), ("reserved", "<u4"), ("aux_off", "<u8"), ("aux_stride", "<u8"),
 ])
 SEG_CAST_BF16 = 1
+SEG_ZERO_FILL = 2
 PIECE_DTYPE = np.dtype([
     ("buf", "<u4"), ("param_id", "<u4"), ("kind", "<u4"), ("reserved", "<u4"),
     ("buf_off", "<u8"), ("len", "<u8"), ("local_start", "<u8"), ("local_cols", "<u8"),
@@ -293,6 +294,38 @@ class StrategyLayout:
         if rows:
             arr[:] = rows
         return arr
+
+
+VOCAB_PARAM_NAMES = ("embedding.word_embeddings.weight", "output_layer.weight")
+
+
+def split_vocab_rows(layout: "StrategyLayout", pieces: np.ndarray, vocab_rows: int):
+    """Cut the pieces of the vocabulary parameters at full row ``vocab_rows``.
+
+    Returns (pieces holding rows below it, [(buf, offset, len)] of the
+    elements at or past it): after a switch to a larger padded vocabulary,
+    the first keep their values and the second are new padding rows.
+    """
+    vocab_ids = {vp.global_index for vp in layout.space.all_virtual_params if vp.name in VOCAB_PARAM_NAMES}
+    keep, zero = [], []
+    for p in pieces:
+        n = int(p["len"])
+        if int(p["param_id"]) not in vocab_ids or int(p["band_rows"]):
+            keep.append(p)
+            continue
+        # Row-split vocabulary shards: full row = local row + row_off.
+        cut = max(0, vocab_rows - int(p["row_off"])) * int(p["local_cols"]) - int(p["local_start"])
+        cut = min(max(cut, 0), n)
+        if cut:
+            q = p.copy()
+            q["len"] = cut
+            keep.append(q)
+        if cut < n:
+            zero.append((int(p["buf"]), int(p["buf_off"]) + cut, n - cut))
+    arr = np.zeros(len(keep), dtype=PIECE_DTYPE)
+    if keep:
+        arr[:] = keep
+    return arr, zero
 
 
 def _piece_row(buf: int, pid: int, kind: int, h: Holder, geo: Geometry):

@@ -38,7 +38,8 @@ from typing import Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from .layout import ARENA_PARAM, SEG_CAST_BF16, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout
+from .layout import (ARENA_PARAM, SEG_CAST_BF16, SEG_ZERO_FILL, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout,
+                     view2d)
 
 
 @dataclass(frozen=True)
@@ -110,15 +111,18 @@ class SegmentBuilder:
         self.rows: List[Tuple] = []
 
     def add(self, sbuf: int, dbuf: int, eb: int, so: int, do: int, n: int, rows: int, ss: int, ds: int,
-            aux: Optional[Tuple[int, int, int]] = None) -> None:
+            aux: Optional[Tuple[int, int, int]] = None, zero: bool = False) -> None:
         if n <= 0 or rows <= 0:
             return
         flags, abuf, aoff, astr = (SEG_CAST_BF16, aux[0], aux[1], aux[2]) if aux else (0, 0, 0, 0)
+        if zero:
+            flags |= SEG_ZERO_FILL
+            so, ss = 0, 0
         if self.rows and rows == 1:
             p = self.rows[-1]
             if (p[0] == sbuf and p[1] == dbuf and p[2] == eb and p[3] == flags and p[7] == 1
-                    and p[4] + p[6] == so and p[5] + p[6] == do
-                    and (not flags or (p[10] == abuf and p[12] + p[6] == aoff))):
+                    and (zero or p[4] + p[6] == so) and p[5] + p[6] == do
+                    and (not aux or (p[10] == abuf and p[12] + p[6] == aoff))):
                 self.rows[-1] = p[:6] + (p[6] + n,) + p[7:]
                 return
         self.rows.append((sbuf, dbuf, eb, flags, so, do, n, rows, ss, ds, abuf, 0, aoff, astr if rows > 1 else 0))
@@ -137,6 +141,37 @@ def _src_replica(vp, holders: List[Holder]) -> List[Holder]:
     return out
 
 
+def _rows_from(rects: Sequence[Rect], first_row: int) -> Iterable[Tuple[int, int, int, int]]:
+    """(dst_off, len, rows, dst_stride) of the parts of ``rects`` at full rows >= first_row."""
+    for d in rects:
+        if d.r1 <= first_row:
+            continue
+        r0 = max(d.r0, first_row)
+        off = d.off + (r0 - d.r0) * d.stride
+        n, rows = d.c1 - d.c0, d.r1 - r0
+        if rows == 1 or n == d.stride:
+            yield off, n * rows, 1, 0
+        else:
+            yield off, n, rows, d.stride
+
+
+def check_compatible(src_space, dst_space) -> None:
+    """Two models that differ at most in the padded vocabulary (rows of the embedding and output layer)."""
+    if src_space is dst_space:
+        return
+    a, b = src_space.all_virtual_params, dst_space.all_virtual_params
+    if len(a) != len(b) or src_space.tied_embeddings != dst_space.tied_embeddings:
+        raise ValueError("the two layouts are of different models")
+    for x, y in zip(a, b):
+        same_attr = (x.name == y.name and x.tensor_parallel_attr.tensor_model_parallel
+                     == y.tensor_parallel_attr.tensor_model_parallel
+                     and x.tensor_parallel_attr.partition_dim == y.tensor_parallel_attr.partition_dim)
+        vocab = x.param_def.name in ("embedding.word_embeddings.weight", "output_layer.weight")
+        same_shape = x.full_shape == y.full_shape or (vocab and x.full_shape[1:] == y.full_shape[1:])
+        if not (same_attr and same_shape):
+            raise ValueError(f"the two layouts are of different models ({x.name} vs {y.name})")
+
+
 def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool = True,
                    include_bf16: bool = True, bf16_source: str = "cast") -> np.ndarray:
     """Segments of a switch between two layouts of the same model.
@@ -151,22 +186,29 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
       parameter.
     * ``"copy"``: the bf16 params are copied from the source bf16 shards.
       28 bytes per parameter; equal bits when main = upcast(param).
+
+    The two layouts may differ in the padded vocabulary (a re-padding switch;
+    the reference keeps it fixed, virtual_param.py:480-481).  Rows the source
+    has and the destination keeps are copied; new padding rows are written
+    as zeros in all four tensors; dropped padding rows are not read.
     """
     if bf16_source not in ("cast", "copy"):
         raise ValueError(bf16_source)
     cast = include_bf16 and bf16_source == "cast"
     if cast and not include_fp32:
         raise ValueError("the bf16 cast rides on the fp32 main segments")
-    space = src.space
-    assert dst.space is space
+    check_compatible(src.space, dst.space)
     fp32 = SegmentBuilder()
     bf16 = SegmentBuilder()
-    for vp in space.all_virtual_params:
+    for vp in dst.space.all_virtual_params:
         # A tied output layer is filled from the source word embedding: the
         # reference broadcasts the new embedding state to it (transfer.py:103-141).
-        sv = space.value_source(vp)
+        sv = src.space.value_source(src.space.all_virtual_params[vp.global_index])
         if not (src.has_param(sv) and dst.has_param(vp)):
             continue  # tied output layer at destination PP 1 (transfer.py:324-330)
+        src_rows = view2d(sv.full_shape, sv.tensor_parallel_attr.partition_dim)[0]
+        dst_rows = view2d(vp.full_shape, vp.tensor_parallel_attr.partition_dim)[0]
+        new_rows = src_rows if dst_rows > src_rows else None
         if include_fp32:
             bf16_base = {h.tp_rank: h.offset for h in dst.bf16_holders(vp)} if cast else {}
             s_rects = [r for h in _src_replica(sv, src.fp32_holders(sv))
@@ -176,12 +218,19 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
             for h in dst.fp32_holders(vp):
                 want += h.hi - h.lo
                 d_rects = holder_rects(h, dst.geometry(vp, h.tp_rank))
-                for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
-                    aux = None
+
+                def aux_of(do, ds):
                     if cast and h.instance == 0:
-                        aux = (ARENA_PARAM, bf16_base[h.tp_rank] + do - h.offset + h.lo, ds)
-                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds, aux)
+                        return ARENA_PARAM, bf16_base[h.tp_rank] + do - h.offset + h.lo, ds
+                    return None
+
+                for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
+                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds, aux_of(do, ds))
                     covered += n * rows
+                if new_rows is not None:
+                    for do, n, rows, ds in _rows_from(d_rects, new_rows):
+                        fp32.add(0, 0, 4, 0, do, n, rows, 0, ds, aux_of(do, ds), zero=True)
+                        covered += n * rows
             if covered != want:
                 raise AssertionError(f"{vp.name}: fp32 plan covers {covered} of {want} elements")
             if cast:
@@ -199,6 +248,10 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
                 for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
                     bf16.add(ARENA_PARAM, ARENA_PARAM, 2, so, do, n, rows, ss, ds)
                     covered += n * rows
+                if new_rows is not None:
+                    for do, n, rows, ds in _rows_from(d_rects, new_rows):
+                        bf16.add(ARENA_PARAM, ARENA_PARAM, 2, 0, do, n, rows, 0, ds, zero=True)
+                        covered += n * rows
             if covered != want:
                 raise AssertionError(f"{vp.name}: bf16 plan covers {covered} of {want} elements")
     return _assemble(fp32.table(), bf16.table())
@@ -235,12 +288,14 @@ def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
         if n * rows <= max_elems:
             out.append(s)
             continue
+        reads = not s["flags"] & SEG_ZERO_FILL
+        cast = bool(s["flags"] & SEG_CAST_BF16)
         if rows == 1:
             for o in range(0, n, max_elems):
                 p = s.copy()
-                p["src_off"] += o
+                p["src_off"] += o if reads else 0
                 p["dst_off"] += o
-                p["aux_off"] += o if s["flags"] else 0
+                p["aux_off"] += o if cast else 0
                 p["len"] = min(max_elems, n - o)
                 out.append(p)
             continue
@@ -249,7 +304,7 @@ def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
             p = s.copy()
             p["src_off"] += r * int(s["src_stride"])
             p["dst_off"] += r * int(s["dst_stride"])
-            p["aux_off"] += r * int(s["aux_stride"]) if s["flags"] else 0
+            p["aux_off"] += r * int(s["aux_stride"])
             p["rows"] = min(step, rows - r)
             out.append(p)
     return np.array(out, dtype=SEGMENT_DTYPE) if out else np.zeros(0, dtype=SEGMENT_DTYPE)
@@ -271,7 +326,8 @@ def _assemble(fp32: np.ndarray, bf16: np.ndarray) -> np.ndarray:
         t["src_buf"] = k
         t["dst_buf"] = k
         if k:
-            for f in ("flags", "aux_buf", "aux_off", "aux_stride"):
+            t["flags"] &= ~np.uint32(SEG_CAST_BF16)
+            for f in ("aux_buf", "aux_off", "aux_stride"):
                 t[f] = 0
     return np.concatenate([out, bf16])
 
@@ -287,5 +343,6 @@ def payload_bytes(table: np.ndarray) -> int:
 
 
 def read_bytes(table: np.ndarray) -> int:
-    """Bytes read per execution."""
-    return int(np.sum(_units(table) * table["elem_bytes"].astype(np.uint64)))
+    """Bytes read per execution (zero fills read nothing)."""
+    reads = (table["flags"] & SEG_ZERO_FILL) == 0
+    return int(np.sum(_units(table) * table["elem_bytes"].astype(np.uint64) * reads.astype(np.uint64)))

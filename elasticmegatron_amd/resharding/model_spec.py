@@ -62,6 +62,9 @@ class ModelSpec:
     num_experts: Optional[int] = None
     moe_ffn_hidden_size: Optional[int] = None
     moe_grouped_gemm: bool = True
+    # true vocabulary and Megatron's padding rule (only used to re-pad the vocabulary)
+    vocab_size: Optional[int] = None
+    make_vocab_size_divisible_by: int = 128
     # distributed-data-parallel / optimizer settings read by the planner
     ddp_bucket_size: Optional[int] = None
     overlap_grad_reduce: bool = False
@@ -129,6 +132,19 @@ class ModelSpec:
         out.append(ParamDef("output_layer.weight", (self.padded_vocab_size, self.hidden_size), True, 0))
         return out
 
+    def padded_vocab_for_tp(self, tp: int) -> int:
+        """Megatron's padded vocabulary at TP size ``tp`` (multiple of divisible_by * tp)."""
+        if self.vocab_size is None:
+            raise ValueError("vocab_size is not set")
+        return _pad_vocab(self.vocab_size, self.make_vocab_size_divisible_by * tp)
+
+    def with_padded_vocab(self, padded_vocab_size: int) -> "ModelSpec":
+        from dataclasses import replace
+
+        if self.vocab_size is not None and padded_vocab_size < self.vocab_size:
+            raise ValueError("padded vocabulary smaller than the vocabulary")
+        return replace(self, padded_vocab_size=padded_vocab_size)
+
     def num_params(self) -> int:
         tot = 0
         for p in self.embedding_params() + self.output_params():
@@ -166,7 +182,7 @@ def llama2_7b() -> ModelSpec:
 
 def llama3_8b() -> ModelSpec:
     return ModelSpec(name="llama3-8b", num_layers=32, hidden_size=4096, num_attention_heads=32,
-                     num_query_groups=8, ffn_hidden_size=14336,
+                     num_query_groups=8, ffn_hidden_size=14336, vocab_size=128256,
                      padded_vocab_size=_pad_vocab(128256, 128 * 2), overlap_grad_reduce=True)
 
 

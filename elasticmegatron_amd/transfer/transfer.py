@@ -44,6 +44,19 @@ class CompiledPlan:
         return self.payload_bytes + self.read_bytes
 
 
+def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
+    """The model the reference would run a switch in: it keeps the padded vocabulary fixed
+    (virtual_param.py:480-481), so a re-padding switch is priced in whichever of the two
+    models both TP sizes divide; None when neither does."""
+    if src.space is dst.space:
+        return src.space
+    tps = (src.strategy.tensor_model_parallel_size, dst.strategy.tensor_model_parallel_size)
+    for space in (src.space, dst.space):
+        if all(space.spec.padded_vocab_size % t == 0 for t in tps):
+            return space
+    return None
+
+
 class TransferManager:
     """Builds, caches and runs copy plans between device-resident training states."""
 
@@ -74,7 +87,9 @@ class TransferManager:
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
         if kind == "transfer":
-            comm = max(reference_comm_bytes(src.space, src.strategy, dst.strategy).values(), default=0)
+            space = _fixed_padding_space(src, dst)
+            comm = max(reference_comm_bytes(space, src.strategy, dst.strategy).values(), default=0) \
+                if space is not None else 0
         elif kind == "backup_up":  # every rank joins the broadcast of its whole shard (transfer.py:377-388)
             comm = max(dst.rank_numel) * FP32_TENSORS_BYTES
         else:  # param_migrate is a local copy (training_state.py:40-60)

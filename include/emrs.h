@@ -66,13 +66,14 @@ extern "C" {
 
 /* emrs_segment flags */
 #define EMRS_SEG_CAST_BF16 1u /* fp32 segment that also writes its values as bf16 to aux */
+#define EMRS_SEG_ZERO_FILL 2u /* write zeros instead of copying: the source is not read */
 
 /* One strided copy.  Units: elements of elem_bytes bytes. */
 typedef struct emrs_segment {
   uint32_t src_buf;    /* index into the src_bases passed at execution */
   uint32_t dst_buf;    /* index into the dst_bases passed at execution */
   uint32_t elem_bytes; /* 1, 2, 4 or 8 */
-  uint32_t flags;      /* 0 or EMRS_SEG_CAST_BF16 */
+  uint32_t flags;      /* 0, EMRS_SEG_CAST_BF16, EMRS_SEG_ZERO_FILL or both */
   uint64_t src_off;    /* first element of row 0 in the source buffer */
   uint64_t dst_off;    /* first element of row 0 in the destination buffer */
   uint64_t len;        /* elements per row */
@@ -98,8 +99,8 @@ typedef struct emrs_plan_stats {
   uint64_t n_device_segments; /* after alignment splitting */
   uint64_t payload_bytes;   /* bytes written per execution, bf16 casts included */
   uint64_t read_bytes;      /* bytes read per execution */
-  uint64_t vector_bytes;    /* bytes read with 16-byte accesses */
-  uint64_t scalar_bytes;    /* bytes read element by element */
+  uint64_t vector_bytes;    /* bytes written through 16-byte units (bf16 images excluded) */
+  uint64_t scalar_bytes;    /* bytes written element by element (bf16 images excluded) */
   uint64_t n_chunks;        /* work chunks per execution */
   uint32_t n_src_bufs;
   uint32_t n_dst_bufs;
@@ -154,8 +155,11 @@ typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
                              0 (default): as many as can be resident at once */
   uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
-  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 1) */
-  uint32_t reserved;
+  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 1;
+                             applies only when run is 0) */
+  uint32_t run;           /* 0: each workgroup copies one contiguous run of chunks;
+                             N > 0: chunks are dealt out round-robin in runs of N, capped at a
+                             quarter of a workgroup's share (default 4) */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);

@@ -4,6 +4,12 @@ Independent of any plan: a TP-local element's full-tensor index follows from
 Megatron's partitioning (contiguous chunks along the partition dim; a fused
 SwiGLU fc1 holds [W_t; V_t], resharding_metadata.py:98-178), and its value
 from the seeded generator.
+
+Re-padding the vocabulary (a switch between two padded vocabulary sizes,
+which the reference does not have: virtual_param.py:480-481 keeps it fixed)
+is pinned by an invariant rather than by the reference: row r of the
+embedding and output layer keeps its values while r is below the source's
+padded size, and rows past it are zero in every tensor.
 """
 
 import numpy as np
@@ -39,10 +45,24 @@ def value_id(p):
     return 0 if (p["shared"] and p["where"] == "out") else p["id"]
 
 
-def piece_values(seed, p, T, t, lo, hi):
-    """{kind: array} for local elements [lo, hi) of TP rank t at TP size T."""
+VOCAB_PARAMS = ("embedding.word_embeddings.weight", "output_layer.weight")
+
+
+def _values(seed, p, kind, f, vocab_rows):
+    v = synth.values(seed, value_id(p), kind, f)
+    if vocab_rows is not None and p["name"] in VOCAB_PARAMS:
+        v = np.where(f // p["shape"][1] < vocab_rows, v, np.zeros((), dtype=v.dtype))
+    return v
+
+
+def piece_values(seed, p, T, t, lo, hi, vocab_rows=None):
+    """{kind: array} for local elements [lo, hi) of TP rank t at TP size T.
+
+    ``vocab_rows``: rows of the vocabulary parameters at and past it are zero
+    (the new padding rows of a re-padded destination).
+    """
     f = full_index(p, T, t, np.arange(lo, hi))
-    return {k: synth.values(seed, value_id(p), k, f) for k in ("main", "exp_avg", "exp_avg_sq")}
+    return {k: _values(seed, p, k, f, vocab_rows) for k in ("main", "exp_avg", "exp_avg_sq")}
 
 
 def shard_key(p, strat, hp, t):
@@ -52,7 +72,7 @@ def shard_key(p, strat, hp, t):
     return ("expert", s, ep_rank(p, strat, hp.num_experts), t)
 
 
-def world(inv, hp, strat, seed, params=None):
+def world(inv, hp, strat, seed, params=None, vocab_rows=None):
     """({(rank, pid): {kind: array}}, {(shard key, pid): bf16 bits}) of a layout."""
     dist = dp_distributions(inv, strat, hp)
     fp32, bf16 = {}, {}
@@ -71,8 +91,8 @@ def world(inv, hp, strat, seed, params=None):
                         g = s * (strat.dp * strat.cp * strat.tp) + (inst * strat.pdp + r) * strat.tp + t
                     else:
                         g = global_rank(strat, s, r, e, t)
-                    fp32[(g, p["id"])] = piece_values(seed, p, T, t, lo, hi)
+                    fp32[(g, p["id"])] = piece_values(seed, p, T, t, lo, hi, vocab_rows)
             n = int(np.prod(local_shape(p, T)))
-            bf16[(shard_key(p, strat, hp, t), p["id"])] = synth.values(
-                seed, value_id(p), "param", full_index(p, T, t, np.arange(n)))
+            bf16[(shard_key(p, strat, hp, t), p["id"])] = _values(
+                seed, p, "param", full_index(p, T, t, np.arange(n)), vocab_rows)
     return fp32, bf16

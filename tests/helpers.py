@@ -90,7 +90,10 @@ def execute_numpy(table, src, dst):
     for s in table:
         a, b = src[int(s["src_buf"])], dst[int(s["dst_buf"])]
         so, do, n, rows = int(s["src_off"]), int(s["dst_off"]), int(s["len"]), int(s["rows"])
-        vals = _view(a, so, rows, n, int(s["src_stride"])).copy()
+        if int(s["flags"]) & 2:  # zero fill
+            vals = np.zeros((rows, n) if rows > 1 else n, dtype=b.dtype)
+        else:
+            vals = _view(a, so, rows, n, int(s["src_stride"])).copy()
         _view(b, do, rows, n, int(s["dst_stride"]))[...] = vals
         if int(s["flags"]) & 1:
             aux = dst[int(s["aux_buf"])]
@@ -147,3 +150,19 @@ def small_llama2_tied():
 
 SMALL_CASES.append(("llama2_tied_pp1_pp2_pp4_tp2pp1",
                     small_llama2_tied, [PS(8, 1, 1), PS(8, 1, 2), PS(8, 2, 4), PS(8, 2, 1)]))
+
+
+# Vocabulary re-padding switches: (spec factory, vocab size, src strategy, dst strategy).
+REPAD_CASES = [
+    (small_llama3, 2300, PS(8, 2, 2), PS(8, 4, 1)),        # 2304 -> 2560, PP merge
+    (small_llama3, 2300, PS(8, 4, 1), PS(8, 2, 2)),        # 2560 -> 2304, dropped rows not read
+    (small_llama3, 1100, PS(8, 1, 1), PS(8, 2, 1)),        # 1152 -> 1280
+    (small_llama2_tied, 900, PS(8, 1, 2), PS(8, 4, 1)),    # tied output layer, 1024 at both sizes
+    (small_llama2_tied, 1100, PS(8, 2, 2), PS(8, 4, 2)),   # tied, 1280 -> 1536, output at PP 1
+]
+
+
+def repad_spaces(spec, tps):
+    """Virtual models of ``spec`` at Megatron's padded vocabulary for each TP size."""
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    return [build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(t))) for t in tps]

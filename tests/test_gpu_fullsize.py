@@ -24,6 +24,7 @@ SEED = 1234
 CASES = [
     pytest.param(ms.llama2_7b, PS(8, 1, 1), PS(8, 4, 1), id="llama2-7b-tp1dp8-tp4dp2"),
     pytest.param(ms.llama3_8b, PS(8, 2, 2), PS(8, 4, 1), id="llama3-8b-tp2pp2dp2-tp4pp1dp2"),
+    pytest.param(ms.llama3_8b, PS(8, 2, 2), PS(8, 4, 1), True, id="llama3-8b-tp2pp2dp2-tp4pp1dp2-repad"),
     pytest.param(ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4),
                  PS(8, 1, 1, expert_model_parallel_size=8), id="mixtral-4l-ep4-ep8"),
     pytest.param(ms.llama2_7b, PS(8, 1, 1), PS(6, 1, 1), id="llama2-7b-dp8-dp6"),
@@ -38,15 +39,22 @@ def _release():
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("factory,src,dst", CASES)
-def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst):
+@pytest.mark.parametrize("factory,src,dst,repad", [p if len(p.values) == 4 else
+                                                   pytest.param(*p.values, False, id=p.id) for p in CASES])
+def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
     spec = factory()
-    print(f"case {spec.name}: {src} -> {dst}", flush=True)
+    print(f"case {spec.name}: {src} -> {dst} repad {repad}", flush=True)
     backup = PS.is_redundant_backup(src, dst)
     kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
     back_kind = "transfer" if backup is None else ("backup_down" if backup else "backup_up")
-    space = build_virtual_model(spec)
-    ls, ld = space.layout(src), space.layout(dst)
+    if repad:  # Megatron's padded vocabulary at each TP size; new padding rows are zero
+        ls, ld = (build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(
+            s.tensor_model_parallel_size))).layout(s) for s in (src, dst))
+        assert ld.space.spec.padded_vocab_size > ls.space.spec.padded_vocab_size
+    else:
+        space = build_virtual_model(spec)
+        ls, ld = space.layout(src), space.layout(dst)
+    vocab_rows = ls.space.spec.padded_vocab_size if repad else None
     tm = TransferManager()
     fwd = tm.compile(ls, ld, kind)
     rev = tm.compile(ld, ls, back_kind)
@@ -56,7 +64,7 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst):
         b = TrainingState.allocate(ld, gpu_device, param=a.param if backup is not None else None)
         a.fill_synthetic(SEED)
         tm.execute(fwd, a, b)
-        bad, first = b.verify_synthetic(SEED)
+        bad, first = b.verify_synthetic(SEED, vocab_rows=vocab_rows)
         assert bad == 0, first
         # Round trip into fresh storage: must reproduce every source element.
         param = a.param

@@ -19,8 +19,8 @@ from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.transfer import TransferManager
 from oracle import model
 from oracle import transfer as oracle1
-from tests.helpers import (SEED, SMALL_CASES, bf16_rne_bits, compare, extract, new_arenas, piece_fill_numpy,
-                           strat)
+from tests.helpers import (REPAD_CASES, SEED, SMALL_CASES, bf16_rne_bits, compare, extract, new_arenas,
+                           piece_fill_numpy, repad_spaces, strat)
 
 pytestmark = pytest.mark.gpu
 
@@ -86,6 +86,79 @@ def test_kernel_matches_oracle1(gpu_device, factory, src, dst, bf16_source):
     assert bad == 0, first
 
 
+@pytest.mark.parametrize("factory,vocab,src,dst", REPAD_CASES)
+@pytest.mark.parametrize("bf16_source", ["cast", "copy"])
+def test_repad_kernel_matches_invariant(gpu_device, factory, vocab, src, dst, bf16_source):
+    """Vocabulary re-padding: kept rows carry their values, new padding rows are zero."""
+    from dataclasses import replace
+    from oracle import canonical
+
+    spec = replace(factory(), vocab_size=vocab)
+    sa, sb = repad_spaces(spec, (src.tensor_model_parallel_size, dst.tensor_model_parallel_size))
+    print(f"case {spec.name} vocab {sa.spec.padded_vocab_size} -> {sb.spec.padded_vocab_size} "
+          f"{src} -> {dst} bf16 {bf16_source}", flush=True)
+    ls, ld = sa.layout(src), sb.layout(dst)
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    for t in b.arenas():
+        t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
+    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, a, b)
+    got32, gotbf = extract(ld, _host_arenas(b))
+    want32, wantbf = canonical.world(model.inventory(sb.spec), sb.spec, strat(dst), SEED,
+                                     vocab_rows=sa.spec.padded_vocab_size)
+    assert compare(got32, gotbf, want32, wantbf) == []
+    bad, first = b.verify_synthetic(SEED, vocab_rows=sa.spec.padded_vocab_size)
+    assert bad == 0, first
+
+
+def test_manager_repad_round_trip(gpu_device):
+    """ElasticMegatronManager(repad_vocab=True): TP2PP2 -> TP4PP1 -> TP2PP2 is the identity."""
+    from dataclasses import replace
+    from elasticmegatron_amd import ElasticMegatronManager
+    from tests.helpers import small_llama3
+
+    spec = replace(small_llama3(), vocab_size=2300)
+    seq = [dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=2),
+           dict(world_size=8, tensor_model_parallel_size=4, pipeline_model_parallel_size=1)]
+    mgr = ElasticMegatronManager(seq, spec, device=gpu_device, repad_vocab=True)
+    mgr.training_state.fill_synthetic(SEED)
+    st = mgr.reshard(new_parallel_strategy=seq[1])
+    assert st.layout.space.spec.padded_vocab_size == 2560
+    assert st.verify_synthetic(SEED, vocab_rows=2304)[0] == 0
+    st = mgr.reshard(new_parallel_strategy=seq[0])
+    assert st.layout.space.spec.padded_vocab_size == 2304
+    assert st.verify_synthetic(SEED)[0] == 0
+
+
+@pytest.mark.parametrize("tuning", [dict(run=0), dict(run=0, xcd_remap=False), dict(run=1), dict(run=64),
+                                    dict(blocks_per_cu=1), dict(nontemporal=False), dict(blocks_per_cu=3, run=7)])
+def test_launch_shape_does_not_change_results(gpu_device, tuning):
+    """Every launch shape of emrs_set_tuning writes the same bits."""
+    from elasticmegatron_amd.resharding.model_spec import tiny_llama2
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
+
+    print(f"case tuning {tuning}", flush=True)
+    space = build_virtual_model(tiny_llama2())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 4, 1))
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    outs = []
+    try:
+        for t in (dict(), tuning):
+            _native.set_tuning(**t)
+            b = TrainingState.allocate(ld, gpu_device)
+            for x in b.arenas():
+                x.fill_(0) if x.dtype != torch.float32 else x.fill_(float("nan"))
+            TransferManager(check_disjoint=True).transfer_optimizer_tensors(None, a, b)
+            outs.append(_host_arenas(b))
+    finally:
+        _native.set_tuning()
+    for x, y in zip(*outs):
+        assert np.array_equal(x, y)
+    assert _native.get_tuning().run == 4
+
+
 def _random_table(rng, n_segs, sizes):
     rows = []
     for _ in range(n_segs):
@@ -106,12 +179,15 @@ def _random_table(rng, n_segs, sizes):
             do = do - (do * eb) % 16 // eb + (so * eb) % 16 // eb
             do = max(0, min(do, nb[1] - dst_ext))
         cast = eb == 4 and rng.random() < 0.5
+        zero = 2 if rng.random() < 0.2 else 0  # zero fill: the source offset is ignored
+        if zero and rng.random() < 0.5:
+            so = int(rng.integers(0, 1 << 40))
         if cast:  # bf16 image into the second destination buffer
             aux_s = ln + int(rng.integers(0, 9)) if r > 1 else 0
             ao = int(rng.integers(0, sizes[1] // 2 - ((r - 1) * aux_s + ln)))
-            rows.append((0, 0, eb, 1, so, do, ln, r, ss, ds, 1, 0, ao, aux_s))
+            rows.append((0, 0, eb, 1 | zero, so, do, ln, r, ss, ds, 1, 0, ao, aux_s))
         else:
-            rows.append((0, 0, eb, 0, so, do, ln, r, ss, ds, 0, 0, 0, 0))
+            rows.append((0, 0, eb, zero, so, do, ln, r, ss, ds, 0, 0, 0, 0))
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
     return t
@@ -119,7 +195,7 @@ def _random_table(rng, n_segs, sizes):
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_random_segments_match_numpy(gpu_device, seed):
-    """Arbitrary element sizes, offsets and strides (scalar, split and vector paths).
+    """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills.
 
     Segments are applied in order and may overlap in the destination here, so
     each segment runs as its own plan and the numpy model applies the same
@@ -129,10 +205,11 @@ def test_random_segments_match_numpy(gpu_device, seed):
     nbytes = 1 << 20
     src_h = rng.integers(0, 256, nbytes, dtype=np.uint8)
     src = torch.from_numpy(src_h).to(gpu_device)
-    dst = torch.zeros(nbytes, dtype=torch.uint8, device=gpu_device)
-    aux = torch.zeros(nbytes, dtype=torch.uint8, device=gpu_device)
-    want = np.zeros(nbytes, dtype=np.uint8)
-    want_aux = np.zeros(nbytes, dtype=np.uint8)
+    fill = rng.integers(0, 256, nbytes, dtype=np.uint8)  # so that written zeros show
+    dst = torch.from_numpy(fill).to(gpu_device)
+    aux = torch.from_numpy(fill).to(gpu_device)
+    want = fill.copy()
+    want_aux = fill.copy()
     table = _random_table(rng, 40, (nbytes, nbytes))
     for s in table:
         one = np.array([s], dtype=SEGMENT_DTYPE)
@@ -144,10 +221,11 @@ def test_random_segments_match_numpy(gpu_device, seed):
         for r in range(int(s["rows"])):
             so = int(s["src_off"]) + r * int(s["src_stride"])
             do = int(s["dst_off"]) + r * int(s["dst_stride"])
-            b[do:do + int(s["len"])] = a[so:so + int(s["len"])]
-            if int(s["flags"]):
+            vals = np.zeros(int(s["len"]), dtype=b.dtype) if int(s["flags"]) & 2 else a[so:so + int(s["len"])]
+            b[do:do + int(s["len"])] = vals
+            if int(s["flags"]) & 1:
                 ao = int(s["aux_off"]) + r * int(s["aux_stride"])
-                want_aux.view(np.uint16)[ao:ao + int(s["len"])] = bf16_rne_bits(a[so:so + int(s["len"])])
+                want_aux.view(np.uint16)[ao:ao + int(s["len"])] = bf16_rne_bits(vals)
     torch.cuda.synchronize()
     assert np.array_equal(dst.cpu().numpy(), want)
     assert np.array_equal(aux.cpu().numpy(), want_aux)

@@ -59,7 +59,9 @@ def _seg(**kw):
     (dict(src_off=250, len=16), -2),
     (dict(dst_off=1, len=256), -2),
     (dict(rows=3, len=10, src_stride=200, dst_stride=10), -2),
-    (dict(flags=2), -1),
+    (dict(flags=4), -1),
+    (dict(flags=2, src_buf=1), -1),
+    (dict(flags=2, dst_off=1000, len=16), -2),
     (dict(reserved=1), -1),
     (dict(flags=1, elem_bytes=2), -1),
     (dict(flags=1, aux_buf=1), -1),
@@ -111,6 +113,22 @@ def test_plan_stats_classify_alignment():
     assert st.vector_bytes == 256 + 32 + 64 + 128
     assert st.scalar_bytes == 16 + 32 + 24 + 128
     assert st.n_segments == 7
+
+
+def test_zero_fill_reads_nothing():
+    """EMRS_SEG_ZERO_FILL: the source offset is ignored and no source byte is counted as read."""
+    rows = [
+        (0, 0, 4, 2, 10 ** 12, 0, 64, 1, 0, 0, 0, 0, 0, 0),        # zeros, vector path
+        (0, 0, 4, 3, 0, 100, 16, 2, 0, 20, 1, 0, 4, 24),           # zeros + bf16 zeros, 2-D
+        (0, 0, 2, 2, 0, 1000, 5, 1, 0, 0, 0, 0, 0, 0),             # 2-byte zeros, scalar path
+        (0, 0, 4, 0, 0, 200, 8, 1, 0, 0, 0, 0, 0, 0),              # an ordinary copy
+    ]
+    t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
+    t[:] = rows
+    st = _native.Plan(t, [64], [4096, 4096], check_disjoint=True).stats()
+    assert st.read_bytes == 32
+    assert st.payload_bytes == 256 + 128 + 64 + 10 + 32
+    assert st.n_segments == 4
 
 
 def test_empty_plan_and_no_device_errors():
