@@ -69,6 +69,7 @@ def parse():
     ap.add_argument("--workload", default="llama2-7b-tp1dp8-tp4dp2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip timing ElasticMegatronManager.reshard end to end")
     ap.add_argument("--placement-trials", type=int, default=0,
                     help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
@@ -248,12 +249,83 @@ def main():
             torch.cuda.synchronize()
             trials.append(round(e0.elapsed_time(e1) / 5, 3))
         out["config"]["placement_trials_ms"] = trials
-    del a, b
+    out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
+    del b
+    if not args.no_e2e:
+        a, out["config"]["reshard_e2e"] = reshard_end_to_end(a, spec, src, dst, repad, tm, args.no_verify)
+    del a
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def copy_ceiling(a, b, stream, traffic_gbps, reps=5):
+    """A plain contiguous copy, by the same kernel, from the source main arena to the destination
+    one: the copy speed of the very allocations the reshard ran on (physical placement moves
+    both together)."""
+    import numpy as np
+    import torch
+
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
+
+    n = min(a.main.numel(), b.main.numel())
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0, 0, 0, 0, 0)
+    plan = _native.Plan(t, [n * 4], [n * 4])
+    run = lambda: plan.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream)  # noqa: E731
+    for _ in range(2):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbps = 2 * n * 4 / (ms / 1e3) / 1e9
+    return {"gbps": round(gbps, 1), "bytes_per_launch": 2 * n * 4, "ms": round(ms, 4),
+            "what": "one contiguous copy of the main arena by copy_plan_kernel, same allocations",
+            "reshard_frac_of_copy": round(traffic_gbps / gbps, 4)}
+
+
+def reshard_end_to_end(a, spec, src, dst, repad, tm, no_verify, reps=3):
+    """ElasticMegatronManager.reshard wall time with the plan cached: allocation of the new
+    state, the launch, release of the old optimizer state.  Two warm-up round trips first."""
+    import logging
+
+    import torch
+
+    from elasticmegatron_amd import ElasticMegatronManager
+
+    log = logging.getLogger("bench.reshard")
+    log.propagate = False
+    log.addHandler(logging.NullHandler())
+    mgr = ElasticMegatronManager([src, dst], spec, training_state=a, repad_vocab=repad)
+    mgr.transfer_manager = tm
+    del a
+    wall, execu = [], []
+    for i in range(2 + reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        mgr.reshard(new_parallel_strategy=dst, logger=log)
+        torch.cuda.synchronize()
+        if i >= 2:
+            wall.append((time.perf_counter() - t0) * 1e3)
+            execu.append(mgr.last_transfer_ms)
+        if i < 1 + reps:
+            mgr.reshard(new_parallel_strategy=src, logger=log)
+    st = mgr.training_state
+    res = {"wall_ms": round(sorted(wall)[len(wall) // 2], 3), "executor_ms": round(sorted(execu)[len(execu) // 2], 3),
+           "reps": reps}
+    if not no_verify:
+        vocab_rows = mgr.space_for(src).spec.padded_vocab_size if repad else None
+        res["verified_bit_exact"] = st.verify_synthetic(SEED, vocab_rows=vocab_rows)[0] == 0
+    # Hand back a state laid out as the source for anything after this.
+    mgr.reshard(new_parallel_strategy=src, logger=log)
+    return mgr.training_state, res
 
 
 def copy_calibration(args, dev, stream):

@@ -56,29 +56,35 @@ class ElasticMegatronManager:
         self.model_spec = model_spec
         self.repad_vocab = repad_vocab
         self._spaces: Dict[int, VirtualParamSpace] = {}
+        cur = self.parallel_strategy_list[0]
+        if training_state is not None:
+            if training_state.parallel_strategy != cur:
+                raise ValueError("training_state does not use the first strategy of the list")
+            # Adopt the state's virtual model when it is the model this manager would build.
+            spec = training_state.layout.space.spec
+            if spec != self._spec_for(cur):
+                raise ValueError("training_state was laid out for another model")
+            self._spaces[spec.padded_vocab_size] = training_state.layout.space
         for s in self.parallel_strategy_list:
             self.space_for(s).build_model_virtual_params(s)
         self.transfer_manager = TransferManager()
         self.release_source = release_source
         self.last_transfer_ms = 0.0
-        cur = self.parallel_strategy_list[0]
         if training_state is None:
             training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device)
-        elif training_state.parallel_strategy != cur:
-            raise ValueError("training_state does not use the first strategy of the list")
-        elif training_state.layout.space is not self.space_for(cur):
-            raise ValueError("training_state was laid out for another model")
         self.training_state = training_state
+
+    def _spec_for(self, strategy: ParallelStrategy) -> ModelSpec:
+        pv = (self.model_spec.padded_vocab_for_tp(strategy.tensor_model_parallel_size) if self.repad_vocab
+              else self.model_spec.padded_vocab_size)
+        return self.model_spec if pv == self.model_spec.padded_vocab_size else self.model_spec.with_padded_vocab(pv)
 
     def space_for(self, strategy: ParallelStrategy) -> VirtualParamSpace:
         """The virtual model a strategy's state is laid out in (one per padded vocabulary size)."""
-        pv = (self.model_spec.padded_vocab_for_tp(strategy.tensor_model_parallel_size) if self.repad_vocab
-              else self.model_spec.padded_vocab_size)
-        space = self._spaces.get(pv)
+        spec = self._spec_for(strategy)
+        space = self._spaces.get(spec.padded_vocab_size)
         if space is None:
-            spec = self.model_spec if pv == self.model_spec.padded_vocab_size else \
-                self.model_spec.with_padded_vocab(pv)
-            space = self._spaces[pv] = build_virtual_model(spec)
+            space = self._spaces[spec.padded_vocab_size] = build_virtual_model(spec)
         return space
 
     @property

@@ -74,7 +74,7 @@ class TransferManager:
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                 include_bf16: bool = True) -> CompiledPlan:
-        key = (src.strategy, dst.strategy, kind, include_bf16, self.bf16_source)
+        key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16, self.bf16_source)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
