@@ -70,6 +70,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip timing ElasticMegatronManager.reshard end to end")
+    ap.add_argument("--no-copy-ceiling", action="store_true", help="skip the plain-copy reference launch")
     ap.add_argument("--placement-trials", type=int, default=0,
                     help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
@@ -249,7 +250,8 @@ def main():
             torch.cuda.synchronize()
             trials.append(round(e0.elapsed_time(e1) / 5, 3))
         out["config"]["placement_trials_ms"] = trials
-    out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
+    if not args.no_copy_ceiling:
+        out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
     del b
     if not args.no_e2e:
         a, out["config"]["reshard_e2e"] = reshard_end_to_end(a, spec, src, dst, repad, tm, args.no_verify)
