@@ -250,6 +250,19 @@ def main():
             torch.cuda.synchronize()
             trials.append(round(e0.elapsed_time(e1) / 5, 3))
         out["config"]["placement_trials_ms"] = trials
+    if not args.no_verify:
+        # The plan's own check of the destination against the source (emrs_plan_compare), timed
+        # on its second call, when its grouped plan is built and cached.
+        tm.verify(a, b, kind)
+        torch.cuda.synchronize()
+        t_v = time.perf_counter()
+        report = tm.verify(a, b, kind)
+        v_ms = (time.perf_counter() - t_v) * 1e3
+        out["config"]["plan_verification"] = {"bit_exact": report.bit_exact, "elements": report.elements,
+                                              "wall_ms": round(v_ms, 3)}
+        if not report.bit_exact:
+            print(f"[bench] plan verification FAILED: {report.lines()[:3]}", file=sys.stderr)
+            return 3
     if not args.no_copy_ceiling:
         out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
     del b

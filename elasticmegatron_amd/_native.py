@@ -36,8 +36,13 @@ EMRS_MAX_BUFFERS = 128
 EXPORTS = (
     "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
     "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
-    "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify",
+    "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare",
 )
+
+# struct emrs_compare_stats
+COMPARE_DTYPE = np.dtype([("elements", "<u8"), ("mismatches", "<u8"), ("nonfinite", "<u8"), ("reserved", "<u8"),
+                          ("sum_sq_diff", "<f8"), ("sum_sq_expected", "<f8"), ("max_abs_diff", "<f4"),
+                          ("max_rel_diff", "<f4"), ("reserved2", "<u8")])
 
 
 class EmrsError(RuntimeError):
@@ -94,6 +99,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_synth_fill.argtypes = [P, U64, P, P, U32, U64, P]
     lib.emrs_synth_verify.restype = I
     lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
+    lib.emrs_plan_compare.restype = I
+    lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
     if lib.emrs_abi_version() != 1:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
@@ -161,6 +168,33 @@ class Plan:
         rc = load().emrs_plan_execute(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
                                       ctypes.c_void_p(int(stream)))
         _check(rc, "emrs_plan_execute")
+
+    def compare(self, src_ptrs: Sequence[int], dst_ptrs: Sequence[int], groups: Optional[np.ndarray] = None,
+                aux_groups: Optional[np.ndarray] = None, n_groups: int = 1, stream: int = 0) -> np.ndarray:
+        """emrs_plan_compare: per group, how the destination differs from what the plan writes.
+
+        ``groups`` / ``aux_groups`` hold one group id per input segment.
+        Returns ``n_groups`` records of :data:`COMPARE_DTYPE`.  Waits for ``stream``.
+        """
+        if len(src_ptrs) != self.n_src or len(dst_ptrs) != self.n_dst:
+            raise ValueError("wrong number of base pointers")
+        n_in = self.stats().n_segments
+        arrs = []
+        for g in (groups, aux_groups):
+            if g is None:
+                arrs.append(None)
+                continue
+            g = np.ascontiguousarray(g, dtype=np.uint32)
+            if g.shape != (n_in,):
+                raise ValueError(f"need one group id per segment ({n_in})")
+            arrs.append(g)
+        out = np.zeros(max(1, n_groups), dtype=COMPARE_DTYPE)
+        rc = load().emrs_plan_compare(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
+                                      arrs[0].ctypes.data if arrs[0] is not None and n_in else None,
+                                      arrs[1].ctypes.data if arrs[1] is not None and n_in else None,
+                                      int(n_groups), out.ctypes.data, ctypes.c_void_p(int(stream)))
+        _check(rc, "emrs_plan_compare")
+        return out
 
     def close(self) -> None:
         if getattr(self, "_handle", None):

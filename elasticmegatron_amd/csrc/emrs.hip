@@ -88,7 +88,7 @@ struct DevSeg {
   uint8_t src_buf;
   uint8_t dst_buf;
   uint8_t aux_buf;
-  uint8_t pad;
+  uint8_t elem_log2;     // element size of the input segment (read only by the compare kernel)
 };
 static_assert(sizeof(DevSeg) == 64, "DevSeg layout");
 
@@ -355,6 +355,7 @@ int current_device(int *dev, int *cus, int *resident_nt, int *resident_t) {
 
 struct emrs_plan {
   std::vector<DevSeg> segs;
+  std::vector<uint32_t> origin;              // input segment of each device segment
   uint64_t n_chunks = 0;
   std::vector<uint64_t> src_bytes, dst_bytes;
   std::vector<uint8_t> src_used, dst_used;  // buffers referenced by a non-empty segment
@@ -376,6 +377,9 @@ struct Aux {
 
 struct Builder {
   std::vector<DevSeg> out;
+  std::vector<uint32_t> origin;  // input segment of each pushed segment
+  uint32_t cur_origin = 0;       // input segment being emitted
+  uint8_t cur_elem_log2 = 0;     // its element size
   uint64_t chunks = 0;
   uint64_t vec_bytes = 0, scalar_bytes = 0;
 
@@ -431,9 +435,11 @@ struct Builder {
     d.aux_buf = (uint8_t)(ax.on ? ax.buf : dbuf);
     d.aux_off = ax.on ? aoff : 0;
     d.aux_stride = ax.on && rows > 1 ? astride : 0;
+    d.elem_log2 = cur_elem_log2;
     const uint64_t units = (uint64_t)len * rows;
     chunks += (units + kChunkUnits - 1) / kChunkUnits;
     out.push_back(d);
+    origin.push_back(cur_origin);
   }
 };
 
@@ -488,6 +494,270 @@ int check_disjoint(const emrs_segment *segs, uint64_t n_segs) {
   return EMRS_OK;
 }
 
+// Base pointers of an execution or comparison: copied into kernel-argument
+// tables and checked (only buffers that some segment references).
+int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *dst_bases, Bases *sb, Bases *db) {
+  const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
+  if ((ns && !src_bases) || (nd && !dst_bases))
+    return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
+  // Only buffers that some segment references are checked: an unreferenced
+  // buffer may be NULL or alias anything.
+  *sb = Bases{};
+  *db = Bases{};
+  for (uint32_t i = 0; i < ns; ++i) {
+    sb->p[i] = static_cast<char *>(src_bases[i]);
+    if (!plan->src_used[i]) continue;
+    if (!sb->p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
+    if (reinterpret_cast<uintptr_t>(sb->p[i]) % 16)
+      return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
+  }
+  for (uint32_t i = 0; i < nd; ++i) {
+    db->p[i] = static_cast<char *>(dst_bases[i]);
+    if (!plan->dst_used[i]) continue;
+    if (!db->p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
+    if (reinterpret_cast<uintptr_t>(db->p[i]) % 16)
+      return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
+  }
+  auto overlap = [](uintptr_t a0, uint64_t an, uintptr_t b0, uint64_t bn) {
+    return an && bn && a0 < b0 + bn && b0 < a0 + an;
+  };
+  for (uint32_t j = 0; j < nd; ++j) {
+    if (!plan->dst_used[j]) continue;
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(db->p[j]);
+    for (uint32_t i = 0; i < ns; ++i)
+      if (plan->src_used[i] &&
+          overlap(reinterpret_cast<uintptr_t>(sb->p[i]), plan->src_bytes[i], d0, plan->dst_bytes[j]))
+        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
+    for (uint32_t k = j + 1; k < nd; ++k)
+      if (plan->dst_used[k] &&
+          overlap(d0, plan->dst_bytes[j], reinterpret_cast<uintptr_t>(db->p[k]), plan->dst_bytes[k]))
+        return fail(EMRS_ERR_ALIAS, "two destination buffers overlap");
+  }
+  return EMRS_OK;
+}
+
+// The plan's segment table on device `dev`, uploaded on first use.
+int device_table(emrs_plan *plan, int dev, DevSeg **table) {
+  std::lock_guard<std::mutex> lk(plan->mu);
+  if ((int)plan->dev_tables.size() <= dev) plan->dev_tables.resize(dev + 1, nullptr);
+  if (!plan->dev_tables[dev]) {
+    const size_t bytes = plan->segs.size() * sizeof(DevSeg);
+    DevSeg *t = nullptr;
+    hipError_t e = hipMalloc(&t, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(plan table)");
+    e = hipMemcpy(t, plan->segs.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(t);
+      return hip_fail(e, "hipMemcpy(plan table)");
+    }
+    plan->dev_tables[dev] = t;
+  }
+  *table = plan->dev_tables[dev];
+  return EMRS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Compare kernel
+// ---------------------------------------------------------------------------
+
+// Device accumulators of one group (emrs_compare_stats minus the element
+// count, which the host knows).  Maxima are non-negative floats, ordered as
+// their bit patterns.
+struct GroupAcc {
+  unsigned long long mismatches;
+  unsigned long long nonfinite;
+  double sum_sq_diff;
+  double sum_sq_expected;
+  unsigned int max_abs_bits;
+  unsigned int max_rel_bits;
+};
+
+struct LaneAcc {
+  uint32_t mismatches = 0, nonfinite = 0;
+  double sq_diff = 0.0, sq_exp = 0.0;
+  float max_abs = 0.0f, max_rel = 0.0f;
+};
+
+__device__ __forceinline__ void cmp_float(LaneAcc &a, uint32_t e_bits, uint32_t g_bits) {
+  const float e = __uint_as_float(e_bits), g = __uint_as_float(g_bits);
+  if (fabsf(e) <= 3.402823466e38f) a.sq_exp += (double)e * (double)e;
+  if (e_bits == g_bits) return;
+  ++a.mismatches;
+  const float d = fabsf(g - e);
+  if (!(d <= 3.402823466e38f)) {  // NaN or infinite difference
+    ++a.nonfinite;
+    return;
+  }
+  a.sq_diff += (double)d * (double)d;
+  a.max_abs = fmaxf(a.max_abs, d);
+  a.max_rel = fmaxf(a.max_rel, d / (fabsf(e) + 1e-12f));
+}
+
+// Compare one unit (1, 2, 4, 8 or 16 bytes held in w[0..3]) element by element.
+__device__ __forceinline__ void cmp_words(LaneAcc &a, const uint32_t *e, const uint32_t *g, uint32_t unit_bytes,
+                                          uint32_t elem_log2) {
+  switch (elem_log2) {
+    case 2:  // fp32
+      for (uint32_t k = 0; k < unit_bytes / 4; ++k) cmp_float(a, e[k], g[k]);
+      break;
+    case 1:  // bf16
+      for (uint32_t k = 0; k < unit_bytes / 2; ++k) {
+        const uint32_t sh = (k & 1) * 16;
+        cmp_float(a, ((e[k >> 1] >> sh) & 0xffffu) << 16, ((g[k >> 1] >> sh) & 0xffffu) << 16);
+      }
+      break;
+    case 0:  // bytes: bits only
+      for (uint32_t k = 0; k < unit_bytes; ++k) {
+        const uint32_t sh = (k & 3) * 8;
+        a.mismatches += ((e[k >> 2] >> sh) & 0xffu) != ((g[k >> 2] >> sh) & 0xffu);
+      }
+      break;
+    default:  // 8-byte elements: bits only
+      for (uint32_t k = 0; k < unit_bytes / 8; ++k)
+        a.mismatches += (e[2 * k] != g[2 * k]) || (e[2 * k + 1] != g[2 * k + 1]);
+      break;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void words_of(const T &v, uint32_t *w) {
+  if constexpr (sizeof(T) == 16) {
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (sizeof(T) == 8) {
+    w[0] = (uint32_t)v; w[1] = (uint32_t)(v >> 32);
+  } else {
+    w[0] = (uint32_t)v;
+  }
+}
+
+template <typename A>
+__device__ __forceinline__ void aux_words_of(const A &v, uint32_t *w) {
+  if constexpr (sizeof(A) == 8) {
+    w[0] = v.x; w[1] = v.y;
+  } else {
+    w[0] = (uint32_t)v;
+  }
+}
+
+// Compare units [u0, u_end) of segment s; with a cast, also its bf16 image.
+template <typename T>
+__device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase, const char *dbase,
+                                              const char *abase, uint32_t u0, uint32_t u_end, LaneAcc &m,
+                                              LaneAcc &x) {
+  typedef typename std::conditional<sizeof(T) == 16 || sizeof(T) == 4, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
+  const T *src = reinterpret_cast<const T *>(sbase);
+  const T *dst = reinterpret_cast<const T *>(dbase);
+  const A *aux = reinterpret_cast<const A *>(abase);
+  for (uint32_t j = 0; j < kUnroll; ++j) {
+    const uint32_t u = u0 + j * kThreads + threadIdx.x;
+    if (u >= u_end) break;
+    uint64_t so = s.src_off + u, dof = s.dst_off + u, ao = s.aux_off + u;
+    if (s.rows > 1) {
+      const uint32_t row = magic_div(u, s.magic, s.sh1, s.sh2), col = u - row * s.len;
+      so = s.src_off + (uint64_t)row * s.src_stride + col;
+      dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
+      ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
+    }
+    const T e = (s.cast & 2) ? T{} : src[so];
+    const T g = dst[dof];
+    uint32_t ew[4] = {0, 0, 0, 0}, gw[4] = {0, 0, 0, 0};
+    words_of(e, ew);
+    words_of(g, gw);
+    cmp_words(m, ew, gw, (uint32_t)sizeof(T), s.elem_log2);
+    if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
+      if (s.cast & 1) {
+        uint32_t ea[2] = {0, 0}, ga[2] = {0, 0};
+        aux_words_of(C::cast(e), ea);
+        aux_words_of(aux[ao], ga);
+        cmp_words(x, ea, ga, (uint32_t)sizeof(A), 1);
+      }
+    }
+  }
+}
+
+// Sum / max over the workgroup; the result is valid in thread 0.
+__device__ void block_reduce(LaneAcc &a, double *lds_d, uint32_t *lds_u, float *lds_f) {
+  for (int off = 32; off > 0; off >>= 1) {
+    a.mismatches += __shfl_xor(a.mismatches, off, 64);
+    a.nonfinite += __shfl_xor(a.nonfinite, off, 64);
+    a.sq_diff += __shfl_xor(a.sq_diff, off, 64);
+    a.sq_exp += __shfl_xor(a.sq_exp, off, 64);
+    a.max_abs = fmaxf(a.max_abs, __shfl_xor(a.max_abs, off, 64));
+    a.max_rel = fmaxf(a.max_rel, __shfl_xor(a.max_rel, off, 64));
+  }
+  const uint32_t wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  __syncthreads();
+  if (lane == 0) {
+    lds_u[2 * wave] = a.mismatches;
+    lds_u[2 * wave + 1] = a.nonfinite;
+    lds_d[2 * wave] = a.sq_diff;
+    lds_d[2 * wave + 1] = a.sq_exp;
+    lds_f[2 * wave] = a.max_abs;
+    lds_f[2 * wave + 1] = a.max_rel;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (uint32_t w = 1; w < kThreads / 64; ++w) {
+      a.mismatches += lds_u[2 * w];
+      a.nonfinite += lds_u[2 * w + 1];
+      a.sq_diff += lds_d[2 * w];
+      a.sq_exp += lds_d[2 * w + 1];
+      a.max_abs = fmaxf(a.max_abs, lds_f[2 * w]);
+      a.max_rel = fmaxf(a.max_rel, lds_f[2 * w + 1]);
+    }
+  }
+}
+
+__device__ void flush(const LaneAcc &a, GroupAcc *g) {
+  if (a.mismatches) atomicAdd(&g->mismatches, (unsigned long long)a.mismatches);
+  if (a.nonfinite) atomicAdd(&g->nonfinite, (unsigned long long)a.nonfinite);
+  if (a.sq_diff != 0.0) atomicAdd(&g->sum_sq_diff, a.sq_diff);
+  if (a.sq_exp != 0.0) atomicAdd(&g->sum_sq_expected, a.sq_exp);
+  if (a.max_abs > 0.0f) atomicMax(&g->max_abs_bits, __float_as_uint(a.max_abs));
+  if (a.max_rel > 0.0f) atomicMax(&g->max_rel_bits, __float_as_uint(a.max_rel));
+}
+
+// One workgroup per chunk, grid-stride over the chunks.  No early exit: every
+// thread reaches every barrier.
+__global__ __launch_bounds__(kThreads) void compare_plan_kernel(
+    const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
+    uint32_t n_segs, uint64_t n_chunks, Bases src, Bases dst, GroupAcc *__restrict__ acc) {
+  __shared__ double lds_d[2 * kThreads / 64];
+  __shared__ uint32_t lds_u[2 * kThreads / 64];
+  __shared__ float lds_f[2 * kThreads / 64];
+  for (uint64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    uint32_t lo = 0, hi = n_segs - 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (segs[mid].chunk_begin <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    const DevSeg s = segs[lo];
+    const uint32_t total = s.len * s.rows;
+    const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
+    const uint32_t u_end = min(u0 + kChunkUnits, total);
+    const char *sb = src.p[s.src_buf];
+    const char *db = dst.p[s.dst_buf];
+    const char *ab = dst.p[s.aux_buf];
+    LaneAcc m, x;
+    switch (s.unit_log2) {
+      case 4: compare_chunk<u32x4>(s, sb, db, ab, u0, u_end, m, x); break;
+      case 3: compare_chunk<uint64_t>(s, sb, db, ab, u0, u_end, m, x); break;
+      case 2: compare_chunk<uint32_t>(s, sb, db, ab, u0, u_end, m, x); break;
+      case 1: compare_chunk<uint16_t>(s, sb, db, ab, u0, u_end, m, x); break;
+      default: compare_chunk<uint8_t>(s, sb, db, ab, u0, u_end, m, x); break;
+    }
+    block_reduce(m, lds_d, lds_u, lds_f);
+    if (threadIdx.x == 0) flush(m, acc + groups[lo]);
+    if (s.cast & 1) {  // uniform across the workgroup
+      block_reduce(x, lds_d, lds_u, lds_f);
+      if (threadIdx.x == 0) flush(x, acc + aux_groups[lo]);
+    }
+    __syncthreads();  // the LDS slots are reused by the next chunk
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -517,6 +787,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   if ((n_src_bufs && !src_buf_bytes) || (n_dst_bufs && !dst_buf_bytes))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "buffer size array is NULL");
   if (flags & ~EMRS_PLAN_CHECK_DISJOINT) return fail(EMRS_ERR_INVALID_ARGUMENT, "unknown flags");
+  if (n_segs > 0xffffffffull) return fail(EMRS_ERR_INVALID_ARGUMENT, "more than 2^32 - 1 segments");
 
   Builder bld;
   bld.out.reserve(n_segs);
@@ -554,6 +825,8 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     if (cast) dst_used[s.aux_buf] = 1;
 
     const uint64_t eb = s.elem_bytes;
+    bld.cur_origin = (uint32_t)i;
+    bld.cur_elem_log2 = (uint8_t)lg;
     // A zero fill has no source: align its phantom source with the destination.
     const uint64_t so = zero ? s.dst_off * eb : s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
     const uint64_t ds = s.rows > 1 ? s.dst_stride * eb : 0, ss = zero ? ds : (s.rows > 1 ? s.src_stride * eb : 0);
@@ -599,9 +872,11 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     if (rc) return rc;
   }
 
+  if (bld.out.size() > 0xffffffffull) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan needs more than 2^32 - 1 device segments");
   emrs_plan *p = new (std::nothrow) emrs_plan;
   if (!p) return fail(EMRS_ERR_INVALID_ARGUMENT, "out of host memory");
   p->segs = std::move(bld.out);
+  p->origin = std::move(bld.origin);
   p->n_chunks = bld.chunks;
   p->src_bytes.assign(src_buf_bytes, src_buf_bytes + n_src_bufs);
   p->dst_bytes.assign(dst_buf_bytes, dst_buf_bytes + n_dst_bufs);
@@ -630,60 +905,17 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
                       void *stream) {
   g_last_error.clear();
   if (!plan) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan is NULL");
-  const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
-  if ((ns && !src_bases) || (nd && !dst_bases))
-    return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
-  // Only buffers that some segment references are checked: an unreferenced
-  // buffer may be NULL or alias anything.
-  Bases sb{}, db{};
-  for (uint32_t i = 0; i < ns; ++i) {
-    sb.p[i] = static_cast<char *>(src_bases[i]);
-    if (!plan->src_used[i]) continue;
-    if (!sb.p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
-    if (reinterpret_cast<uintptr_t>(sb.p[i]) % 16)
-      return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
-  }
-  for (uint32_t i = 0; i < nd; ++i) {
-    db.p[i] = static_cast<char *>(dst_bases[i]);
-    if (!plan->dst_used[i]) continue;
-    if (!db.p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
-    if (reinterpret_cast<uintptr_t>(db.p[i]) % 16)
-      return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
-  }
-  auto overlap = [](uintptr_t a0, uint64_t an, uintptr_t b0, uint64_t bn) {
-    return an && bn && a0 < b0 + bn && b0 < a0 + an;
-  };
-  for (uint32_t j = 0; j < nd; ++j) {
-    if (!plan->dst_used[j]) continue;
-    const uintptr_t d0 = reinterpret_cast<uintptr_t>(db.p[j]);
-    for (uint32_t i = 0; i < ns; ++i)
-      if (plan->src_used[i] && overlap(reinterpret_cast<uintptr_t>(sb.p[i]), plan->src_bytes[i], d0, plan->dst_bytes[j]))
-        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
-    for (uint32_t k = j + 1; k < nd; ++k)
-      if (plan->dst_used[k] && overlap(d0, plan->dst_bytes[j], reinterpret_cast<uintptr_t>(db.p[k]), plan->dst_bytes[k]))
-        return fail(EMRS_ERR_ALIAS, "two destination buffers overlap");
-  }
+  Bases sb, db;
+  int rc = resolve_bases(plan, src_bases, dst_bases, &sb, &db);
+  if (rc) return rc;
   if (plan->n_chunks == 0) return EMRS_OK;
 
   int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
-  int rc = current_device(&dev, &cus, &resident_nt, &resident_t);
+  rc = current_device(&dev, &cus, &resident_nt, &resident_t);
   if (rc) return rc;
   DevSeg *table = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(plan->mu);
-    if ((int)plan->dev_tables.size() <= dev) plan->dev_tables.resize(dev + 1, nullptr);
-    if (!plan->dev_tables[dev]) {
-      const size_t bytes = plan->segs.size() * sizeof(DevSeg);
-      hipError_t e = hipMalloc(&plan->dev_tables[dev], bytes);
-      if (e != hipSuccess) {
-        plan->dev_tables[dev] = nullptr;
-        return hip_fail(e, "hipMalloc(plan table)");
-      }
-      e = hipMemcpy(plan->dev_tables[dev], plan->segs.data(), bytes, hipMemcpyHostToDevice);
-      if (e != hipSuccess) return hip_fail(e, "hipMemcpy(plan table)");
-    }
-    table = plan->dev_tables[dev];
-  }
+  rc = device_table(plan, dev, &table);
+  if (rc) return rc;
 
   const bool nt = g_tuning.nontemporal.load() != 0;
   const uint32_t bpc = g_tuning.blocks_per_cu.load();
@@ -710,6 +942,79 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
                        (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, run, sb, db);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "copy_plan_kernel launch");
+  return EMRS_OK;
+}
+
+int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
+                      const uint32_t *aux_groups, uint32_t n_groups, emrs_compare_stats *stats, void *stream) {
+  g_last_error.clear();
+  if (!plan || !stats) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (n_groups == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, "n_groups must be >= 1");
+  const uint64_t n_in = plan->stats.n_segments;
+  for (uint64_t i = 0; i < n_in; ++i)
+    if ((groups && groups[i] >= n_groups) || (aux_groups && aux_groups[i] >= n_groups))
+      return fail(EMRS_ERR_INVALID_ARGUMENT, "group id >= n_groups");
+  Bases sb, db;
+  int rc = resolve_bases(plan, src_bases, dst_bases, &sb, &db);
+  if (rc) return rc;
+
+  // Per device segment: its groups, and the element counts on the host.
+  const size_t nd = plan->segs.size();
+  std::vector<uint32_t> g_host(2 * nd);
+  std::vector<uint64_t> elements(n_groups, 0);
+  for (size_t k = 0; k < nd; ++k) {
+    const DevSeg &d = plan->segs[k];
+    const uint32_t o = plan->origin[k];
+    const uint32_t g = groups ? groups[o] : 0, ga = aux_groups ? aux_groups[o] : g;
+    g_host[k] = g;
+    g_host[nd + k] = ga;
+    const uint64_t units = (uint64_t)d.len * d.rows;
+    elements[g] += units << (d.unit_log2 - d.elem_log2);
+    if (d.cast & 1) elements[ga] += units << (d.unit_log2 - 2);
+  }
+  for (uint32_t g = 0; g < n_groups; ++g) {
+    stats[g] = emrs_compare_stats{};
+    stats[g].elements = elements[g];
+  }
+  if (plan->n_chunks == 0) return EMRS_OK;
+
+  int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
+  rc = current_device(&dev, &cus, &resident_nt, &resident_t);
+  if (rc) return rc;
+  DevSeg *table = nullptr;
+  rc = device_table(plan, dev, &table);
+  if (rc) return rc;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
+  const size_t grp_bytes = g_host.size() * sizeof(uint32_t);
+  char *buf = nullptr;
+  hipError_t e = hipMalloc(&buf, acc_bytes + grp_bytes);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(compare buffers)");
+  GroupAcc *acc = reinterpret_cast<GroupAcc *>(buf);
+  uint32_t *grp = reinterpret_cast<uint32_t *>(buf + acc_bytes);
+  std::vector<GroupAcc> host(n_groups);
+  e = hipMemsetAsync(acc, 0, acc_bytes, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(grp, g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) {
+    const uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * 8);
+    hipLaunchKernelGGL(compare_plan_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp, grp + nd,
+                       (uint32_t)nd, plan->n_chunks, sb, db, acc);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFree(buf);
+  if (e != hipSuccess) return hip_fail(e, "compare_plan_kernel");
+  for (uint32_t g = 0; g < n_groups; ++g) {
+    stats[g].mismatches = host[g].mismatches;
+    stats[g].nonfinite = host[g].nonfinite;
+    stats[g].sum_sq_diff = host[g].sum_sq_diff;
+    stats[g].sum_sq_expected = host[g].sum_sq_expected;
+    uint32_t ma = host[g].max_abs_bits, mr = host[g].max_rel_bits;
+    memcpy(&stats[g].max_abs_diff, &ma, 4);
+    memcpy(&stats[g].max_rel_diff, &mr, 4);
+  }
   return EMRS_OK;
 }
 

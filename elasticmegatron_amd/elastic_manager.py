@@ -70,6 +70,7 @@ class ElasticMegatronManager:
         self.transfer_manager = TransferManager()
         self.release_source = release_source
         self.last_transfer_ms = 0.0
+        self.last_verification = None
         if training_state is None:
             training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device)
         self.training_state = training_state
@@ -132,12 +133,18 @@ class ElasticMegatronManager:
         return msg
 
     def reshard(self, new_parallel_strategy: StrategyLike, logger: Optional[logging.Logger] = None,
-                is_meta_device: bool = False, save_ckpt: bool = False) -> Optional[TrainingState]:
+                is_meta_device: bool = False, save_ckpt: bool = False,
+                verify: bool = False) -> Optional[TrainingState]:
         """Switch every rank's state to ``new_parallel_strategy``; returns the new state.
 
         ``is_meta_device=True`` builds and caches the plan without touching
         device memory and returns None (the reference's meta-device
         pre-build, elastic_manager.py:268-304).
+
+        ``verify=True`` compares the new state with the old one on the device
+        before the old one is released (the reference's offline checkpoint
+        comparison, tools/ckpt/compare_ckpt.py, done in place); the report is
+        kept in ``last_verification`` and a mismatch raises RuntimeError.
         """
         if is_meta_device and save_ckpt:
             raise AssertionError("Can't save checkpoint in meta device")
@@ -167,7 +174,14 @@ class ElasticMegatronManager:
             dst_state = TrainingState.allocate(dst_layout, src_state.device, param=src_state.param)
             elapsed = self.redundant_backup(src_state, dst_state, backup)
         self.last_transfer_ms = elapsed
-        if self.release_source:
+        if verify:
+            kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+            report = self.transfer_manager.verify(src_state, dst_state, kind)
+            self.last_verification = report
+            if not report.bit_exact:
+                lines = report.lines()
+                raise RuntimeError(f"reshard verification failed: {report.mismatches} elements differ\n"
+                                   + "\n".join(lines[:20]))
             src_state.release_optimizer()
         self.training_state = dst_state
         msg = self.log_communication_info(elapsed, logger)

@@ -109,16 +109,17 @@ class SegmentBuilder:
 
     def __init__(self):
         self.rows: List[Tuple] = []
+        self.groups: List[int] = []  # parameter of each row; rows of different parameters never merge
 
     def add(self, sbuf: int, dbuf: int, eb: int, so: int, do: int, n: int, rows: int, ss: int, ds: int,
-            aux: Optional[Tuple[int, int, int]] = None, zero: bool = False) -> None:
+            aux: Optional[Tuple[int, int, int]] = None, zero: bool = False, group: int = 0) -> None:
         if n <= 0 or rows <= 0:
             return
         flags, abuf, aoff, astr = (SEG_CAST_BF16, aux[0], aux[1], aux[2]) if aux else (0, 0, 0, 0)
         if zero:
             flags |= SEG_ZERO_FILL
             so, ss = 0, 0
-        if self.rows and rows == 1:
+        if self.rows and rows == 1 and self.groups[-1] == group:
             p = self.rows[-1]
             if (p[0] == sbuf and p[1] == dbuf and p[2] == eb and p[3] == flags and p[7] == 1
                     and (zero or p[4] + p[6] == so) and p[5] + p[6] == do
@@ -126,12 +127,16 @@ class SegmentBuilder:
                 self.rows[-1] = p[:6] + (p[6] + n,) + p[7:]
                 return
         self.rows.append((sbuf, dbuf, eb, flags, so, do, n, rows, ss, ds, abuf, 0, aoff, astr if rows > 1 else 0))
+        self.groups.append(group)
 
     def table(self) -> np.ndarray:
         arr = np.zeros(len(self.rows), dtype=SEGMENT_DTYPE)
         if self.rows:
             arr[:] = self.rows
         return arr
+
+    def group_array(self) -> np.ndarray:
+        return np.asarray(self.groups, dtype=np.int64)
 
 
 def _src_replica(vp, holders: List[Holder]) -> List[Holder]:
@@ -173,7 +178,7 @@ def check_compatible(src_space, dst_space) -> None:
 
 
 def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool = True,
-                   include_bf16: bool = True, bf16_source: str = "cast") -> np.ndarray:
+                   include_bf16: bool = True, bf16_source: str = "cast", with_groups: bool = False):
     """Segments of a switch between two layouts of the same model.
 
     Buffers 0..2 are the fp32 arenas (main, exp_avg, exp_avg_sq) and buffer 3
@@ -191,6 +196,12 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
     the reference keeps it fixed, virtual_param.py:480-481).  Rows the source
     has and the destination keeps are copied; new padding rows are written
     as zeros in all four tensors; dropped padding rows are not read.
+
+    ``with_groups=True`` returns ``(table, groups, aux_groups)`` instead: no
+    segment spans two parameters, and each segment's elements (and its bf16
+    image) carry the group ``4 * parameter index + kind`` (kind 0 bf16 param,
+    1 main, 2 exp_avg, 3 exp_avg_sq).  That table is for verification
+    (:func:`emrs_plan_compare`); the executed one merges across parameters.
     """
     if bf16_source not in ("cast", "copy"):
         raise ValueError(bf16_source)
@@ -206,6 +217,7 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
         sv = src.space.value_source(src.space.all_virtual_params[vp.global_index])
         if not (src.has_param(sv) and dst.has_param(vp)):
             continue  # tied output layer at destination PP 1 (transfer.py:324-330)
+        gid = vp.global_index if with_groups else 0
         src_rows = view2d(sv.full_shape, sv.tensor_parallel_attr.partition_dim)[0]
         dst_rows = view2d(vp.full_shape, vp.tensor_parallel_attr.partition_dim)[0]
         new_rows = src_rows if dst_rows > src_rows else None
@@ -225,11 +237,11 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
                     return None
 
                 for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
-                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds, aux_of(do, ds))
+                    fp32.add(0, 0, 4, so, do, n, rows, ss, ds, aux_of(do, ds), group=gid)
                     covered += n * rows
                 if new_rows is not None:
                     for do, n, rows, ds in _rows_from(d_rects, new_rows):
-                        fp32.add(0, 0, 4, 0, do, n, rows, 0, ds, aux_of(do, ds), zero=True)
+                        fp32.add(0, 0, 4, 0, do, n, rows, 0, ds, aux_of(do, ds), zero=True, group=gid)
                         covered += n * rows
             if covered != want:
                 raise AssertionError(f"{vp.name}: fp32 plan covers {covered} of {want} elements")
@@ -246,19 +258,22 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
                 want += h.hi - h.lo
                 d_rects = holder_rects(h, dst.geometry(vp, h.tp_rank))
                 for so, do, n, rows, ss, ds in _intersections(s_rects, d_rects):
-                    bf16.add(ARENA_PARAM, ARENA_PARAM, 2, so, do, n, rows, ss, ds)
+                    bf16.add(ARENA_PARAM, ARENA_PARAM, 2, so, do, n, rows, ss, ds, group=gid)
                     covered += n * rows
                 if new_rows is not None:
                     for do, n, rows, ds in _rows_from(d_rects, new_rows):
-                        bf16.add(ARENA_PARAM, ARENA_PARAM, 2, 0, do, n, rows, 0, ds, zero=True)
+                        bf16.add(ARENA_PARAM, ARENA_PARAM, 2, 0, do, n, rows, 0, ds, zero=True, group=gid)
                         covered += n * rows
             if covered != want:
                 raise AssertionError(f"{vp.name}: bf16 plan covers {covered} of {want} elements")
-    return _assemble(fp32.table(), bf16.table())
+    return _assemble(fp32.table(), bf16.table(), fp32.group_array(), bf16.group_array(), with_groups)
 
 
-def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool) -> np.ndarray:
-    """fp32 segments of a Group-ZeRO switch (instances change, shards do not)."""
+def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False):
+    """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
+
+    ``with_groups``: as for :func:`lower_transfer`.
+    """
     space = src.space
     if src.strategy.optimizer_data_parallel_size != dst.strategy.optimizer_data_parallel_size:
         raise AssertionError("Group-ZeRO switch must keep the optimizer DP size")
@@ -272,21 +287,26 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
             s = src_by.get((inst, h.tp_rank, h.lo))
             if s is None or s.hi != h.hi:
                 raise AssertionError(f"{vp.name}: no matching source shard for a Group-ZeRO copy")
-            b.add(0, 0, 4, s.offset, h.offset, h.hi - h.lo, 1, 0, 0)
-    return _assemble(b.table(), np.zeros(0, dtype=SEGMENT_DTYPE))
+            b.add(0, 0, 4, s.offset, h.offset, h.hi - h.lo, 1, 0, 0, group=vp.global_index if with_groups else 0)
+    return _assemble(b.table(), np.zeros(0, dtype=SEGMENT_DTYPE), b.group_array(), np.zeros(0, dtype=np.int64),
+                     with_groups)
 
 
 # Elements per interleaved piece: 1 MiB of fp32.
 INTERLEAVE_ELEMS = 1 << 18
 
 
-def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
-    """Cut segments into pieces of at most ``max_elems`` elements (whole rows for strided ones)."""
-    out = []
-    for s in table:
+def _split(table: np.ndarray, max_elems: int, groups: np.ndarray):
+    """Cut segments into pieces of at most ``max_elems`` elements (whole rows for strided ones).
+
+    Returns the pieces and the group of each.
+    """
+    out, out_g = [], []
+    for s, g in zip(table, groups):
         n, rows = int(s["len"]), int(s["rows"])
         if n * rows <= max_elems:
             out.append(s)
+            out_g.append(g)
             continue
         reads = not s["flags"] & SEG_ZERO_FILL
         cast = bool(s["flags"] & SEG_CAST_BF16)
@@ -298,6 +318,7 @@ def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
                 p["aux_off"] += o if cast else 0
                 p["len"] = min(max_elems, n - o)
                 out.append(p)
+                out_g.append(g)
             continue
         step = max(1, max_elems // n)
         for r in range(0, rows, step):
@@ -307,10 +328,12 @@ def _split(table: np.ndarray, max_elems: int) -> np.ndarray:
             p["aux_off"] += r * int(s["aux_stride"])
             p["rows"] = min(step, rows - r)
             out.append(p)
-    return np.array(out, dtype=SEGMENT_DTYPE) if out else np.zeros(0, dtype=SEGMENT_DTYPE)
+            out_g.append(g)
+    arr = np.array(out, dtype=SEGMENT_DTYPE) if out else np.zeros(0, dtype=SEGMENT_DTYPE)
+    return arr, np.asarray(out_g, dtype=np.int64)
 
 
-def _assemble(fp32: np.ndarray, bf16: np.ndarray) -> np.ndarray:
+def _assemble(fp32: np.ndarray, bf16: np.ndarray, g32: np.ndarray, gbf: np.ndarray, with_groups: bool):
     """Replicate the fp32 segments over the three optimizer kinds; only main carries the bf16 cast.
 
     The kinds are interleaved in pieces of about 1 MiB: the kernel hands
@@ -318,18 +341,25 @@ def _assemble(fp32: np.ndarray, bf16: np.ndarray) -> np.ndarray:
     the bf16 cast costs more than the others, so every run must hold the same
     mix of kinds.
     """
-    base = _split(fp32, INTERLEAVE_ELEMS)
+    base, gbase = _split(fp32, INTERLEAVE_ELEMS, g32)
     out = np.zeros(3 * len(base), dtype=SEGMENT_DTYPE)
+    groups = np.zeros(3 * len(base), dtype=np.int64)
     for k in range(3):
         t = out[k::3]
         t[...] = base
         t["src_buf"] = k
         t["dst_buf"] = k
+        groups[k::3] = 4 * gbase + 1 + k
         if k:
             t["flags"] &= ~np.uint32(SEG_CAST_BF16)
             for f in ("aux_buf", "aux_off", "aux_stride"):
                 t[f] = 0
-    return np.concatenate([out, bf16])
+    table = np.concatenate([out, bf16])
+    if not with_groups:
+        return table
+    groups = np.concatenate([groups, 4 * gbf])
+    aux_groups = np.concatenate([4 * np.repeat(gbase, 3), 4 * gbf])
+    return table, groups.astype(np.uint32), aux_groups.astype(np.uint32)
 
 
 def _units(table: np.ndarray) -> np.ndarray:

@@ -26,6 +26,7 @@ from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import StrategyLayout
+from .verify import VerifyReport, report_from_stats
 
 
 @dataclass
@@ -65,6 +66,7 @@ class TransferManager:
         self.check_disjoint = check_disjoint
         self.bf16_source = bf16_source
         self.fake_transfer = False
+        self._verify_plans: Dict[Tuple, Tuple] = {}
         self._payload_bytes = 0
         self._comm_bytes = 0
 
@@ -114,6 +116,41 @@ class TransferManager:
             plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)
         self._payload_bytes += plan.payload_bytes
         self._comm_bytes += plan.reference_comm_bytes
+
+    def verify(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
+               include_bf16: bool = True, stream: Optional[torch.cuda.Stream] = None) -> VerifyReport:
+        """Check, on the device, that ``dst`` holds what the switch from ``src`` must produce.
+
+        Replaces the reference's offline checkpoint comparison
+        (tools/ckpt/compare_ckpt.py:17-76): per parameter and tensor kind, the
+        bits that differ and compare_ckpt's max-abs / max-rel / RMS / relative
+        RMS.  ``src`` must still hold the state it was resharded from.
+        """
+        if src.device.type != "cuda" or dst.device.type != "cuda":
+            raise RuntimeError("training states must live in GPU memory: verification has no CPU path")
+        sl, dl = src.layout, dst.layout
+        key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source)
+        vp = self._verify_plans.get(key)
+        if vp is None:
+            if kind == "transfer":
+                table, groups, aux_groups = lower_transfer(sl, dl, include_bf16=include_bf16,
+                                                           bf16_source=self.bf16_source, with_groups=True)
+            elif kind in ("backup_up", "backup_down"):
+                table, groups, aux_groups = lower_redundant_backup(sl, dl, scale_up=kind == "backup_up",
+                                                                   with_groups=True)
+            else:
+                raise ValueError(kind)
+            sb = [sl.fp32_numel * 4] * 3 + [sl.bf16_numel * 2]
+            db = [dl.fp32_numel * 4] * 3 + [dl.bf16_numel * 2]
+            names = [p.name for p in dl.space.all_virtual_params]
+            vp = (_native.Plan(table, sb, db), groups, aux_groups, names)
+            self._verify_plans[key] = vp
+        plan, groups, aux_groups, names = vp
+        st = stream if stream is not None else torch.cuda.current_stream(src.device)
+        with torch.cuda.device(src.device):
+            stats = plan.compare(src.arena_ptrs(), dst.arena_ptrs(), groups, aux_groups, 4 * len(names),
+                                 st.cuda_stream)
+        return report_from_stats(stats, names)
 
     def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
                                    dst: Optional[TrainingState] = None, include_bf16: bool = True,

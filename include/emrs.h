@@ -148,6 +148,50 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases,
 int emrs_plan_destroy(emrs_plan *plan);
 
 /*
+ * Verification of an executed plan: per group, how the destination differs
+ * from what the plan would write there.
+ *
+ * The numbers are those of the reference's checkpoint check,
+ * tools/ckpt/compare_ckpt.py:17-76 (max |a - b|, max |a - b| / (|b| + 1e-12),
+ * RMS and relative RMS per tensor), plus an exact bit comparison.  The
+ * reference first converts the source checkpoint on the CPU and then diffs
+ * the two.  Here both states stay on the device: the plan supplies, for
+ * every destination element, the source element (or zero) it must equal.
+ * A cast segment's bf16 image is checked against bf16(source) as well.
+ *
+ * "expected" below is that value; "actual" is what the destination holds.
+ * fp32 and bf16 elements (elem_bytes 4 and 2) are compared as numbers and
+ * bit patterns; 1- and 8-byte elements as bit patterns only.
+ */
+typedef struct emrs_compare_stats {
+  uint64_t elements;        /* elements compared */
+  uint64_t mismatches;      /* elements whose bits differ from the expected value */
+  uint64_t nonfinite;       /* mismatching fp32/bf16 elements with a NaN or infinite difference */
+  uint64_t reserved;
+  double sum_sq_diff;       /* sum of (actual - expected)^2 over finite differences */
+  double sum_sq_expected;   /* sum of expected^2 over finite expected fp32/bf16 values */
+  float max_abs_diff;       /* max |actual - expected| over finite differences */
+  float max_rel_diff;       /* max |actual - expected| / (|expected| + 1e-12) */
+  uint64_t reserved2;
+} emrs_compare_stats;
+
+/*
+ * Compare the destination buffers with what `plan` writes from the source
+ * buffers, and accumulate the differences per group.
+ *   groups[i]:     group of input segment i's elements (NULL: all group 0)
+ *   aux_groups[i]: group of input segment i's bf16 image (NULL: groups[i])
+ *   stats:         n_groups host records, filled when the call returns
+ * Base pointers follow emrs_plan_execute's rules.  The call runs on `stream`
+ * and waits for it.  It allocates and frees a small device buffer (the
+ * group tables and accumulators), so it is not for capture into a graph.
+ * Errors: INVALID_ARGUMENT (n_groups == 0, a group id >= n_groups), the
+ * base-pointer errors of emrs_plan_execute, NO_DEVICE, HIP.
+ */
+int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
+                      const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,
+                      emrs_compare_stats *stats, void *stream);
+
+/*
  * Launch-shape knobs of emrs_plan_execute, process-wide.  Results never
  * depend on them; only speed does.
  */

@@ -166,3 +166,60 @@ def repad_spaces(spec, tps):
     """Virtual models of ``spec`` at Megatron's padded vocabulary for each TP size."""
     from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
     return [build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(t))) for t in tps]
+
+
+def compare_numpy(table, groups, aux_groups, n_groups, src, dst):
+    """Reference semantics of emrs_plan_compare on host arrays (any integer dtype; viewed per segment).
+
+    Returns ``n_groups`` records of _native.COMPARE_DTYPE.  fp32 and bf16
+    differences are taken in fp32, squared in fp64, as compare_ckpt.py's
+    figures define them (tools/ckpt/compare_ckpt.py:52-66).
+    """
+    from elasticmegatron_amd._native import COMPARE_DTYPE
+
+    out = np.zeros(n_groups, dtype=COMPARE_DTYPE)
+    udt = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}
+
+    def acc(g, e, a, eb):
+        r = out[g]
+        r["elements"] += e.size
+        mism = e != a
+        r["mismatches"] += int(mism.sum())
+        if eb not in (2, 4):
+            return
+        if eb == 2:
+            e32 = (e.astype(np.uint32) << np.uint32(16)).view(np.float32)
+            a32 = (a.astype(np.uint32) << np.uint32(16)).view(np.float32)
+        else:
+            e32, a32 = e.view(np.float32), a.view(np.float32)
+        with np.errstate(all="ignore"):
+            fe = np.isfinite(e32)
+            r["sum_sq_expected"] += float(np.sum(e32[fe].astype(np.float64) ** 2))
+            d = np.abs(a32 - e32)
+            fin = np.isfinite(d)
+            r["nonfinite"] += int((mism & ~fin).sum())
+            sel = mism & fin
+            if sel.any():
+                r["sum_sq_diff"] += float(np.sum(d[sel].astype(np.float64) ** 2))
+                r["max_abs_diff"] = max(float(r["max_abs_diff"]), float(d[sel].max()))
+                rel = (d / (np.abs(e32) + np.float32(1e-12))).astype(np.float32)
+                r["max_rel_diff"] = max(float(r["max_rel_diff"]), float(rel[sel].max()))
+
+    for s, g, ga in zip(table, groups, aux_groups):
+        eb = int(s["elem_bytes"])
+        n, rows = int(s["len"]), int(s["rows"])
+        if n == 0:
+            continue
+        d_arr = dst[int(s["dst_buf"])].view(udt[eb])
+        act = _view(d_arr, int(s["dst_off"]), rows, n, int(s["dst_stride"])).reshape(-1)
+        if int(s["flags"]) & 2:
+            exp = np.zeros(act.shape, dtype=act.dtype)
+        else:
+            s_arr = src[int(s["src_buf"])].view(udt[eb])
+            exp = _view(s_arr, int(s["src_off"]), rows, n, int(s["src_stride"])).reshape(-1)
+        acc(int(g), exp, act, eb)
+        if int(s["flags"]) & 1:
+            aux = dst[int(s["aux_buf"])].view(np.uint16)
+            act_a = _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"])).reshape(-1)
+            acc(int(ga), bf16_rne_bits(exp.view(np.uint32)), act_a, 2)
+    return out

@@ -66,6 +66,8 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
         tm.execute(fwd, a, b)
         bad, first = b.verify_synthetic(SEED, vocab_rows=vocab_rows)
         assert bad == 0, first
+        report = tm.verify(a, b, kind)  # the plan's own check, against the source state
+        assert report.bit_exact, report.lines()[:5]
         # Round trip into fresh storage: must reproduce every source element.
         param = a.param
         del a

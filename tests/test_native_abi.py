@@ -40,6 +40,15 @@ def test_record_layouts_match_header():
         assert getattr(Seg, name).offset == off
     assert PIECE_DTYPE.itemsize == 88
 
+    class Cmp(ctypes.Structure):  # struct emrs_compare_stats
+        _fields_ = [(n, ctypes.c_uint64) for n in ("elements", "mismatches", "nonfinite", "reserved")] + \
+                   [("sum_sq_diff", ctypes.c_double), ("sum_sq_expected", ctypes.c_double),
+                    ("max_abs_diff", ctypes.c_float), ("max_rel_diff", ctypes.c_float), ("reserved2", ctypes.c_uint64)]
+
+    assert ctypes.sizeof(Cmp) == _native.COMPARE_DTYPE.itemsize == 64
+    for name, (dt, off) in _native.COMPARE_DTYPE.fields.items():
+        assert getattr(Cmp, name).offset == off
+
 
 def _seg(**kw):
     row = dict(src_buf=0, dst_buf=0, elem_bytes=4, flags=0, src_off=0, dst_off=0, len=16, rows=1,
