@@ -182,6 +182,7 @@ class ElasticMegatronManager:
                 lines = report.lines()
                 raise RuntimeError(f"reshard verification failed: {report.mismatches} elements differ\n"
                                    + "\n".join(lines[:20]))
+        if self.release_source:
             src_state.release_optimizer()
         self.training_state = dst_state
         msg = self.log_communication_info(elapsed, logger)

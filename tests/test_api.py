@@ -86,3 +86,30 @@ def test_manager_adopts_a_given_state():
         ParallelStrategy(**SEQ[0])), "cpu")
     with pytest.raises(ValueError):
         ElasticMegatronManager(SEQ, spec, training_state=other)
+
+
+def test_reshard_releases_the_source_state(monkeypatch):
+    """After a switch only the new state holds optimizer memory (training_state.py:313-315), with or without
+    verification.  The device calls are stubbed: this checks the host-side ownership only."""
+    import gc
+    import weakref
+
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+    from elasticmegatron_amd.transfer.verify import VerifyReport
+
+    monkeypatch.setattr(TransferManager, "execute", lambda self, plan, src, dst, stream=None: None)
+    monkeypatch.setattr(TransferManager, "verify", lambda self, src, dst, kind="transfer", include_bf16=True,
+                        stream=None: VerifyReport({}))
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
+    arenas = [weakref.ref(mgr.training_state.main)]
+    for i, s in enumerate(SEQ[1:] + SEQ[:1] + SEQ[1:]):
+        mgr.reshard(s, verify=bool(i % 2))
+        arenas.append(weakref.ref(mgr.training_state.main))
+        gc.collect()
+        alive = [r for r in arenas if r() is not None and r().numel() > 0]
+        assert len(alive) == 1 and alive[0]() is mgr.training_state.main
+    keep = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu", release_source=False)
+    first = keep.training_state
+    keep.reshard(SEQ[1])
+    assert first.main.numel() > 0
