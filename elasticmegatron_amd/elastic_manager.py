@@ -26,7 +26,7 @@ are carried over and new padding rows are zero in all four tensors.
 from __future__ import annotations
 
 import logging
-from typing import Dict, List, Optional, Union
+from typing import Callable, Dict, List, Optional, Union
 
 import torch
 
@@ -47,7 +47,14 @@ def _as_strategy(s: StrategyLike) -> ParallelStrategy:
 class ElasticMegatronManager:
     def __init__(self, parallel_strategy_list: List[StrategyLike], model_spec: ModelSpec,
                  training_state: Optional[TrainingState] = None, device=None,
-                 release_source: bool = True, repad_vocab: bool = False):
+                 release_source: bool = True, repad_vocab: bool = False,
+                 send_fn: Optional[Callable] = None, recv_fn: Optional[Callable] = None,
+                 broadcast_fn: Optional[Callable] = None, use_p2p_to_collective: bool = True):
+        """``model_spec`` and ``training_state`` stand in for the reference's live Megatron
+        ``model`` / ``optimizer`` (elastic_manager.py:41-82).  ``send_fn``, ``recv_fn``,
+        ``broadcast_fn`` and ``use_p2p_to_collective`` are accepted as the reference accepts
+        them and handed to the TransferManager; on one device no message is sent.
+        """
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
         if repad_vocab and model_spec.vocab_size is None:
@@ -67,7 +74,8 @@ class ElasticMegatronManager:
             self._spaces[spec.padded_vocab_size] = training_state.layout.space
         for s in self.parallel_strategy_list:
             self.space_for(s).build_model_virtual_params(s)
-        self.transfer_manager = TransferManager()
+        self.transfer_manager = TransferManager(send_fn, recv_fn, broadcast_fn)
+        self.use_p2p_to_collective = use_p2p_to_collective
         self.release_source = release_source
         self.last_transfer_ms = 0.0
         self.last_verification = None

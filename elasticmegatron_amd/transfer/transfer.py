@@ -15,7 +15,7 @@ messages are the same operation on one device.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, Optional, Tuple
+from typing import Callable, Dict, Optional, Tuple
 
 import numpy as np
 import torch
@@ -59,9 +59,21 @@ def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
 
 
 class TransferManager:
-    """Builds, caches and runs copy plans between device-resident training states."""
+    """Builds, caches and runs copy plans between device-resident training states.
 
-    def __init__(self, check_disjoint: bool = False, bf16_source: str = "cast"):
+    The constructor keeps the reference's ``send_fn`` / ``recv_fn`` /
+    ``broadcast_fn`` parameters (transfer.py:23-34) so that existing call
+    sites construct it unchanged.  With every rank's state on one device
+    every hop is a local copy inside the plan, so they are kept but never
+    called.
+    """
+
+    def __init__(self, send_fn: Optional[Callable] = None, recv_fn: Optional[Callable] = None,
+                 broadcast_fn: Optional[Callable] = None, *, check_disjoint: bool = False,
+                 bf16_source: str = "cast"):
+        if bf16_source not in ("cast", "copy"):
+            raise ValueError(f"bf16_source must be 'cast' or 'copy', not {bf16_source!r}")
+        self.send_fn, self.recv_fn, self.broadcast_fn = send_fn, recv_fn, broadcast_fn
         self._plans: Dict[Tuple, CompiledPlan] = {}
         self.check_disjoint = check_disjoint
         self.bf16_source = bf16_source

@@ -113,3 +113,22 @@ def test_reshard_releases_the_source_state(monkeypatch):
     first = keep.training_state
     keep.reshard(SEQ[1])
     assert first.main.numel() > 0
+
+
+def test_reference_constructor_arguments_are_accepted():
+    """TransferManager(send_fn, recv_fn, broadcast_fn) and the manager's transport arguments, as the
+    reference takes them (transfer.py:23-34, elastic_manager.py:41-82)."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    calls = []
+    send = lambda t, dst: calls.append(("send", dst))  # noqa: E731
+    recv = lambda t, src: calls.append(("recv", src))  # noqa: E731
+    tm = TransferManager(send, recv, None)
+    assert tm.send_fn is send and tm.recv_fn is recv and tm.broadcast_fn is None
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu", send_fn=send, recv_fn=recv,
+                                 broadcast_fn=None, use_p2p_to_collective=False)
+    assert mgr.transfer_manager.send_fn is send
+    assert mgr.reshard(SEQ[1], is_meta_device=True) is None
+    assert calls == []   # one device: every hop is a local copy inside the plan
+    with pytest.raises(ValueError):
+        TransferManager(bf16_source="fp8")

@@ -63,3 +63,26 @@ def test_group_zero_plan_invariants():
         st = _native.Plan(t, [lx.fp32_numel * 4] * 3 + [lx.bf16_numel * 2],
                           [ly.fp32_numel * 4] * 3 + [ly.bf16_numel * 2], check_disjoint=True).stats()
         assert st.scalar_bytes == 0
+
+
+@pytest.mark.parametrize("bf16_source", ["cast", "copy"])
+def test_switch_to_the_same_strategy_is_the_identity(bf16_source):
+    """reshard(S -> S) reproduces every stored element.  (It is the identity on values, not on offsets:
+    parameters that are not TP-split are read from TP rank 0 for every TP rank, and a tied output layer
+    from the word embedding, as the reference reads them.)"""
+    import numpy as np
+
+    from tests.helpers import SEED, SMALL_CASES, compare, execute_numpy, extract, new_arenas, piece_fill_numpy
+
+    for _, factory, seq in SMALL_CASES:
+        space = build_virtual_model(factory())
+        for s in seq:
+            lay = space.layout(s)
+            t = lower_transfer(lay, lay, bf16_source=bf16_source)
+            assert ((t["flags"] & 2) == 0).all()
+            assert np.array_equal(t["src_buf"], t["dst_buf"])
+            a = new_arenas(lay)
+            piece_fill_numpy(lay.pieces(), a, SEED)
+            b = new_arenas(lay, fill=0)
+            execute_numpy(t, a, b)
+            assert compare(*extract(lay, b), *extract(lay, a)) == []
