@@ -283,14 +283,24 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
 // Persistent grid.  With run == 0 every workgroup takes one contiguous run of
 // chunks_per_block chunks (xcd_stride != 0: each XCD's workgroups cover one
 // contiguous slice).  With run > 0 the chunks are dealt out round-robin in
-// runs of `run` chunks, so all workgroups sweep the plan together.
+// runs of `run` chunks, so the workgroups sweep the plan together; with
+// xcd_stride != 0 as well (the grid is then a multiple of 8, and workgroup b
+// runs on XCD b % 8), each XCD sweeps its own contiguous eighth, so that no
+// page is touched from two XCDs' translation caches.
 template <bool kNT>
 __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
     const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
     uint64_t chunks_per_block, uint32_t xcd_stride, uint32_t run, Bases src, Bases dst) {
   if (run) {
-    for (uint64_t c = (uint64_t)blockIdx.x * run; c < n_chunks; c += (uint64_t)gridDim.x * run)
-      copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + run, n_chunks), src, dst);
+    uint64_t c1 = n_chunks, c = (uint64_t)blockIdx.x * run, step = (uint64_t)gridDim.x * run;
+    if (xcd_stride) {
+      const uint64_t x = blockIdx.x & 7;
+      const uint64_t c0 = n_chunks * x / 8;
+      c1 = n_chunks * (x + 1) / 8;
+      c = c0 + (uint64_t)(blockIdx.x >> 3) * run;
+      step = (uint64_t)(gridDim.x >> 3) * run;
+    }
+    for (; c < c1; c += step) copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + run, c1), src, dst);
     return;
   }
   uint64_t b = blockIdx.x;
@@ -922,13 +932,13 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint64_t max_blocks = (uint64_t)cus * (bpc ? bpc : (uint32_t)(nt ? resident_nt : resident_t));
   uint64_t blocks = std::min<uint64_t>(plan->n_chunks, max_blocks);
   uint32_t run = g_tuning.run.load();
+  const bool remap = g_tuning.xcd_remap.load() != 0;
   if (run) {
     // Round-robin runs: at most a quarter of each workgroup's share, so that
     // small plans still spread over the whole grid.
     run = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(run, plan->n_chunks / (blocks * 4)));
     blocks = std::min<uint64_t>(blocks, (plan->n_chunks + run - 1) / run);
   }
-  const bool remap = !run && g_tuning.xcd_remap.load() != 0;
   if (remap) blocks = (blocks + 7) / 8 * 8;
   const uint64_t cpb = (plan->n_chunks + blocks - 1) / blocks;
   if (!remap && !run) blocks = (plan->n_chunks + cpb - 1) / cpb;

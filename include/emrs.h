@@ -199,8 +199,8 @@ typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
                              0 (default): as many as can be resident at once */
   uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
-  uint32_t xcd_remap;     /* 1: each XCD walks one contiguous slice of the chunks (default 1;
-                             applies only when run is 0) */
+  uint32_t xcd_remap;     /* 1 (default): each XCD works through one contiguous eighth of the chunks
+                             (workgroup b runs on XCD b % 8) */
   uint32_t run;           /* 0: each workgroup copies one contiguous run of chunks;
                              N > 0: chunks are dealt out round-robin in runs of N, capped at a
                              quarter of a workgroup's share (default 4) */

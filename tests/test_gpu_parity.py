@@ -132,7 +132,8 @@ def test_manager_repad_round_trip(gpu_device):
 
 
 @pytest.mark.parametrize("tuning", [dict(run=0), dict(run=0, xcd_remap=False), dict(run=1), dict(run=64),
-                                    dict(blocks_per_cu=1), dict(nontemporal=False), dict(blocks_per_cu=3, run=7)])
+                                    dict(blocks_per_cu=1), dict(nontemporal=False), dict(blocks_per_cu=3, run=7),
+                                    dict(run=4, xcd_remap=False), dict(run=1, blocks_per_cu=1, xcd_remap=False)])
 def test_launch_shape_does_not_change_results(gpu_device, tuning):
     """Every launch shape of emrs_set_tuning writes the same bits."""
     from elasticmegatron_amd.resharding.model_spec import tiny_llama2
