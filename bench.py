@@ -84,7 +84,7 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(spec_fn, src, dst, backup, target_s=10.0, max_reps=25):
+def cpu_baseline(spec_fn, src, dst, backup, target_s=10.0, max_reps=25, full_payload=0):
     """Oracle-1 (the reference's three-pass executor restated on CPU torch tensors) on layer 0."""
     import torch
 
@@ -113,10 +113,26 @@ def cpu_baseline(spec_fn, src, dst, backup, target_s=10.0, max_reps=25):
         total_b += sum(a.size * 2 for a in dbf.values())
         reps += 1
     n = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
-    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"transformer layer 0 ({len(params)} params, {n} elements) of the same switch, "
-                      f"executed {reps}x: {total_b / 1e9:.1f} GB payload in {total_t:.1f} s; "
-                      f"torch CPU threads={cores}"}
+    rate = total_b / total_t
+    out = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+           "sample": f"transformer layer 0 ({len(params)} params, {n} elements) of the same switch, "
+                     f"executed {reps}x: {total_b / 1e9:.1f} GB payload in {total_t:.1f} s; "
+                     f"torch CPU threads={cores}",
+           "ms_per_rep": round(total_t / reps * 1e3, 2), "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
+    if full_payload:
+        out["full_switch_ms_at_this_rate"] = round(full_payload / rate * 1e3, 1)
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -271,7 +287,7 @@ def main():
     del a
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup)
+        out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup, full_payload=payload)
     print(json.dumps(out), flush=True)
     return 0
 
