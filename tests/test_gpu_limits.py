@@ -1,0 +1,73 @@
+"""GPU: the executor at the limits of its ABI.
+
+- EMRS_MAX_BUFFERS (128) source and destination buffers in one plan.
+- Segments beyond 2^30 units, which emrs_plan_create splits so that the
+  kernel's unit arithmetic stays in 32 bits: a 1-D and a 2-D byte segment
+  of 1.5 GiB each (the element-wise path, where a unit is one byte).
+Expected results come from torch slicing on the device.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from elasticmegatron_amd import _native
+from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
+
+pytestmark = pytest.mark.gpu
+
+
+def test_max_buffers(gpu_device):
+    n = _native.EMRS_MAX_BUFFERS
+    size = 4096
+    srcs = [torch.full((size,), i, dtype=torch.uint8, device=gpu_device) for i in range(n)]
+    for i, s in enumerate(srcs):
+        s[:size // 2] = torch.arange(size // 2, device=gpu_device, dtype=torch.int32).to(torch.uint8) ^ i
+    dsts = [torch.zeros(size, dtype=torch.uint8, device=gpu_device) for _ in range(n)]
+    rows = []
+    for i in range(n):
+        j = n - 1 - i
+        rows.append((i, j, 1, 0, i, 3 * i, 1000 + i, 1, 0, 0, 0, 0, 0, 0))        # element-wise path
+        rows.append((i, j, 4, 0, 512, 768, 64, 1, 0, 0, 0, 0, 0, 0))             # 16-byte path
+    t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
+    t[:] = rows
+    plan = _native.Plan(t, [size] * n, [size] * n, check_disjoint=True)
+    plan.execute([s.data_ptr() for s in srcs], [d.data_ptr() for d in dsts], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for i in range(n):
+        j = n - 1 - i
+        want = torch.zeros(size, dtype=torch.uint8, device=gpu_device)
+        want[3 * i:3 * i + 1000 + i] = srcs[i][i:i + 1000 + i]
+        want[768 * 4:(768 + 64) * 4] = srcs[i][512 * 4:(512 + 64) * 4]
+        assert torch.equal(dsts[j], want), (i, j)
+
+
+def test_segments_beyond_two_to_the_thirty_units(gpu_device):
+    nbytes = 3 << 29  # 1.5 GiB
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu_device)
+    dst = torch.zeros(nbytes + 64, dtype=torch.uint8, device=gpu_device)
+    n1 = nbytes - 3
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 1, 0, 1, 2, n1, 1, 0, 0, 0, 0, 0, 0)  # offsets 1 and 2: element-wise, 1-byte units
+    plan = _native.Plan(t, [nbytes], [nbytes + 64])
+    assert plan.stats().n_device_segments >= 2 and plan.stats().scalar_bytes == n1
+    plan.execute([src.data_ptr()], [dst.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[2:2 + n1], src[1:1 + n1])
+    assert int(dst[:2].sum()) == 0 and int(dst[2 + n1:].sum()) == 0
+
+    # 2-D: 1,500,000 rows of 1,000 bytes with strides 1,001 and 1,003 (split by rows).
+    rows, ln = 1_500_000, 1000
+    del dst
+    src2 = src[:rows * 1001]
+    t[0] = (0, 0, 1, 0, 0, 5, ln, rows, 1001, 1003, 0, 0, 0, 0)
+    need = 5 + rows * 1003  # whole last row stride, so that the result can be viewed as rows x 1003
+    dst2 = torch.zeros(need, dtype=torch.uint8, device=gpu_device)
+    plan = _native.Plan(t, [rows * 1001], [need])
+    assert plan.stats().n_device_segments >= 2
+    plan.execute([src2.data_ptr()], [dst2.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = dst2[5:5 + rows * 1003].view(rows, 1003)[:, :ln]
+    want = src2.view(rows, 1001)[:, :ln]
+    assert torch.equal(got, want)
+    assert int(dst2[5:5 + rows * 1003].view(rows, 1003)[:, ln:].sum()) == 0
