@@ -2,8 +2,8 @@
 
 Nothing here is part of the product.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import
-it, and only as the checker (or as the timed CPU restatement of the
-reference); the product path never routes through it.
+it, and only to check results against (or as the timed CPU restatement
+of the reference); the product path never routes through it.
 
 Contents
   synth          numpy restatement of the seeded synthetic generator
@@ -28,6 +28,10 @@ Parity status
   megatron_buffer: parity unpinned.  Megatron-core (core_r0.11.0) is not
   vendored with the reference and cannot be imported here; its layout rules
   are restated from its published algorithm and checked only by invariants.
+  canonical.world(vocab_rows=...): the vocabulary re-padding extension has
+  no counterpart in the reference (virtual_param.py:480-481 keeps the padded
+  vocabulary fixed); it is an invariant (kept rows keep their values, new
+  rows are zero), checked by grow-then-shrink round trips.
   Every other function is pinned by closed forms, brute force on small
   shapes, or the Oracle-1 == Oracle-2 cross-check (see tests/).
 """
