@@ -1030,15 +1030,17 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
 
 int emrs_plan_destroy(emrs_plan *plan) {
   if (!plan) return EMRS_OK;
+  int prev = 0;
+  (void)hipGetDevice(&prev);
   for (size_t d = 0; d < plan->dev_tables.size(); ++d) {
     if (plan->dev_tables[d]) {
-      int prev = 0;
-      (void)hipGetDevice(&prev);
       (void)hipSetDevice((int)d);
+      // Launches enqueued on any stream may still read the table.
+      (void)hipDeviceSynchronize();
       (void)hipFree(plan->dev_tables[d]);
-      (void)hipSetDevice(prev);
     }
   }
+  (void)hipSetDevice(prev);
   delete plan;
   return EMRS_OK;
 }

@@ -145,6 +145,10 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
 int emrs_plan_execute(emrs_plan *plan, void *const *src_bases,
                       void *const *dst_bases, void *stream);
 
+/*
+ * Free the plan.  It first waits for every device that holds its table, so a
+ * plan may be destroyed while launches that use it are still queued.
+ */
 int emrs_plan_destroy(emrs_plan *plan);
 
 /*

@@ -310,6 +310,24 @@ def test_execute_errors(gpu_device):
     assert torch.equal(other[1024:1088], buf[:64])
 
 
+def test_destroy_right_after_execute(gpu_device):
+    """A plan destroyed while its launch is still queued: the launch completes correctly."""
+    n = 1 << 24
+    src = torch.arange(n, dtype=torch.int32, device=gpu_device)
+    dst = torch.zeros(n, dtype=torch.int32, device=gpu_device)
+    side = torch.cuda.Stream(device=gpu_device)
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0, 0, 0, 0, 0)
+    for _ in range(3):
+        dst.zero_()
+        torch.cuda.synchronize()
+        plan = _native.Plan(t, [n * 4], [n * 4])
+        plan.execute([src.data_ptr()], [dst.data_ptr()], side.cuda_stream)
+        plan.close()
+        side.synchronize()
+        assert torch.equal(dst, src)
+
+
 def test_manager_sequence(gpu_device):
     """ElasticMegatronManager.reshard through the tiny TP2DP4 -> TP1DP8 -> TP4DP2 sequence."""
     from elasticmegatron_amd import ElasticMegatronManager, tiny_llama2
