@@ -344,3 +344,27 @@ def test_manager_sequence(gpu_device):
     # Back to the start: the round trip is the identity.
     st = mgr.reshard(new_parallel_strategy=seq[0])
     assert st.verify_synthetic(SEED)[0] == 0
+
+
+def _random_cases():
+    from tests.test_random_switches import _cases
+    return _cases()
+
+
+@pytest.mark.parametrize("spec,src,dst,bf16_source", _random_cases())
+def test_random_switch_kernel_matches_oracle1(gpu_device, spec, src, dst, bf16_source):
+    """The seeded random models and strategy pairs of tests/test_random_switches.py, on the GPU."""
+    print(f"case {spec.name} {src} -> {dst} bf16 {bf16_source}", flush=True)
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    for t in b.arenas():
+        t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
+    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, a, b)
+    got32, gotbf = extract(ld, _host_arenas(b))
+    inv = model.inventory(spec)
+    S, D = strat(src), strat(dst)
+    dw, dbf, _ = oracle1.transfer(inv, spec, S, D, oracle1.build_src_world(inv, spec, S, SEED))
+    assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []
