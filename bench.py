@@ -71,6 +71,8 @@ def parse():
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip timing ElasticMegatronManager.reshard end to end")
     ap.add_argument("--no-copy-ceiling", action="store_true", help="skip the plain-copy reference launch")
+    ap.add_argument("--tensors", action="store_true",
+                    help="run the per-tensor plan (one buffer per stored tensor, as views into the arenas)")
     ap.add_argument("--placement-trials", type=int, default=0,
                     help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
@@ -179,16 +181,30 @@ def main():
     tm = TransferManager(bf16_source=args.bf16_source)
     kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
     plan = tm.compile(ls, ld, kind)
+    tplan = tm.compile_tensors(ls, ld, kind) if args.tensors else None
     t_plan = time.time() - t0
     a = TrainingState.allocate(ls, dev)
     b = TrainingState.allocate(ld, dev, param=a.param if backup is not None else None)
     a.fill_synthetic(SEED, bf16=True)
     torch.cuda.synchronize()
+    views = {}
+
+    def step(a, b):
+        if tplan is None:
+            tm.execute(plan, a, b, stream)
+            return
+        if views.get("a") is not a or views.get("b") is not b:
+            # One tensor view per buffer, as a caller holding per-tensor state passes them.  The cache
+            # holds the states it was built from and is cleared before either is released.
+            views.clear()
+            views.update(a=a, b=b, v=(tplan.src.views(a), tplan.dst.views(b)))
+        tm.execute_tensors(tplan, *views["v"], stream)
+
     print(f"[bench] {args.workload}: plan {plan.segments.shape[0]} segments, payload {plan.payload_bytes / 1e9:.2f} GB,"
           f" planning {t_plan:.2f}s", file=sys.stderr, flush=True)
 
     for _ in range(args.warmup):
-        tm.execute(plan, a, b, stream)
+        step(a, b)
     torch.cuda.synchronize()
     verified = None
     if not args.no_verify:
@@ -204,7 +220,7 @@ def main():
     t_wall = time.perf_counter()
     events[0].record(stream)
     for i in range(args.steps):
-        tm.execute(plan, a, b, stream)
+        step(a, b)
         events[i + 1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1e3
@@ -236,8 +252,10 @@ def main():
         "dtype": "bf16+fp32 (bitwise copy)",
         "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
         "config": {"workload": desc, "params": spec.num_params(), "payload_bytes": payload,
+                   "buffers": (f"one per stored tensor: {len(tplan.src)} source, {len(tplan.dst)} destination"
+                               if tplan is not None else "four arenas per side"),
                    "read_bytes": plan.read_bytes, "bf16_source": tm.bf16_source if backup is None else None,
-                   "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
+                   "segments": int((tplan or plan).segments.shape[0]), "verified_bit_exact": verified,
                    "wall_ms_per_step": round(wall_ms / args.steps, 4),
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4),
                    "median_ms": round(sorted(step_ms)[len(step_ms) // 2], 4),
@@ -251,17 +269,18 @@ def main():
 
         trials = []
         for _ in range(args.placement_trials):
+            views.clear()
             del b
             gc.collect()
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
             b = TrainingState.allocate(ld, dev, param=a.param if backup is not None else None)
             for _ in range(2):
-                tm.execute(plan, a, b, stream)
+                step(a, b)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
             for _ in range(5):
-                tm.execute(plan, a, b, stream)
+                step(a, b)
             e1.record(stream)
             torch.cuda.synchronize()
             trials.append(round(e0.elapsed_time(e1) / 5, 3))
@@ -281,6 +300,7 @@ def main():
             return 3
     if not args.no_copy_ceiling:
         out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
+    views.clear()
     del b
     if not args.no_e2e:
         a, out["config"]["reshard_e2e"] = reshard_end_to_end(a, spec, src, dst, repad, tm, args.no_verify)

@@ -30,7 +30,8 @@ ERRORS = {
     -8: "EMRS_ERR_ALIAS",
 }
 EMRS_PLAN_CHECK_DISJOINT = 1
-EMRS_MAX_BUFFERS = 128
+EMRS_MAX_BUFFERS = 65535
+EMRS_ARG_BUFFERS = 128  # buffers per side passed in kernel arguments (more use a device table)
 
 # Every function include/emrs.h declares.
 EXPORTS = (
@@ -101,7 +102,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
     lib.emrs_plan_compare.restype = I
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
-    if lib.emrs_abi_version() != 1:
+    if lib.emrs_abi_version() != 2:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib

@@ -62,9 +62,15 @@ constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Buffers passed by value in kernel arguments; plans with more buffers on
+// either side pass a device-memory table of pointers instead.  (Kernel
+// arguments are limited to a few KB: this table must stay small.)
+constexpr uint32_t kArgBuffers = 128;
+
 struct Bases {
-  char *p[EMRS_MAX_BUFFERS];
+  char *p[kArgBuffers];
 };
+static_assert(sizeof(Bases) <= 1024, "Bases travels in kernel arguments");
 
 // Segment as the kernel sees it.  Offsets and strides are in units of
 // (1 << unit_log2) bytes: 16 for the vector path, the element size otherwise.
@@ -81,24 +87,28 @@ struct DevSeg {
   uint32_t dst_stride;
   uint32_t aux_stride;
   uint32_t magic;        // row = (t + ((u - t) >> sh1)) >> sh2, t = umulhi(magic, u)
-  uint8_t sh1;
+  uint16_t src_buf;
+  uint16_t dst_buf;
+  uint16_t aux_buf;
   uint8_t sh2;
-  uint8_t unit_log2;
-  uint8_t cast;          // bit 0: also write bf16 to aux; bit 1: write zeros, read nothing
-  uint8_t src_buf;
-  uint8_t dst_buf;
-  uint8_t aux_buf;
-  uint8_t elem_log2;     // element size of the input segment (read only by the compare kernel)
+  uint8_t bits;          // bit 0: sh1; bits 1-3: unit_log2; bits 4-5: cast; bits 6-7: elem_log2
+
+  // cast bit 0: also write bf16 to aux; bit 1: write zeros, read nothing.
+  // elem_log2: element size of the input segment (read only by the compare kernel).
+  __host__ __device__ uint32_t sh1() const { return bits & 1u; }
+  __host__ __device__ uint32_t unit_log2() const { return (bits >> 1) & 7u; }
+  __host__ __device__ uint32_t cast() const { return (bits >> 4) & 3u; }
+  __host__ __device__ uint32_t elem_log2() const { return (bits >> 6) & 3u; }
 };
 static_assert(sizeof(DevSeg) == 64, "DevSeg layout");
 
 // Division by an invariant divisor (Granlund & Montgomery 1994, fig. 4.1).
-void make_magic(uint32_t d, uint32_t *m, uint8_t *sh1, uint8_t *sh2) {
+void make_magic(uint32_t d, uint32_t *m, uint32_t *sh1, uint8_t *sh2) {
   uint32_t l = 0;
   while ((1ull << l) < d) ++l;
   uint64_t num = (uint64_t)(((unsigned __int128)1 << 32) * (((unsigned __int128)1 << l) - d) / d) + 1;
   *m = (uint32_t)num;
-  *sh1 = l < 1 ? (uint8_t)l : 1;
+  *sh1 = l < 1 ? l : 1;
   *sh2 = l > 1 ? (uint8_t)(l - 1) : 0;
 }
 
@@ -209,7 +219,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
 #pragma unroll
   for (int j = 0; j < kUnroll; ++j) {
     const uint32_t u = u0 + min(j * kThreads + tid, n - 1);
-    row[j] = magic_div(u, s.magic, s.sh1, s.sh2);
+    row[j] = magic_div(u, s.magic, s.sh1(), s.sh2);
     col[j] = u - row[j] * s.len;
     if constexpr (kZero) v[j] = T{};
     else v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row[j] * s.src_stride + col[j]);
@@ -223,10 +233,20 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
     }
 }
 
+// Base address of buffer i: from the kernel-argument table, or (kTable) from
+// a device-memory table of pointers for plans with more buffers than fit in
+// kernel arguments.
+template <bool kTable>
+__device__ __forceinline__ char *base_of(const Bases &b, const uint64_t *tab, uint32_t i) {
+  if constexpr (kTable) return reinterpret_cast<char *>(tab[i]);
+  else return b.p[i];
+}
+
 // Copy chunks [c, c_end), starting from the segment that contains chunk c.
-template <bool kNT>
+template <bool kNT, bool kTable>
 __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
-                                               uint64_t c, uint64_t c_end, const Bases &src, const Bases &dst) {
+                                               uint64_t c, uint64_t c_end, const Bases &src, const Bases &dst,
+                                               const uint64_t *src_tab, const uint64_t *dst_tab) {
   // Last segment whose first chunk is <= c.
   uint32_t lo = 0, hi = n_segs - 1;
   while (lo < hi) {
@@ -247,15 +267,16 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
     const uint32_t total = s.len * s.rows;
     const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
     const uint32_t u_end = min(u0 + kChunkUnits, total);
-    const char *sb = src.p[s.src_buf];
-    char *db = dst.p[s.dst_buf];
-    char *ab = dst.p[s.aux_buf];
-    if (s.cast & 2) {  // zero fill, with or without the bf16 image
-      if (s.cast & 1) {
-        if (s.unit_log2 == 4) copy_chunk<u32x4, kNT, true, true>(s, sb, db, ab, u0, u_end);
+    const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
+    char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
+    char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+    const uint32_t cast = s.cast(), ul = s.unit_log2();
+    if (cast & 2) {  // zero fill, with or without the bf16 image
+      if (cast & 1) {
+        if (ul == 4) copy_chunk<u32x4, kNT, true, true>(s, sb, db, ab, u0, u_end);
         else copy_chunk<uint32_t, kNT, true, true>(s, sb, db, ab, u0, u_end);
       } else {
-        switch (s.unit_log2) {
+        switch (ul) {
           case 4: copy_chunk<u32x4, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
           case 3: copy_chunk<uint64_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
           case 2: copy_chunk<uint32_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
@@ -265,12 +286,12 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
       }
       continue;
     }
-    if (s.cast) {
-      if (s.unit_log2 == 4) copy_chunk<u32x4, kNT, true>(s, sb, db, ab, u0, u_end);
+    if (cast) {
+      if (ul == 4) copy_chunk<u32x4, kNT, true>(s, sb, db, ab, u0, u_end);
       else copy_chunk<uint32_t, kNT, true>(s, sb, db, ab, u0, u_end);
       continue;
     }
-    switch (s.unit_log2) {
+    switch (ul) {
       case 4: copy_chunk<u32x4, kNT, false>(s, sb, db, ab, u0, u_end); break;
       case 3: copy_chunk<uint64_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
       case 2: copy_chunk<uint32_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
@@ -287,10 +308,11 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
 // xcd_stride != 0 as well (the grid is then a multiple of 8, and workgroup b
 // runs on XCD b % 8), each XCD sweeps its own contiguous eighth, so that no
 // page is touched from two XCDs' translation caches.
-template <bool kNT>
+template <bool kNT, bool kTable>
 __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
     const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
-    uint64_t chunks_per_block, uint32_t xcd_stride, uint32_t run, Bases src, Bases dst) {
+    uint64_t chunks_per_block, uint32_t xcd_stride, uint32_t run, Bases src, Bases dst,
+    const uint64_t *__restrict__ src_tab, const uint64_t *__restrict__ dst_tab) {
   if (run) {
     uint64_t c1 = n_chunks, c = (uint64_t)blockIdx.x * run, step = (uint64_t)gridDim.x * run;
     if (xcd_stride) {
@@ -300,14 +322,16 @@ __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
       c = c0 + (uint64_t)(blockIdx.x >> 3) * run;
       step = (uint64_t)(gridDim.x >> 3) * run;
     }
-    for (; c < c1; c += step) copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + run, c1), src, dst);
+    for (; c < c1; c += step)
+      copy_chunk_run<kNT, kTable>(segs, n_segs, n_chunks, c, min(c + run, c1), src, dst, src_tab, dst_tab);
     return;
   }
   uint64_t b = blockIdx.x;
   if (xcd_stride) b = (b & 7) * xcd_stride + (b >> 3);  // one contiguous slice per XCD
   const uint64_t c = b * chunks_per_block;
   if (c >= n_chunks) return;
-  copy_chunk_run<kNT>(segs, n_segs, n_chunks, c, min(c + chunks_per_block, n_chunks), src, dst);
+  copy_chunk_run<kNT, kTable>(segs, n_segs, n_chunks, c, min(c + chunks_per_block, n_chunks), src, dst, src_tab,
+                              dst_tab);
 }
 
 // ---------------------------------------------------------------------------
@@ -325,7 +349,8 @@ std::vector<DeviceProps> g_dev_props;
 template <bool kNT>
 void copy_plan_kernel_occupancy(int *out) {
   int v = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, copy_plan_kernel<kNT>, kThreads, 0) != hipSuccess || v <= 0) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, copy_plan_kernel<kNT, false>, kThreads, 0) != hipSuccess ||
+      v <= 0) {
     (void)hipGetLastError();
     v = 4;
   }
@@ -437,15 +462,15 @@ struct Builder {
     d.rows = rows;
     d.src_stride = rows > 1 ? ss : 0;
     d.dst_stride = rows > 1 ? ds : 0;
-    make_magic(len, &d.magic, &d.sh1, &d.sh2);
-    d.unit_log2 = (uint8_t)ul;
-    d.src_buf = (uint8_t)sbuf;
-    d.dst_buf = (uint8_t)dbuf;
-    d.cast = (ax.on ? 1 : 0) | (ax.zero ? 2 : 0);
-    d.aux_buf = (uint8_t)(ax.on ? ax.buf : dbuf);
+    uint32_t sh1 = 0;
+    make_magic(len, &d.magic, &sh1, &d.sh2);
+    const uint32_t cast = (ax.on ? 1u : 0u) | (ax.zero ? 2u : 0u);
+    d.bits = (uint8_t)(sh1 | (ul << 1) | (cast << 4) | ((uint32_t)cur_elem_log2 << 6));
+    d.src_buf = (uint16_t)sbuf;
+    d.dst_buf = (uint16_t)dbuf;
+    d.aux_buf = (uint16_t)(ax.on ? ax.buf : dbuf);
     d.aux_off = ax.on ? aoff : 0;
     d.aux_stride = ax.on && rows > 1 ? astride : 0;
-    d.elem_log2 = cur_elem_log2;
     const uint64_t units = (uint64_t)len * rows;
     chunks += (units + kChunkUnits - 1) / kChunkUnits;
     out.push_back(d);
@@ -504,44 +529,79 @@ int check_disjoint(const emrs_segment *segs, uint64_t n_segs) {
   return EMRS_OK;
 }
 
-// Base pointers of an execution or comparison: copied into kernel-argument
-// tables and checked (only buffers that some segment references).
-int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *dst_bases, Bases *sb, Bases *db) {
+// Base pointers of an execution or comparison, checked (only buffers that
+// some segment references) and laid out for the launch.
+struct ResolvedBases {
+  Bases src{}, dst{};
+  bool table = false;         // pointers go through a device table: src then dst
+  std::vector<uint64_t> ptrs;
+};
+
+int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *dst_bases, ResolvedBases *rb) {
   const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
   if ((ns && !src_bases) || (nd && !dst_bases))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
   // Only buffers that some segment references are checked: an unreferenced
   // buffer may be NULL or alias anything.
-  *sb = Bases{};
-  *db = Bases{};
+  struct Iv {
+    uintptr_t b, e;
+    bool dst;
+  };
+  std::vector<Iv> iv;
+  iv.reserve(ns + nd);
   for (uint32_t i = 0; i < ns; ++i) {
-    sb->p[i] = static_cast<char *>(src_bases[i]);
     if (!plan->src_used[i]) continue;
-    if (!sb->p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
-    if (reinterpret_cast<uintptr_t>(sb->p[i]) % 16)
-      return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
+    const uintptr_t b = reinterpret_cast<uintptr_t>(src_bases[i]);
+    if (!b) return fail(EMRS_ERR_INVALID_ARGUMENT, "source base is NULL");
+    if (b % 16) return fail(EMRS_ERR_MISALIGNED, "source base is not 16-byte aligned");
+    if (plan->src_bytes[i]) iv.push_back({b, b + plan->src_bytes[i], false});
   }
   for (uint32_t i = 0; i < nd; ++i) {
-    db->p[i] = static_cast<char *>(dst_bases[i]);
     if (!plan->dst_used[i]) continue;
-    if (!db->p[i]) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
-    if (reinterpret_cast<uintptr_t>(db->p[i]) % 16)
-      return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
+    const uintptr_t b = reinterpret_cast<uintptr_t>(dst_bases[i]);
+    if (!b) return fail(EMRS_ERR_INVALID_ARGUMENT, "destination base is NULL");
+    if (b % 16) return fail(EMRS_ERR_MISALIGNED, "destination base is not 16-byte aligned");
+    if (plan->dst_bytes[i]) iv.push_back({b, b + plan->dst_bytes[i], true});
   }
-  auto overlap = [](uintptr_t a0, uint64_t an, uintptr_t b0, uint64_t bn) {
-    return an && bn && a0 < b0 + bn && b0 < a0 + an;
-  };
-  for (uint32_t j = 0; j < nd; ++j) {
-    if (!plan->dst_used[j]) continue;
-    const uintptr_t d0 = reinterpret_cast<uintptr_t>(db->p[j]);
-    for (uint32_t i = 0; i < ns; ++i)
-      if (plan->src_used[i] &&
-          overlap(reinterpret_cast<uintptr_t>(sb->p[i]), plan->src_bytes[i], d0, plan->dst_bytes[j]))
-        return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
-    for (uint32_t k = j + 1; k < nd; ++k)
-      if (plan->dst_used[k] &&
-          overlap(d0, plan->dst_bytes[j], reinterpret_cast<uintptr_t>(db->p[k]), plan->dst_bytes[k]))
-        return fail(EMRS_ERR_ALIAS, "two destination buffers overlap");
+  // Out of place: no destination range may overlap another referenced range.
+  // Sweep in address order; an earlier range overlaps the current one exactly
+  // when its end lies past the current start.
+  std::sort(iv.begin(), iv.end(), [](const Iv &x, const Iv &y) { return x.b < y.b; });
+  uintptr_t end_src = 0, end_dst = 0;
+  for (const Iv &x : iv) {
+    if (x.b < end_dst)
+      return fail(EMRS_ERR_ALIAS, x.dst ? "two destination buffers overlap" : "a source buffer overlaps a destination buffer");
+    if (x.dst && x.b < end_src) return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
+    (x.dst ? end_dst : end_src) = std::max(x.dst ? end_dst : end_src, x.e);
+  }
+  rb->table = ns > kArgBuffers || nd > kArgBuffers;
+  if (rb->table) {
+    rb->ptrs.resize((size_t)ns + nd);
+    for (uint32_t i = 0; i < ns; ++i) rb->ptrs[i] = reinterpret_cast<uint64_t>(src_bases[i]);
+    for (uint32_t i = 0; i < nd; ++i) rb->ptrs[ns + i] = reinterpret_cast<uint64_t>(dst_bases[i]);
+  } else {
+    for (uint32_t i = 0; i < ns; ++i) rb->src.p[i] = static_cast<char *>(src_bases[i]);
+    for (uint32_t i = 0; i < nd; ++i) rb->dst.p[i] = static_cast<char *>(dst_bases[i]);
+  }
+  return EMRS_OK;
+}
+
+// Stream-ordered device copy of the pointer table; freed after the launch
+// with free_pointer_table on the same stream.
+int upload_pointer_table(const ResolvedBases &rb, hipStream_t st, uint64_t **out) {
+  *out = nullptr;
+  if (!rb.table) return EMRS_OK;
+  const size_t bytes = rb.ptrs.size() * sizeof(uint64_t);
+  hipError_t e = hipMallocAsync(reinterpret_cast<void **>(out), bytes, st);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    return hip_fail(e, "hipMallocAsync(pointer table)");
+  }
+  e = hipMemcpyAsync(*out, rb.ptrs.data(), bytes, hipMemcpyHostToDevice, st);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(*out, st);
+    *out = nullptr;
+    return hip_fail(e, "hipMemcpyAsync(pointer table)");
   }
   return EMRS_OK;
 }
@@ -664,19 +724,19 @@ __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase
     if (u >= u_end) break;
     uint64_t so = s.src_off + u, dof = s.dst_off + u, ao = s.aux_off + u;
     if (s.rows > 1) {
-      const uint32_t row = magic_div(u, s.magic, s.sh1, s.sh2), col = u - row * s.len;
+      const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2), col = u - row * s.len;
       so = s.src_off + (uint64_t)row * s.src_stride + col;
       dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
       ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
     }
-    const T e = (s.cast & 2) ? T{} : src[so];
+    const T e = (s.cast() & 2) ? T{} : src[so];
     const T g = dst[dof];
     uint32_t ew[4] = {0, 0, 0, 0}, gw[4] = {0, 0, 0, 0};
     words_of(e, ew);
     words_of(g, gw);
-    cmp_words(m, ew, gw, (uint32_t)sizeof(T), s.elem_log2);
+    cmp_words(m, ew, gw, (uint32_t)sizeof(T), s.elem_log2());
     if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
-      if (s.cast & 1) {
+      if (s.cast() & 1) {
         uint32_t ea[2] = {0, 0}, ga[2] = {0, 0};
         aux_words_of(C::cast(e), ea);
         aux_words_of(aux[ao], ga);
@@ -730,9 +790,11 @@ __device__ void flush(const LaneAcc &a, GroupAcc *g) {
 
 // One workgroup per chunk, grid-stride over the chunks.  No early exit: every
 // thread reaches every barrier.
+template <bool kTable>
 __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
-    uint32_t n_segs, uint64_t n_chunks, Bases src, Bases dst, GroupAcc *__restrict__ acc) {
+    uint32_t n_segs, uint64_t n_chunks, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
+    const uint64_t *__restrict__ dst_tab, GroupAcc *__restrict__ acc) {
   __shared__ double lds_d[2 * kThreads / 64];
   __shared__ uint32_t lds_u[2 * kThreads / 64];
   __shared__ float lds_f[2 * kThreads / 64];
@@ -747,11 +809,11 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     const uint32_t total = s.len * s.rows;
     const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
     const uint32_t u_end = min(u0 + kChunkUnits, total);
-    const char *sb = src.p[s.src_buf];
-    const char *db = dst.p[s.dst_buf];
-    const char *ab = dst.p[s.aux_buf];
+    const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
+    const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
+    const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
     LaneAcc m, x;
-    switch (s.unit_log2) {
+    switch (s.unit_log2()) {
       case 4: compare_chunk<u32x4>(s, sb, db, ab, u0, u_end, m, x); break;
       case 3: compare_chunk<uint64_t>(s, sb, db, ab, u0, u_end, m, x); break;
       case 2: compare_chunk<uint32_t>(s, sb, db, ab, u0, u_end, m, x); break;
@@ -760,7 +822,7 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     }
     block_reduce(m, lds_d, lds_u, lds_f);
     if (threadIdx.x == 0) flush(m, acc + groups[lo]);
-    if (s.cast & 1) {  // uniform across the workgroup
+    if (s.cast() & 1) {  // uniform across the workgroup
       block_reduce(x, lds_d, lds_u, lds_f);
       if (threadIdx.x == 0) flush(x, acc + aux_groups[lo]);
     }
@@ -915,8 +977,8 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
                       void *stream) {
   g_last_error.clear();
   if (!plan) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan is NULL");
-  Bases sb, db;
-  int rc = resolve_bases(plan, src_bases, dst_bases, &sb, &db);
+  ResolvedBases rb;
+  int rc = resolve_bases(plan, src_bases, dst_bases, &rb);
   if (rc) return rc;
   if (plan->n_chunks == 0) return EMRS_OK;
 
@@ -944,14 +1006,27 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   if (!remap && !run) blocks = (plan->n_chunks + cpb - 1) / cpb;
   const uint32_t xcd_stride = remap ? (uint32_t)(blocks / 8) : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (nt)
-    hipLaunchKernelGGL(copy_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
-                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, run, sb, db);
+  uint64_t *tab = nullptr;
+  rc = upload_pointer_table(rb, st, &tab);
+  if (rc) return rc;
+  const uint64_t *stab = tab, *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
+  const dim3 grid((uint32_t)blocks), block(kThreads);
+  const uint32_t nseg = (uint32_t)plan->segs.size();
+  if (nt && rb.table)
+    hipLaunchKernelGGL((copy_plan_kernel<true, true>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
+                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+  else if (nt)
+    hipLaunchKernelGGL((copy_plan_kernel<true, false>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
+                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+  else if (rb.table)
+    hipLaunchKernelGGL((copy_plan_kernel<false, true>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
+                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
   else
-    hipLaunchKernelGGL(copy_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table,
-                       (uint32_t)plan->segs.size(), plan->n_chunks, cpb, xcd_stride, run, sb, db);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "copy_plan_kernel launch");
+    hipLaunchKernelGGL((copy_plan_kernel<false, false>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
+                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+  hipError_t le = hipGetLastError();
+  if (tab) (void)hipFreeAsync(tab, st);
+  if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
   return EMRS_OK;
 }
 
@@ -964,8 +1039,8 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   for (uint64_t i = 0; i < n_in; ++i)
     if ((groups && groups[i] >= n_groups) || (aux_groups && aux_groups[i] >= n_groups))
       return fail(EMRS_ERR_INVALID_ARGUMENT, "group id >= n_groups");
-  Bases sb, db;
-  int rc = resolve_bases(plan, src_bases, dst_bases, &sb, &db);
+  ResolvedBases rb;
+  int rc = resolve_bases(plan, src_bases, dst_bases, &rb);
   if (rc) return rc;
 
   // Per device segment: its groups, and the element counts on the host.
@@ -979,8 +1054,8 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
     g_host[k] = g;
     g_host[nd + k] = ga;
     const uint64_t units = (uint64_t)d.len * d.rows;
-    elements[g] += units << (d.unit_log2 - d.elem_log2);
-    if (d.cast & 1) elements[ga] += units << (d.unit_log2 - 2);
+    elements[g] += units << (d.unit_log2() - d.elem_log2());
+    if (d.cast() & 1) elements[ga] += units << (d.unit_log2() - 2);
   }
   for (uint32_t g = 0; g < n_groups; ++g) {
     stats[g] = emrs_compare_stats{};
@@ -1006,12 +1081,20 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   std::vector<GroupAcc> host(n_groups);
   e = hipMemsetAsync(acc, 0, acc_bytes, st);
   if (e == hipSuccess) e = hipMemcpyAsync(grp, g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
+  uint64_t *tab = nullptr;
+  if (e == hipSuccess && upload_pointer_table(rb, st, &tab) != EMRS_OK) e = hipErrorOutOfMemory;
   if (e == hipSuccess) {
     const uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * 8);
-    hipLaunchKernelGGL(compare_plan_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp, grp + nd,
-                       (uint32_t)nd, plan->n_chunks, sb, db, acc);
+    const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
+    if (rb.table)
+      hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
+                         grp + nd, (uint32_t)nd, plan->n_chunks, rb.src, rb.dst, tab, dtab, acc);
+    else
+      hipLaunchKernelGGL(compare_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
+                         grp + nd, (uint32_t)nd, plan->n_chunks, rb.src, rb.dst, tab, dtab, acc);
     e = hipGetLastError();
   }
+  if (tab) (void)hipFreeAsync(tab, st);
   if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   (void)hipFree(buf);

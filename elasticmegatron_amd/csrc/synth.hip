@@ -50,9 +50,14 @@ struct DevPiece {
   uint32_t buf, kind;
 };
 
+// Buffers of a synthetic fill or check, passed by value in kernel arguments
+// (which are limited to a few KB).
+constexpr uint32_t kSynthBuffers = 128;
+
 struct SynthBases {
-  char *p[EMRS_MAX_BUFFERS];
+  char *p[kSynthBuffers];
 };
+static_assert(sizeof(SynthBases) <= 1024, "SynthBases travels in kernel arguments");
 
 __device__ __forceinline__ uint32_t synth_bits(const DevPiece &pc, float scale, uint64_t i) {
   const uint64_t li = pc.local_start + i;
@@ -138,7 +143,7 @@ int sfail(int code, const std::string &m) { return emrs_internal::fail(code, m);
 int build_pieces(const emrs_piece *pieces, uint64_t n, const uint64_t *buf_bytes, uint32_t n_bufs,
                  uint64_t seed, std::vector<DevPiece> *out, uint64_t *n_chunks) {
   if (n && !pieces) return sfail(EMRS_ERR_INVALID_ARGUMENT, "pieces is NULL");
-  if (n_bufs > EMRS_MAX_BUFFERS) return sfail(EMRS_ERR_TOO_MANY_BUFFERS, "too many buffers");
+  if (n_bufs > kSynthBuffers) return sfail(EMRS_ERR_TOO_MANY_BUFFERS, "more than 128 buffers");
   if (n_bufs && !buf_bytes) return sfail(EMRS_ERR_INVALID_ARGUMENT, "buf_bytes is NULL");
   if (n >= (1ull << 24)) return sfail(EMRS_ERR_INVALID_ARGUMENT, "too many pieces");
   uint64_t chunks = 0;

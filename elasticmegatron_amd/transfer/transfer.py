@@ -26,6 +26,7 @@ from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import StrategyLayout
+from ..resharding.tensors import TensorBuffers, rebase_on_tensors
 from .verify import VerifyReport, report_from_stats
 
 
@@ -56,6 +57,18 @@ def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
         if all(space.spec.padded_vocab_size % t == 0 for t in tps):
             return space
     return None
+
+
+@dataclass
+class CompiledTensorPlan:
+    """A switch over per-tensor buffers (one buffer per stored tensor; see resharding.tensors)."""
+
+    segments: np.ndarray
+    native: _native.Plan
+    src: TensorBuffers
+    dst: TensorBuffers
+    payload_bytes: int
+    read_bytes: int
 
 
 class TransferManager:
@@ -112,6 +125,44 @@ class TransferManager:
                           read_bytes(table), src.strategy, dst.strategy, comm)
         self._plans[key] = cp
         return cp
+
+    def compile_tensors(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
+                        include_bf16: bool = True) -> CompiledTensorPlan:
+        """The switch over one buffer per stored tensor, as the reference holds them: the
+        ``OptimizerTensorInfo`` tensors of every (rank, parameter) and the bf16 parameter of every
+        model-parallel shard.  ``plan.src.keys`` / ``plan.dst.keys`` name the tensors in buffer
+        order."""
+        key = ("tensors", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
+               self.bf16_source)
+        cp = self._plans.get(key)
+        if cp is not None:
+            return cp
+        arena_plan = self.compile(src, dst, kind, include_bf16)
+        sb, db = TensorBuffers(src), TensorBuffers(dst)
+        table = rebase_on_tensors(arena_plan.segments, sb, db)
+        cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,
+                                payload_bytes(table), read_bytes(table))
+        self._plans[key] = cp
+        return cp
+
+    def execute_tensors(self, plan: CompiledTensorPlan, src_tensors, dst_tensors,
+                        stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Run a per-tensor plan; ``src_tensors`` / ``dst_tensors`` follow ``plan.src.keys`` / ``plan.dst.keys``."""
+        if self.fake_transfer:
+            return
+        if len(src_tensors) != len(plan.src) or len(dst_tensors) != len(plan.dst):
+            raise ValueError("tensor lists do not match the plan's buffers")
+        for t, n in zip(list(src_tensors) + list(dst_tensors), plan.src.numel + plan.dst.numel):
+            if t.numel() != n or not t.is_contiguous():
+                raise ValueError("a tensor does not match its buffer (size or layout)")
+        dev = src_tensors[0].device if len(src_tensors) else dst_tensors[0].device
+        if dev.type != "cuda":
+            raise RuntimeError("tensors must live in GPU memory: the reshard has no CPU path")
+        st = stream if stream is not None else torch.cuda.current_stream(dev)
+        with torch.cuda.device(dev):
+            plan.native.execute([t.data_ptr() for t in src_tensors], [t.data_ptr() for t in dst_tensors],
+                                st.cuda_stream)
+        self._payload_bytes += plan.payload_bytes
 
     def execute(self, plan: CompiledPlan, src: TrainingState, dst: TrainingState,
                 stream: Optional[torch.cuda.Stream] = None) -> None:

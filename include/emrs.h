@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 1
+#define EMRS_ABI_VERSION 2
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -58,8 +58,11 @@ extern "C" {
 #define EMRS_ERR_TOO_MANY_BUFFERS (-7)
 #define EMRS_ERR_ALIAS (-8)
 
-/* Maximum number of source (and, separately, destination) buffers. */
-#define EMRS_MAX_BUFFERS 128
+/* Maximum number of source (and, separately, destination) buffers.  Up to
+ * 128 per side travel in kernel arguments; a plan with more on either side
+ * passes its base pointers through a device table that each execution
+ * uploads and frees on its stream (hipMallocAsync / hipFreeAsync). */
+#define EMRS_MAX_BUFFERS 65535
 
 /* emrs_plan_create flags */
 #define EMRS_PLAN_CHECK_DISJOINT 1u /* reject plans whose destination ranges overlap */
@@ -249,6 +252,7 @@ typedef struct emrs_piece {
 } emrs_piece;
 
 /* Write the synthetic values of every piece into its buffer. */
+/* emrs_synth_fill / emrs_synth_verify take at most 128 buffers. */
 int emrs_synth_fill(const emrs_piece *pieces, uint64_t n_pieces,
                     void *const *bases, const uint64_t *buf_bytes,
                     uint32_t n_bufs, uint64_t seed, void *stream);

@@ -1,6 +1,7 @@
 """GPU: the executor at the limits of its ABI.
 
-- EMRS_MAX_BUFFERS (128) source and destination buffers in one plan.
+- 128 source and destination buffers (passed in kernel arguments) and 3000
+  (passed through a device table of pointers) in one plan.
 - Segments beyond 2^30 units, which emrs_plan_create splits so that the
   kernel's unit arithmetic stays in 32 bits: a 1-D and a 2-D byte segment
   of 1.5 GiB each (the element-wise path, where a unit is one byte).
@@ -17,17 +18,20 @@ from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
 pytestmark = pytest.mark.gpu
 
 
-def test_max_buffers(gpu_device):
-    n = _native.EMRS_MAX_BUFFERS
+@pytest.mark.parametrize("n", [_native.EMRS_ARG_BUFFERS, 3000])
+def test_many_buffers(gpu_device, n):
+    """128 buffers per side (kernel arguments) and 3000 (device pointer table)."""
     size = 4096
-    srcs = [torch.full((size,), i, dtype=torch.uint8, device=gpu_device) for i in range(n)]
-    for i, s in enumerate(srcs):
-        s[:size // 2] = torch.arange(size // 2, device=gpu_device, dtype=torch.int32).to(torch.uint8) ^ i
+    srcs = []
+    for i in range(n):
+        t = torch.arange(size, device=gpu_device, dtype=torch.int32).to(torch.uint8) ^ (i % 251)
+        srcs.append(t)
     dsts = [torch.zeros(size, dtype=torch.uint8, device=gpu_device) for _ in range(n)]
     rows = []
     for i in range(n):
         j = n - 1 - i
-        rows.append((i, j, 1, 0, i, 3 * i, 1000 + i, 1, 0, 0, 0, 0, 0, 0))        # element-wise path
+        k = i % 200
+        rows.append((i, j, 1, 0, k, 3 * k, 1000 + k, 1, 0, 0, 0, 0, 0, 0))        # element-wise path
         rows.append((i, j, 4, 0, 512, 768, 64, 1, 0, 0, 0, 0, 0, 0))             # 16-byte path
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
@@ -35,9 +39,9 @@ def test_max_buffers(gpu_device):
     plan.execute([s.data_ptr() for s in srcs], [d.data_ptr() for d in dsts], torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     for i in range(n):
-        j = n - 1 - i
+        j, k = n - 1 - i, i % 200
         want = torch.zeros(size, dtype=torch.uint8, device=gpu_device)
-        want[3 * i:3 * i + 1000 + i] = srcs[i][i:i + 1000 + i]
+        want[3 * k:3 * k + 1000 + k] = srcs[i][k:k + 1000 + k]
         want[768 * 4:(768 + 64) * 4] = srcs[i][512 * 4:(512 + 64) * 4]
         assert torch.equal(dsts[j], want), (i, j)
 

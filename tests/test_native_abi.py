@@ -25,7 +25,7 @@ def test_exports_every_declared_symbol():
     assert set(declared) == set(_native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.emrs_abi_version() == 1
+    assert lib.emrs_abi_version() == 2
 
 
 def test_record_layouts_match_header():
@@ -99,7 +99,7 @@ def test_plan_create_overlap_check():
 
 def test_too_many_buffers():
     with pytest.raises(_native.EmrsError) as e:
-        _native.Plan(_seg(), [64] * 129, [64])
+        _native.Plan(_seg(), [64] * 65536, [64])
     assert e.value.code == -7
 
 
