@@ -39,6 +39,8 @@ class CompiledPlan:
     src: ParallelStrategy
     dst: ParallelStrategy
     reference_comm_bytes: int = 0   # the reference's per-rank cross-rank volume, max over ranks
+    src_buf_bytes: Tuple[int, ...] = ()   # arena sizes the plan was checked against
+    dst_buf_bytes: Tuple[int, ...] = ()
 
     @property
     def traffic_bytes(self) -> int:
@@ -122,7 +124,7 @@ class TransferManager:
         else:  # param_migrate is a local copy (training_state.py:40-60)
             comm = 0
         cp = CompiledPlan(table, _native.Plan(table, sb, db, self.check_disjoint), payload_bytes(table),
-                          read_bytes(table), src.strategy, dst.strategy, comm)
+                          read_bytes(table), src.strategy, dst.strategy, comm, tuple(sb), tuple(db))
         self._plans[key] = cp
         return cp
 
@@ -152,9 +154,9 @@ class TransferManager:
             return
         if len(src_tensors) != len(plan.src) or len(dst_tensors) != len(plan.dst):
             raise ValueError("tensor lists do not match the plan's buffers")
-        for t, n in zip(list(src_tensors) + list(dst_tensors), plan.src.numel + plan.dst.numel):
-            if t.numel() != n or not t.is_contiguous():
-                raise ValueError("a tensor does not match its buffer (size or layout)")
+        for t, nb in zip(list(src_tensors) + list(dst_tensors), plan.src.nbytes() + plan.dst.nbytes()):
+            if t.numel() * t.element_size() != nb or not t.is_contiguous():
+                raise ValueError("a tensor does not match its buffer (bytes or layout)")
         dev = src_tensors[0].device if len(src_tensors) else dst_tensors[0].device
         if dev.type != "cuda":
             raise RuntimeError("tensors must live in GPU memory: the reshard has no CPU path")
@@ -174,6 +176,12 @@ class TransferManager:
             raise ValueError("source and destination states must be on the same device")
         if src.device.type != "cuda":
             raise RuntimeError("training states must live in GPU memory: the reshard has no CPU path")
+        # The kernel trusts the sizes the plan was built for; a state laid out for another model
+        # (another padded vocabulary, say) must not reach it.
+        for have, need in zip(src.arena_bytes() + dst.arena_bytes(), plan.src_buf_bytes + plan.dst_buf_bytes):
+            if need and have < need:
+                raise ValueError("a training state's arena is smaller than the plan's buffer: "
+                                 "it was laid out for another model")
         st = stream if stream is not None else torch.cuda.current_stream(src.device)
         with torch.cuda.device(src.device):
             plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)

@@ -132,3 +132,37 @@ def test_reference_constructor_arguments_are_accepted():
     assert calls == []   # one device: every hop is a local copy inside the plan
     with pytest.raises(ValueError):
         TransferManager(bf16_source="fp8")
+
+
+def test_execute_refuses_states_of_another_model(monkeypatch):
+    """A plan runs only on arenas at least as large as those it was built for (no device access otherwise)."""
+    from dataclasses import replace
+
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+    from tests.helpers import small_llama3
+
+    spec = replace(small_llama3(), vocab_size=2300)
+    big = build_virtual_model(spec.with_padded_vocab(2560))
+    small = build_virtual_model(spec.with_padded_vocab(2304))
+    s, d = ParallelStrategy(8, 4, 1), ParallelStrategy(8, 2, 1)
+    tm = TransferManager()
+    plan = tm.compile(big.layout(s), big.layout(d))
+    a = TrainingState.allocate(small.layout(s), "cpu")
+    b = TrainingState.allocate(small.layout(d), "cpu")
+    # Pretend the states are on a GPU: the size check comes before any device work.
+    monkeypatch.setattr(TrainingState, "device", property(lambda self: torch.device("cuda", 0)))
+    with pytest.raises(ValueError, match="another model"):
+        tm.execute(plan, a, b)
+
+
+def test_execute_tensors_checks_bytes():
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(tiny_llama2())
+    tm = TransferManager()
+    tp = tm.compile_tensors(space.layout(ParallelStrategy(**SEQ[0])), space.layout(ParallelStrategy(**SEQ[1])))
+    src = [torch.empty(n, dtype=torch.float32 if k[0] != "param" else torch.bfloat16) for n, k in
+           zip(tp.src.numel, tp.src.keys)]
+    dst = [torch.empty(n, dtype=torch.int8) for n in tp.dst.numel]   # right numel, too few bytes
+    with pytest.raises(ValueError, match="bytes"):
+        tm.execute_tensors(tp, src, dst)
