@@ -85,6 +85,31 @@ class TensorBuffers:
             raise ValueError(f"{ARENA_NAMES[arena]} element {off} lies in padding")
         return b, off - self.offset[b]
 
+    def locate_many(self, arenas: np.ndarray, offs: np.ndarray, extents: np.ndarray):
+        """Vector form of :meth:`locate` for ranges [off, off + extent): (buffer ids, offsets,
+        whether the whole range lies in that one tensor).  Rows whose arena has no tensors
+        come back with ok = False."""
+        arenas = np.asarray(arenas, dtype=np.int64)
+        offs = np.asarray(offs, dtype=np.int64)
+        ids = np.zeros(len(offs), dtype=np.int64)
+        local = np.zeros(len(offs), dtype=np.int64)
+        ok = np.zeros(len(offs), dtype=bool)
+        numel = np.asarray(self.numel, dtype=np.int64)
+        for a in np.unique(arenas):
+            m = arenas == a
+            if int(a) not in self._starts:
+                continue
+            starts = np.asarray(self._starts[int(a)], dtype=np.int64)
+            idmap = np.asarray(self._ids[int(a)], dtype=np.int64)
+            j = np.searchsorted(starts, offs[m], side="right") - 1
+            valid = j >= 0
+            jj = np.where(valid, j, 0)
+            b = idmap[jj]
+            loc = offs[m] - starts[jj]
+            ids[m], local[m] = b, loc
+            ok[m] = valid & (loc + np.asarray(extents)[m] <= numel[b])
+        return ids, local, ok
+
     def boundaries(self, arena: int, lo: int, hi: int) -> List[int]:
         """Tensor starts strictly inside (lo, hi)."""
         starts = self._starts[arena]
@@ -104,52 +129,66 @@ def rebase_on_tensors(table: np.ndarray, src: TensorBuffers, dst: TensorBuffers)
     A one-row segment that runs across tensor boundaries (tensors of one
     parameter on consecutive ranks can be adjacent in an arena) is cut at
     every boundary on the source, destination and bf16-image sides; a
-    strided segment always lies inside one tensor on each side.
+    strided segment always lies inside one tensor on each side.  Segments
+    that need no cut are mapped in bulk.
     """
-    out = []
-    for s in table:
-        n, rows = int(s["len"]), int(s["rows"])
-        if n == 0:
-            continue
-        zero = bool(int(s["flags"]) & SEG_ZERO_FILL)
-        cast = bool(int(s["flags"]) & SEG_CAST_BF16)
-        sa, da = int(s["src_buf"]), int(s["dst_buf"])
-        so, do, ao = int(s["src_off"]), int(s["dst_off"]), int(s["aux_off"])
-        if rows > 1:
-            cuts = [0, n]
-            _check_inside(src, sa, so, (rows - 1) * int(s["src_stride"]) + n, zero)
-            _check_inside(dst, da, do, (rows - 1) * int(s["dst_stride"]) + n, False)
-            if cast:
-                _check_inside(dst, ARENA_PARAM, ao, (rows - 1) * int(s["aux_stride"]) + n, False)
-        else:
-            pts = {0, n}
-            if not zero:
-                pts.update(b - so for b in src.boundaries(sa, so, so + n))
-            pts.update(b - do for b in dst.boundaries(da, do, do + n))
-            if cast:
-                pts.update(b - ao for b in dst.boundaries(ARENA_PARAM, ao, ao + n))
-            cuts = sorted(pts)
-        for c0, c1 in zip(cuts, cuts[1:]):
-            r = s.copy()
-            if zero:
-                r["src_buf"], r["src_off"] = 0, 0
-            else:
-                r["src_buf"], r["src_off"] = src.locate(sa, so + c0)
-            r["dst_buf"], r["dst_off"] = dst.locate(da, do + c0)
-            if cast:
-                r["aux_buf"], r["aux_off"] = dst.locate(ARENA_PARAM, ao + c0)
-            if rows == 1:
-                r["len"] = c1 - c0
-            out.append(r)
-    return np.array(out, dtype=SEGMENT_DTYPE) if out else np.zeros(0, dtype=SEGMENT_DTYPE)
+    table = table[(table["len"] > 0)]
+    n = len(table)
+    if n == 0:
+        return np.zeros(0, dtype=SEGMENT_DTYPE)
+    ln = table["len"].astype(np.int64)
+    rows = table["rows"].astype(np.int64)
+    zero = (table["flags"] & SEG_ZERO_FILL) != 0
+    cast = (table["flags"] & SEG_CAST_BF16) != 0
+    ext_s = np.where(rows > 1, (rows - 1) * table["src_stride"].astype(np.int64), 0) + ln
+    ext_d = np.where(rows > 1, (rows - 1) * table["dst_stride"].astype(np.int64), 0) + ln
+    ext_a = np.where(rows > 1, (rows - 1) * table["aux_stride"].astype(np.int64), 0) + ln
+    sb, so, s_ok = src.locate_many(table["src_buf"], table["src_off"], ext_s)
+    db, do, d_ok = dst.locate_many(table["dst_buf"], table["dst_off"], ext_d)
+    ab, ao, a_ok = dst.locate_many(np.full(n, ARENA_PARAM), table["aux_off"], ext_a)
+    fits = (zero | s_ok) & d_ok & (~cast | a_ok)
+    out = table[fits].copy()
+    f = np.flatnonzero(fits)
+    out["src_buf"] = np.where(zero[f], 0, sb[f])
+    out["src_off"] = np.where(zero[f], 0, so[f])
+    out["dst_buf"], out["dst_off"] = db[f], do[f]
+    out["aux_buf"] = np.where(cast[f], ab[f], out["aux_buf"])
+    out["aux_off"] = np.where(cast[f], ao[f], out["aux_off"])
+    rest = [_cut(s, src, dst) for s in table[~fits]]
+    if rest:
+        out = np.concatenate([out] + rest)
+    return out
 
 
-def _check_inside(bufs: TensorBuffers, arena: int, off: int, extent: int, skip: bool) -> None:
-    if skip:
-        return
-    b, local = bufs.locate(arena, off)
-    if local + extent > bufs.numel[b]:
+def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
+    """One segment that crosses tensor boundaries, cut at each of them."""
+    n, rows = int(s["len"]), int(s["rows"])
+    if rows > 1:
         raise AssertionError("a strided segment leaves its tensor")
+    zero = bool(int(s["flags"]) & SEG_ZERO_FILL)
+    cast = bool(int(s["flags"]) & SEG_CAST_BF16)
+    sa, da = int(s["src_buf"]), int(s["dst_buf"])
+    so, do, ao = int(s["src_off"]), int(s["dst_off"]), int(s["aux_off"])
+    pts = {0, n}
+    if not zero:
+        pts.update(b - so for b in src.boundaries(sa, so, so + n))
+    pts.update(b - do for b in dst.boundaries(da, do, do + n))
+    if cast:
+        pts.update(b - ao for b in dst.boundaries(ARENA_PARAM, ao, ao + n))
+    cuts = sorted(pts)
+    out = np.zeros(len(cuts) - 1, dtype=SEGMENT_DTYPE)
+    for i, (c0, c1) in enumerate(zip(cuts, cuts[1:])):
+        r = s.copy()
+        if zero:
+            r["src_buf"], r["src_off"] = 0, 0
+        else:
+            r["src_buf"], r["src_off"] = src.locate(sa, so + c0)
+        r["dst_buf"], r["dst_off"] = dst.locate(da, do + c0)
+        if cast:
+            r["aux_buf"], r["aux_off"] = dst.locate(ARENA_PARAM, ao + c0)
+        r["len"] = c1 - c0
+        out[i] = r
+    return out
 
 
 def tensor_sizes(bufs: TensorBuffers) -> Sequence[int]:
