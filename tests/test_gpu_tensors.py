@@ -68,3 +68,39 @@ def test_full_size_tensor_views(gpu_device):
         a = b = None  # noqa: F841
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+
+
+def test_compare_through_pointer_table(gpu_device):
+    """emrs_plan_compare over a per-tensor plan with more than 128 buffers per side."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 1, 1)), space.layout(PS(6, 2, 1))
+    tm = TransferManager()
+    tp = tm.compile_tensors(ls, ld)
+    assert len(tp.src) > 128 and len(tp.dst) > 128
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    sv, dv = tp.src.views(a), tp.dst.views(b)
+    tm.execute_tensors(tp, sv, dv)
+    stream = torch.cuda.current_stream().cuda_stream
+    ps, pd = [t.data_ptr() for t in sv], [t.data_ptr() for t in dv]
+    stats = tp.native.compare(ps, pd, stream=stream)
+    total = int((tp.segments["len"] * tp.segments["rows"]).sum()) + \
+        int((tp.segments["len"] * tp.segments["rows"])[(tp.segments["flags"] & 1) != 0].sum())
+    assert int(stats["elements"][0]) == total and int(stats["mismatches"][0]) == 0
+    # One element changed on the host, uploaded back: exactly one mismatch.
+    host = b.main.cpu()
+    host[7] = host[7] + 1.0
+    b.main.copy_(host)
+    torch.cuda.synchronize()
+    stats = tp.native.compare(ps, pd, stream=stream)
+    assert int(stats["mismatches"][0]) == (1 if 7 in _covered(tp, ld) else 0)
+
+
+def _covered(tp, ld):
+    """Element indices of the main arena that some fp32 tensor holds (the checked ones)."""
+    out = set()
+    for a, o, n in zip(tp.dst.arena, tp.dst.offset, tp.dst.numel):
+        if a == 0 and o <= 7 < o + n:
+            out.add(7)
+    return out
