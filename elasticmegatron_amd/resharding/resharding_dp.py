@@ -13,7 +13,7 @@ from __future__ import annotations
 from typing import TYPE_CHECKING, Any, Dict, List, Optional
 
 from ..megatron_manager.parallel_strategy import ParallelStrategy, global_rank_of
-from .ddp_layout import BufferLayout, build_buffer_layout, dp_distribution
+from .ddp_layout import build_buffer_layout, dp_distribution
 from .resharding_pp import PipelineParallelReshardingInfo
 from .util import Range
 

@@ -17,7 +17,7 @@ holder; holders in arena order.
 from __future__ import annotations
 
 import bisect
-from typing import Dict, List, Sequence, Tuple
+from typing import Dict, List, Tuple
 
 import numpy as np
 
@@ -189,7 +189,3 @@ def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
         r["len"] = c1 - c0
         out[i] = r
     return out
-
-
-def tensor_sizes(bufs: TensorBuffers) -> Sequence[int]:
-    return bufs.nbytes()

@@ -15,7 +15,7 @@ padded size, and rows past it are zero in every tensor.
 import numpy as np
 
 from . import synth
-from .plan import dp_distributions, local_shape, stage, ep_rank, global_rank, tp_size, Strat
+from .plan import dp_distributions, ep_rank, global_rank, local_shape, stage, tp_size
 
 
 def full_index(p, T, t, local_idx):

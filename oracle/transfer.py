@@ -20,7 +20,7 @@ import torch
 
 from .canonical import piece_values, shard_key
 from .model import numel
-from .plan import ParamPlan, Strat, dp_distributions, ep_rank, global_rank, local_shape, stage, tp_size
+from .plan import ParamPlan, dp_distributions, ep_rank, global_rank, local_shape, stage, tp_size
 
 KINDS = ("main", "exp_avg", "exp_avg_sq")
 

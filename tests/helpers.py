@@ -1,12 +1,10 @@
 """Shared test utilities: small model shapes, numpy executors and comparisons."""
 
-from dataclasses import replace
-
 import numpy as np
 
 from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
 from elasticmegatron_amd.resharding import model_spec as ms
-from elasticmegatron_amd.resharding.layout import ARENA_PARAM, PIECE_DTYPE
+from elasticmegatron_amd.resharding.layout import ARENA_PARAM
 from oracle import synth
 from oracle.plan import Strat
 

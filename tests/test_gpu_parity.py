@@ -6,8 +6,6 @@ tables: against the numpy reference semantics of emrs_plan_execute, covering
 the vector, scalar, strided and split-alignment paths.
 """
 
-import ctypes
-
 import numpy as np
 import pytest
 import torch

@@ -7,7 +7,6 @@ side) or a device table (more); either way the result must equal the arena
 path's, checked element by element against the seeded generator.
 """
 
-import numpy as np
 import pytest
 import torch
 

@@ -6,7 +6,6 @@ destination piece from its full-tensor indices.  Both must agree with each
 other and with the product's lowering, bit for bit.
 """
 
-import numpy as np
 import pytest
 
 from elasticmegatron_amd.resharding.lowering import lower_transfer

@@ -11,7 +11,6 @@ import pytest
 
 from elasticmegatron_amd import _native
 from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
-from elasticmegatron_amd.resharding.layout import ARENA_PARAM
 from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lower_transfer
 from elasticmegatron_amd.resharding.tensors import TensorBuffers, rebase_on_tensors
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
