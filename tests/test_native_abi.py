@@ -7,6 +7,7 @@ import re
 
 import numpy as np
 import pytest
+import torch
 
 from elasticmegatron_amd import _native
 from elasticmegatron_amd.resharding.layout import PIECE_DTYPE, SEGMENT_DTYPE
@@ -149,3 +150,50 @@ def test_empty_plan_and_no_device_errors():
         with pytest.raises(_native.EmrsError) as e:
             t.execute([0x10000], [0x20000], 0)
         assert e.value.code == -6
+
+
+def _two_seg_plan(n_bufs=2):
+    t = np.zeros(2, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 0, 0, 16, 1, 0, 0, 0, 0, 0, 0)
+    t[1] = (n_bufs - 1, n_bufs - 1, 4, 0, 0, 0, 16, 1, 0, 0, 0, 0, 0, 0)
+    return _native.Plan(t, [1024] * n_bufs, [1024] * n_bufs)
+
+
+@pytest.mark.parametrize("n_bufs", [2, 300])   # kernel-argument path and device-table path
+def test_alias_checks_before_any_device_work(n_bufs):
+    """Host-side buffer checks of emrs_plan_execute: out of place, destinations disjoint."""
+    plan = _two_seg_plan(n_bufs)
+    base = 1 << 40
+    src = [base + i * 4096 for i in range(n_bufs)]
+    dst = [base + (1 << 30) + i * 4096 for i in range(n_bufs)]
+    # Two referenced destinations overlapping.
+    bad = list(dst)
+    bad[n_bufs - 1] = dst[0] + 512
+    with pytest.raises(_native.EmrsError) as e:
+        plan.execute(src, bad, 0)
+    assert e.value.code == -8
+    # A referenced source overlapping a referenced destination.
+    bad = list(src)
+    bad[0] = dst[n_bufs - 1] + 16
+    with pytest.raises(_native.EmrsError) as e:
+        plan.execute(bad, dst, 0)
+    assert e.value.code == -8
+    # Sources may overlap each other, unreferenced buffers may alias anything or be NULL;
+    # the call then gets as far as looking for a device.
+    ok_src = list(src)
+    ok_src[n_bufs - 1] = src[0] + 16
+    ok_dst = list(dst)
+    if n_bufs > 2:
+        ok_dst[1] = dst[0]
+        ok_src[1] = 0
+    if torch.cuda.is_available():
+        return
+    with pytest.raises(_native.EmrsError) as e:
+        plan.execute(ok_src, ok_dst, 0)
+    assert e.value.code == -6
+    # Misaligned referenced base.
+    bad = list(src)
+    bad[0] += 8
+    with pytest.raises(_native.EmrsError) as e:
+        plan.execute(bad, dst, 0)
+    assert e.value.code == -3
