@@ -235,7 +235,9 @@ def main():
     if os.path.exists(tf):
         with open(tf) as f:
             rec = json.load(f)
-        if rec.get("bf16_source", "cast") == (tm.bf16_source if backup is None else None) or backup is not None:
+        same_source = rec.get("bf16_source", "cast") == (tm.bf16_source if backup is None else None) or backup is not None
+        # Counters measured on another plan (a different lowering of this workload) do not apply.
+        if same_source and rec.get("algorithmic_bytes_per_launch") == plan.traffic_bytes:
             traffic = rec.get("hbm_bytes_per_launch")
 
     out = {

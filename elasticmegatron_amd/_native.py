@@ -102,7 +102,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
     lib.emrs_plan_compare.restype = I
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
-    if lib.emrs_abi_version() != 2:
+    if lib.emrs_abi_version() != 3:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib

@@ -90,26 +90,28 @@ struct DevSeg {
   uint16_t src_buf;
   uint16_t dst_buf;
   uint16_t aux_buf;
-  uint8_t sh2;
-  uint8_t bits;          // bit 0: sh1; bits 1-3: unit_log2; bits 4-5: cast; bits 6-7: elem_log2
+  uint8_t sh;            // bits 0-4: sh2; bit 5: sh1
+  uint8_t bits;          // bits 0-2: unit_log2; bits 3-4: elem_log2; bits 5-7: ops
 
-  // cast bit 0: also write bf16 to aux; bit 1: write zeros, read nothing.
-  // elem_log2: element size of the input segment (read only by the compare kernel).
-  __host__ __device__ uint32_t sh1() const { return bits & 1u; }
-  __host__ __device__ uint32_t unit_log2() const { return (bits >> 1) & 7u; }
-  __host__ __device__ uint32_t cast() const { return (bits >> 4) & 3u; }
-  __host__ __device__ uint32_t elem_log2() const { return (bits >> 6) & 3u; }
+  // ops bit 0: also write bf16 to aux; bit 1: write zeros, read nothing;
+  // bit 2: also write the values unchanged to aux.  elem_log2: element size of
+  // the input segment (read by the compare kernel and for duplicates).
+  __host__ __device__ uint32_t sh1() const { return (sh >> 5) & 1u; }
+  __host__ __device__ uint32_t sh2() const { return sh & 31u; }
+  __host__ __device__ uint32_t unit_log2() const { return bits & 7u; }
+  __host__ __device__ uint32_t elem_log2() const { return (bits >> 3) & 3u; }
+  __host__ __device__ uint32_t ops() const { return (bits >> 5) & 7u; }
 };
 static_assert(sizeof(DevSeg) == 64, "DevSeg layout");
 
 // Division by an invariant divisor (Granlund & Montgomery 1994, fig. 4.1).
-void make_magic(uint32_t d, uint32_t *m, uint32_t *sh1, uint8_t *sh2) {
+void make_magic(uint32_t d, uint32_t *m, uint32_t *sh1, uint32_t *sh2) {
   uint32_t l = 0;
   while ((1ull << l) < d) ++l;
   uint64_t num = (uint64_t)(((unsigned __int128)1 << 32) * (((unsigned __int128)1 << l) - d) / d) + 1;
   *m = (uint32_t)num;
   *sh1 = l < 1 ? l : 1;
-  *sh2 = l > 1 ? (uint8_t)(l - 1) : 0;
+  *sh2 = l > 1 ? l - 1 : 0;
 }
 
 __host__ __device__ __forceinline__ uint32_t umulhi32(uint32_t a, uint32_t b) {
@@ -174,7 +176,7 @@ struct CastOf<uint32_t> {
 // kCast also store each unit's bf16 image to aux.  In a partial chunk, lanes
 // past the end load the last unit again (in bounds) so that every load is
 // unconditional; only their stores are masked off.
-template <typename T, bool kNT, bool kCast, bool kZero = false>
+template <typename T, bool kNT, bool kCast, bool kZero = false, bool kDup = false>
 __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, char *dbase, char *abase,
                                            uint32_t u0, uint32_t u_end) {
   typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
@@ -182,6 +184,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
   const T *src = reinterpret_cast<const T *>(sbase);
   T *dst = reinterpret_cast<T *>(dbase);
   A *aux = reinterpret_cast<A *>(abase);
+  T *dup = reinterpret_cast<T *>(abase);  // kDup: the second destination, same unit type
   const uint32_t tid = threadIdx.x;
   const uint32_t n = u_end - u0;
   T v[kUnroll];
@@ -189,6 +192,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
     const T *sp = src + s.src_off + u0;
     T *dp = dst + s.dst_off + u0;
     A *ap = aux + s.aux_off + u0;
+    T *pp = dup + s.aux_off + u0;
     if constexpr (kZero) {
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j) v[j] = T{};
@@ -201,6 +205,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
       for (int j = 0; j < kUnroll; ++j) {
         st<T, kNT>(dp + j * kThreads + tid, v[j]);
         if constexpr (kCast) st<A, kNT>(ap + j * kThreads + tid, C::cast(v[j]));
+        if constexpr (kDup) st<T, kNT>(pp + j * kThreads + tid, v[j]);
       }
     } else {
 #pragma unroll
@@ -211,6 +216,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
         if (j * kThreads + tid < n) {
           st<T, kNT>(dp + j * kThreads + tid, v[j]);
           if constexpr (kCast) st<A, kNT>(ap + j * kThreads + tid, C::cast(v[j]));
+          if constexpr (kDup) st<T, kNT>(pp + j * kThreads + tid, v[j]);
         }
     }
     return;
@@ -219,7 +225,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
 #pragma unroll
   for (int j = 0; j < kUnroll; ++j) {
     const uint32_t u = u0 + min(j * kThreads + tid, n - 1);
-    row[j] = magic_div(u, s.magic, s.sh1(), s.sh2);
+    row[j] = magic_div(u, s.magic, s.sh1(), s.sh2());
     col[j] = u - row[j] * s.len;
     if constexpr (kZero) v[j] = T{};
     else v[j] = ld<T, kNT>(src + s.src_off + (uint64_t)row[j] * s.src_stride + col[j]);
@@ -230,7 +236,21 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
       st<T, kNT>(dst + s.dst_off + (uint64_t)row[j] * s.dst_stride + col[j], v[j]);
       if constexpr (kCast)
         st<A, kNT>(aux + s.aux_off + (uint64_t)row[j] * s.aux_stride + col[j], C::cast(v[j]));
+      if constexpr (kDup) st<T, kNT>(dup + s.aux_off + (uint64_t)row[j] * s.aux_stride + col[j], v[j]);
     }
+}
+
+// copy_chunk for the unit width of a segment that carries no bf16 image.
+template <bool kNT, bool kCast, bool kZero, bool kDup>
+__device__ __forceinline__ void dispatch_units(uint32_t ul, const DevSeg &s, const char *sb, char *db, char *ab,
+                                               uint32_t u0, uint32_t u_end) {
+  switch (ul) {
+    case 4: copy_chunk<u32x4, kNT, kCast, kZero, kDup>(s, sb, db, ab, u0, u_end); break;
+    case 3: copy_chunk<uint64_t, kNT, kCast, kZero, kDup>(s, sb, db, ab, u0, u_end); break;
+    case 2: copy_chunk<uint32_t, kNT, kCast, kZero, kDup>(s, sb, db, ab, u0, u_end); break;
+    case 1: copy_chunk<uint16_t, kNT, kCast, kZero, kDup>(s, sb, db, ab, u0, u_end); break;
+    default: copy_chunk<uint8_t, kNT, kCast, kZero, kDup>(s, sb, db, ab, u0, u_end); break;
+  }
 }
 
 // Base address of buffer i: from the kernel-argument table, or (kTable) from
@@ -270,34 +290,27 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
     const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
     char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
     char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
-    const uint32_t cast = s.cast(), ul = s.unit_log2();
-    if (cast & 2) {  // zero fill, with or without the bf16 image
-      if (cast & 1) {
+    const uint32_t ops = s.ops(), ul = s.unit_log2();
+    if (ops & 4) {  // duplicate to aux, with or without zero fill
+      if (ops & 2) dispatch_units<kNT, false, true, true>(ul, s, sb, db, ab, u0, u_end);
+      else dispatch_units<kNT, false, false, true>(ul, s, sb, db, ab, u0, u_end);
+      continue;
+    }
+    if (ops & 2) {  // zero fill, with or without the bf16 image
+      if (ops & 1) {
         if (ul == 4) copy_chunk<u32x4, kNT, true, true>(s, sb, db, ab, u0, u_end);
         else copy_chunk<uint32_t, kNT, true, true>(s, sb, db, ab, u0, u_end);
       } else {
-        switch (ul) {
-          case 4: copy_chunk<u32x4, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
-          case 3: copy_chunk<uint64_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
-          case 2: copy_chunk<uint32_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
-          case 1: copy_chunk<uint16_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
-          default: copy_chunk<uint8_t, kNT, false, true>(s, sb, db, ab, u0, u_end); break;
-        }
+        dispatch_units<kNT, false, true, false>(ul, s, sb, db, ab, u0, u_end);
       }
       continue;
     }
-    if (cast) {
+    if (ops & 1) {
       if (ul == 4) copy_chunk<u32x4, kNT, true>(s, sb, db, ab, u0, u_end);
       else copy_chunk<uint32_t, kNT, true>(s, sb, db, ab, u0, u_end);
       continue;
     }
-    switch (ul) {
-      case 4: copy_chunk<u32x4, kNT, false>(s, sb, db, ab, u0, u_end); break;
-      case 3: copy_chunk<uint64_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
-      case 2: copy_chunk<uint32_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
-      case 1: copy_chunk<uint16_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
-      default: copy_chunk<uint8_t, kNT, false>(s, sb, db, ab, u0, u_end); break;
-    }
+    dispatch_units<kNT, false, false, false>(ul, s, sb, db, ab, u0, u_end);
   }
 }
 
@@ -401,10 +414,13 @@ struct emrs_plan {
 
 namespace {
 
-// Optional bf16 image of a segment: buffer, offset and row stride in units
-// of half the segment's unit.
+// Second destination of a segment: its bf16 image (cast; offsets in units
+// of half the segment's unit) or a duplicate (dup; offsets in the segment's
+// own units): buffer, offset and row stride.
 struct Aux {
-  bool on = false;
+  bool on = false;    // cast or dup
+  bool cast = false;  // EMRS_SEG_CAST_BF16
+  bool dup = false;   // EMRS_SEG_DUP
   bool zero = false;  // the segment writes zeros (EMRS_SEG_ZERO_FILL)
   uint32_t buf = 0;
   uint64_t off = 0, stride = 0;
@@ -462,10 +478,11 @@ struct Builder {
     d.rows = rows;
     d.src_stride = rows > 1 ? ss : 0;
     d.dst_stride = rows > 1 ? ds : 0;
-    uint32_t sh1 = 0;
-    make_magic(len, &d.magic, &sh1, &d.sh2);
-    const uint32_t cast = (ax.on ? 1u : 0u) | (ax.zero ? 2u : 0u);
-    d.bits = (uint8_t)(sh1 | (ul << 1) | (cast << 4) | ((uint32_t)cur_elem_log2 << 6));
+    uint32_t sh1 = 0, sh2 = 0;
+    make_magic(len, &d.magic, &sh1, &sh2);
+    d.sh = (uint8_t)(sh2 | (sh1 << 5));
+    const uint32_t ops = (ax.cast ? 1u : 0u) | (ax.zero ? 2u : 0u) | (ax.dup ? 4u : 0u);
+    d.bits = (uint8_t)(ul | ((uint32_t)cur_elem_log2 << 3) | (ops << 5));
     d.src_buf = (uint16_t)sbuf;
     d.dst_buf = (uint16_t)dbuf;
     d.aux_buf = (uint16_t)(ax.on ? ax.buf : dbuf);
@@ -500,7 +517,7 @@ int check_disjoint(const emrs_segment *segs, uint64_t n_segs) {
   };
   uint64_t total_rows = 0;
   for (uint64_t i = 0; i < n_segs; ++i)
-    if (segs[i].len) total_rows += segs[i].rows * ((segs[i].flags & EMRS_SEG_CAST_BF16) ? 2 : 1);
+    if (segs[i].len) total_rows += segs[i].rows * ((segs[i].flags & (EMRS_SEG_CAST_BF16 | EMRS_SEG_DUP)) ? 2 : 1);
   if (total_rows > (1ull << 27))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "disjointness check: too many rows to check");
   std::vector<Iv> iv;
@@ -511,9 +528,10 @@ int check_disjoint(const emrs_segment *segs, uint64_t n_segs) {
     for (uint64_t r = 0; r < s.rows; ++r) {
       const uint64_t b = (s.dst_off + r * s.dst_stride) * s.elem_bytes;
       iv.push_back({s.dst_buf, b, b + s.len * s.elem_bytes});
-      if (s.flags & EMRS_SEG_CAST_BF16) {
-        const uint64_t a = (s.aux_off + r * s.aux_stride) * 2;
-        iv.push_back({s.aux_buf, a, a + s.len * 2});
+      if (s.flags & (EMRS_SEG_CAST_BF16 | EMRS_SEG_DUP)) {
+        const uint64_t w = (s.flags & EMRS_SEG_CAST_BF16) ? 2 : s.elem_bytes;
+        const uint64_t a = (s.aux_off + r * s.aux_stride) * w;
+        iv.push_back({s.aux_buf, a, a + s.len * w});
       }
     }
   }
@@ -709,7 +727,8 @@ __device__ __forceinline__ void aux_words_of(const A &v, uint32_t *w) {
   }
 }
 
-// Compare units [u0, u_end) of segment s; with a cast, also its bf16 image.
+// Compare units [u0, u_end) of segment s; with a cast, also its bf16 image;
+// with a duplicate, also the second copy.
 template <typename T>
 __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase, const char *dbase,
                                               const char *abase, uint32_t u0, uint32_t u_end, LaneAcc &m,
@@ -724,19 +743,25 @@ __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase
     if (u >= u_end) break;
     uint64_t so = s.src_off + u, dof = s.dst_off + u, ao = s.aux_off + u;
     if (s.rows > 1) {
-      const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2), col = u - row * s.len;
+      const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2()), col = u - row * s.len;
       so = s.src_off + (uint64_t)row * s.src_stride + col;
       dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
       ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
     }
-    const T e = (s.cast() & 2) ? T{} : src[so];
+    const uint32_t ops = s.ops();
+    const T e = (ops & 2) ? T{} : src[so];
     const T g = dst[dof];
     uint32_t ew[4] = {0, 0, 0, 0}, gw[4] = {0, 0, 0, 0};
     words_of(e, ew);
     words_of(g, gw);
     cmp_words(m, ew, gw, (uint32_t)sizeof(T), s.elem_log2());
+    if (ops & 4) {
+      uint32_t dw[4] = {0, 0, 0, 0};
+      words_of(reinterpret_cast<const T *>(abase)[ao], dw);
+      cmp_words(x, ew, dw, (uint32_t)sizeof(T), s.elem_log2());
+    }
     if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
-      if (s.cast() & 1) {
+      if (ops & 1) {
         uint32_t ea[2] = {0, 0}, ga[2] = {0, 0};
         aux_words_of(C::cast(e), ea);
         aux_words_of(aux[ao], ga);
@@ -822,7 +847,7 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     }
     block_reduce(m, lds_d, lds_u, lds_f);
     if (threadIdx.x == 0) flush(m, acc + groups[lo]);
-    if (s.cast() & 1) {  // uniform across the workgroup
+    if (s.ops() & 5) {  // cast or duplicate; uniform across the workgroup
       block_reduce(x, lds_d, lds_u, lds_f);
       if (threadIdx.x == 0) flush(x, acc + aux_groups[lo]);
     }
@@ -873,28 +898,34 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     const int lg = log2_of(s.elem_bytes);
     const bool cast = (s.flags & EMRS_SEG_CAST_BF16) != 0;
     const bool zero = (s.flags & EMRS_SEG_ZERO_FILL) != 0;
+    const bool dup = (s.flags & EMRS_SEG_DUP) != 0;
+    const bool has_aux = cast || dup;
     if (lg < 0) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "elem_bytes must be 1, 2, 4 or 8");
-    if ((s.flags & ~(EMRS_SEG_CAST_BF16 | EMRS_SEG_ZERO_FILL)) || s.reserved)
+    if ((s.flags & ~(EMRS_SEG_CAST_BF16 | EMRS_SEG_ZERO_FILL | EMRS_SEG_DUP)) || s.reserved)
       return fail(EMRS_ERR_INVALID_ARGUMENT, at + "unknown flags");
+    if (cast && dup) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a segment carries a bf16 image or a duplicate, not both");
     if (cast && s.elem_bytes != 4) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a bf16 cast needs fp32 elements");
-    if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs || (cast && s.aux_buf >= n_dst_bufs))
+    if (s.src_buf >= n_src_bufs || s.dst_buf >= n_dst_bufs || (has_aux && s.aux_buf >= n_dst_bufs))
       return fail(EMRS_ERR_INVALID_ARGUMENT, at + "buffer id out of range");
     if (s.rows == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, at + "rows must be >= 1");
     if (s.len == 0) continue;
-    if (s.rows > 1 && (s.dst_stride < s.len || (cast && s.aux_stride < s.len)))
+    if (s.rows > 1 && (s.dst_stride < s.len || (has_aux && s.aux_stride < s.len)))
       return fail(EMRS_ERR_INVALID_ARGUMENT, at + "a destination stride < len makes rows overlap");
     if (!zero && extent_end(s.src_off, s.len, s.rows, s.rows > 1 ? s.src_stride : 0, s.elem_bytes) >
                      src_buf_bytes[s.src_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "source range exceeds its buffer");
     if (extent_end(s.dst_off, s.len, s.rows, s.rows > 1 ? s.dst_stride : 0, s.elem_bytes) > dst_buf_bytes[s.dst_buf])
       return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "destination range exceeds its buffer");
-    if (cast && extent_end(s.aux_off, s.len, s.rows, s.rows > 1 ? s.aux_stride : 0, 2) > dst_buf_bytes[s.aux_buf])
-      return fail(EMRS_ERR_OUT_OF_BOUNDS, at + "bf16 range exceeds its buffer");
+    // Bytes per aux element: a bf16 image, or a duplicate of the element.
+    const uint64_t aeb = cast ? 2 : (dup ? s.elem_bytes : 0);
+    if (has_aux && extent_end(s.aux_off, s.len, s.rows, s.rows > 1 ? s.aux_stride : 0, (uint32_t)aeb) >
+                       dst_buf_bytes[s.aux_buf])
+      return fail(EMRS_ERR_OUT_OF_BOUNDS, at + (cast ? "bf16 range exceeds its buffer" : "duplicate range exceeds its buffer"));
     if (!zero) read += s.len * s.rows * s.elem_bytes;
-    payload += s.len * s.rows * (s.elem_bytes + (cast ? 2 : 0));
+    payload += s.len * s.rows * (s.elem_bytes + aeb);
     if (!zero) src_used[s.src_buf] = 1;
     dst_used[s.dst_buf] = 1;
-    if (cast) dst_used[s.aux_buf] = 1;
+    if (has_aux) dst_used[s.aux_buf] = 1;
 
     const uint64_t eb = s.elem_bytes;
     bld.cur_origin = (uint32_t)i;
@@ -902,36 +933,41 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
     // A zero fill has no source: align its phantom source with the destination.
     const uint64_t so = zero ? s.dst_off * eb : s.src_off * eb, dof = s.dst_off * eb, lb = s.len * eb;
     const uint64_t ds = s.rows > 1 ? s.dst_stride * eb : 0, ss = zero ? ds : (s.rows > 1 ? s.src_stride * eb : 0);
-    const uint64_t ao = cast ? s.aux_off * 2 : 0, as = cast && s.rows > 1 ? s.aux_stride * 2 : 0;
+    const uint64_t ao = s.aux_off * aeb, as = s.rows > 1 ? s.aux_stride * aeb : 0;
     Aux ax;
-    ax.on = cast;
+    ax.on = has_aux;
+    ax.cast = cast;
+    ax.dup = dup;
     ax.zero = zero;
     ax.buf = s.aux_buf;
-    // The bf16 image of a 16-byte unit is 8 bytes: the vector path needs it 8-byte aligned.
-    const bool aux_vec_ok = !cast || (ao % 8 == 0 && as % 8 == 0);
-    const bool rows1 = s.rows == 1 || (ss == lb && ds == lb && (!cast || as == s.len * 2));
+    // Aux bytes per 16-byte unit: 8 for a bf16 image of fp32, 16 for a duplicate.
+    const uint64_t avu = has_aux ? 16 * aeb / eb : 16;
+    const bool aux_vec_ok = !has_aux || (ao % avu == 0 && as % avu == 0);
+    const bool rows1 = s.rows == 1 || (ss == lb && ds == lb && (!has_aux || as == s.len * aeb));
     if (rows1) {
       const uint64_t L = lb * s.rows;  // contiguous bytes
       if (so % 16 == 0 && dof % 16 == 0 && L % 16 == 0 && aux_vec_ok) {
-        ax.off = ao / 8;
+        ax.off = ao / avu;
         bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, L / 16, 1, 0, 0, ax);
-      } else if (so % 16 == dof % 16 && (!cast || (ao % 8) * 2 == so % 16)) {
+      } else if (so % 16 == dof % 16 && (!has_aux || (ao % avu) * eb / aeb == so % 16)) {
+        // Source, destination and aux reach a 16-byte boundary at the same element.
         const uint64_t head = std::min<uint64_t>((16 - so % 16) % 16, L);
         const uint64_t body = (L - head) / 16 * 16;
         const uint64_t tail = L - head - body;
-        ax.off = ao / 2;
+        const uint64_t aux_head = head * aeb / eb, aux_body = body * aeb / eb;
+        ax.off = has_aux ? ao / aeb : 0;
         bld.emit(s.src_buf, s.dst_buf, lg, so / eb, dof / eb, head / eb, 1, 0, 0, ax);
-        ax.off = (ao + head / 2) / 8;
+        ax.off = has_aux ? (ao + aux_head) / avu : 0;
         bld.emit(s.src_buf, s.dst_buf, 4, (so + head) / 16, (dof + head) / 16, body / 16, 1, 0, 0, ax);
-        ax.off = (ao + (head + body) / 2) / 2;
+        ax.off = has_aux ? (ao + aux_head + aux_body) / aeb : 0;
         bld.emit(s.src_buf, s.dst_buf, lg, (so + head + body) / eb, (dof + head + body) / eb, tail / eb, 1, 0, 0, ax);
       } else {
         ax.off = s.aux_off;
         bld.emit(s.src_buf, s.dst_buf, lg, so / eb, s.dst_off, L / eb, 1, 0, 0, ax);
       }
     } else if (so % 16 == 0 && dof % 16 == 0 && lb % 16 == 0 && ss % 16 == 0 && ds % 16 == 0 && aux_vec_ok) {
-      ax.off = ao / 8;
-      ax.stride = as / 8;
+      ax.off = ao / avu;
+      ax.stride = as / avu;
       bld.emit(s.src_buf, s.dst_buf, 4, so / 16, dof / 16, lb / 16, s.rows, ss / 16, ds / 16, ax);
     } else {
       ax.off = s.aux_off;
@@ -1055,7 +1091,8 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
     g_host[nd + k] = ga;
     const uint64_t units = (uint64_t)d.len * d.rows;
     elements[g] += units << (d.unit_log2() - d.elem_log2());
-    if (d.cast() & 1) elements[ga] += units << (d.unit_log2() - 2);
+    if (d.ops() & 1) elements[ga] += units << (d.unit_log2() - 2);
+    if (d.ops() & 4) elements[ga] += units << (d.unit_log2() - d.elem_log2());
   }
   for (uint32_t g = 0; g < n_groups; ++g) {
     stats[g] = emrs_compare_stats{};

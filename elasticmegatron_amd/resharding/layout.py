@@ -50,6 +50,7 @@ SEGMENT_DTYPE = np.dtype([
 ])
 SEG_CAST_BF16 = 1
 SEG_ZERO_FILL = 2
+SEG_DUP = 4
 PIECE_DTYPE = np.dtype([
     ("buf", "<u4"), ("param_id", "<u4"), ("kind", "<u4"), ("reserved", "<u4"),
     ("buf_off", "<u8"), ("len", "<u8"), ("local_start", "<u8"), ("local_cols", "<u8"),

@@ -34,11 +34,11 @@ training_state.py:40-60).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterable, List, Optional, Sequence, Tuple
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from .layout import (ARENA_PARAM, SEG_CAST_BF16, SEG_ZERO_FILL, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout,
+from .layout import (ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout,
                      view2d)
 
 
@@ -112,10 +112,13 @@ class SegmentBuilder:
         self.groups: List[int] = []  # parameter of each row; rows of different parameters never merge
 
     def add(self, sbuf: int, dbuf: int, eb: int, so: int, do: int, n: int, rows: int, ss: int, ds: int,
-            aux: Optional[Tuple[int, int, int]] = None, zero: bool = False, group: int = 0) -> None:
+            aux: Optional[Tuple[int, int, int]] = None, zero: bool = False, group: int = 0,
+            dup: bool = False) -> None:
+        """``aux`` = (buffer, offset, row stride) of a second destination: the bf16
+        image of the values, or with ``dup`` an unchanged copy."""
         if n <= 0 or rows <= 0:
             return
-        flags, abuf, aoff, astr = (SEG_CAST_BF16, aux[0], aux[1], aux[2]) if aux else (0, 0, 0, 0)
+        flags, abuf, aoff, astr = ((SEG_DUP if dup else SEG_CAST_BF16), aux[0], aux[1], aux[2]) if aux else (0, 0, 0, 0)
         if zero:
             flags |= SEG_ZERO_FILL
             so, ss = 0, 0
@@ -272,6 +275,11 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
 def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False):
     """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
 
+    On a scale-up every new instance of a shard is filled from instance 0's
+    copy (transfer.py:343-388).  The destinations of one source shard are
+    taken in pairs, each pair as one duplicating segment: the shard is read
+    once per two copies written.
+
     ``with_groups``: as for :func:`lower_transfer`.
     """
     space = src.space
@@ -281,13 +289,22 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     for vp in space.all_virtual_params:
         if not (src.has_param(vp) and dst.has_param(vp)):
             continue
+        g = vp.global_index if with_groups else 0
         src_by = {(h.instance, h.tp_rank, h.lo): h for h in src.fp32_holders(vp)}
+        # Destinations per source shard, in destination order.
+        fills: Dict[int, Tuple[Holder, List[Holder]]] = {}
         for h in dst.fp32_holders(vp):
             inst = 0 if scale_up else h.instance
             s = src_by.get((inst, h.tp_rank, h.lo))
             if s is None or s.hi != h.hi:
                 raise AssertionError(f"{vp.name}: no matching source shard for a Group-ZeRO copy")
-            b.add(0, 0, 4, s.offset, h.offset, h.hi - h.lo, 1, 0, 0, group=vp.global_index if with_groups else 0)
+            fills.setdefault(id(s), (s, []))[1].append(h)
+        for s, hs in fills.values():
+            n = s.hi - s.lo
+            for i in range(0, len(hs) - 1, 2):
+                b.add(0, 0, 4, s.offset, hs[i].offset, n, 1, 0, 0, aux=(0, hs[i + 1].offset, 0), group=g, dup=True)
+            if len(hs) % 2:
+                b.add(0, 0, 4, s.offset, hs[-1].offset, n, 1, 0, 0, group=g)
     return _assemble(b.table(), np.zeros(0, dtype=SEGMENT_DTYPE), b.group_array(), np.zeros(0, dtype=np.int64),
                      with_groups)
 
@@ -309,13 +326,13 @@ def _split(table: np.ndarray, max_elems: int, groups: np.ndarray):
             out_g.append(g)
             continue
         reads = not s["flags"] & SEG_ZERO_FILL
-        cast = bool(s["flags"] & SEG_CAST_BF16)
+        aux = bool(s["flags"] & (SEG_CAST_BF16 | SEG_DUP))
         if rows == 1:
             for o in range(0, n, max_elems):
                 p = s.copy()
                 p["src_off"] += o if reads else 0
                 p["dst_off"] += o
-                p["aux_off"] += o if cast else 0
+                p["aux_off"] += o if aux else 0
                 p["len"] = min(max_elems, n - o)
                 out.append(p)
                 out_g.append(g)
@@ -336,6 +353,8 @@ def _split(table: np.ndarray, max_elems: int, groups: np.ndarray):
 def _assemble(fp32: np.ndarray, bf16: np.ndarray, g32: np.ndarray, gbf: np.ndarray, with_groups: bool):
     """Replicate the fp32 segments over the three optimizer kinds; only main carries the bf16 cast.
 
+    A duplicating segment duplicates within its own kind's arena.
+
     The kinds are interleaved in pieces of about 1 MiB: the kernel hands
     every workgroup an equal run of chunks, and a main chunk that also writes
     the bf16 cast costs more than the others, so every run must hold the same
@@ -350,15 +369,19 @@ def _assemble(fp32: np.ndarray, bf16: np.ndarray, g32: np.ndarray, gbf: np.ndarr
         t["src_buf"] = k
         t["dst_buf"] = k
         groups[k::3] = 4 * gbase + 1 + k
+        dup = (base["flags"] & SEG_DUP) != 0
+        t["aux_buf"] = np.where(dup, k, t["aux_buf"])
         if k:
             t["flags"] &= ~np.uint32(SEG_CAST_BF16)
             for f in ("aux_buf", "aux_off", "aux_stride"):
-                t[f] = 0
+                t[f] = np.where(dup, t[f], 0)
     table = np.concatenate([out, bf16])
     if not with_groups:
         return table
     groups = np.concatenate([groups, 4 * gbf])
-    aux_groups = np.concatenate([4 * np.repeat(gbase, 3), 4 * gbf])
+    # The bf16 image counts to the parameter's bf16 group, a duplicate to its own kind.
+    dup3 = (out["flags"] & SEG_DUP) != 0
+    aux_groups = np.concatenate([np.where(dup3, groups[:len(out)], 4 * np.repeat(gbase, 3)), 4 * gbf])
     return table, groups.astype(np.uint32), aux_groups.astype(np.uint32)
 
 
@@ -367,9 +390,11 @@ def _units(table: np.ndarray) -> np.ndarray:
 
 
 def payload_bytes(table: np.ndarray) -> int:
-    """Bytes written per execution (bf16 casts included)."""
-    cast = (table["flags"] & SEG_CAST_BF16) != 0
-    return int(np.sum(_units(table) * (table["elem_bytes"].astype(np.uint64) + 2 * cast.astype(np.uint64))))
+    """Bytes written per execution (bf16 images and duplicates included)."""
+    eb = table["elem_bytes"].astype(np.uint64)
+    cast = ((table["flags"] & SEG_CAST_BF16) != 0).astype(np.uint64)
+    dup = ((table["flags"] & SEG_DUP) != 0).astype(np.uint64)
+    return int(np.sum(_units(table) * (eb + 2 * cast + eb * dup)))
 
 
 def read_bytes(table: np.ndarray) -> int:

@@ -21,7 +21,7 @@ from typing import Dict, List, Tuple
 
 import numpy as np
 
-from .layout import ARENA_NAMES, ARENA_PARAM, SEG_CAST_BF16, SEG_ZERO_FILL, SEGMENT_DTYPE, StrategyLayout
+from .layout import ARENA_NAMES, ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, SEGMENT_DTYPE, StrategyLayout
 
 FP32_KINDS = ("main", "exp_avg", "exp_avg_sq")
 
@@ -128,9 +128,9 @@ def rebase_on_tensors(table: np.ndarray, src: TensorBuffers, dst: TensorBuffers)
 
     A one-row segment that runs across tensor boundaries (tensors of one
     parameter on consecutive ranks can be adjacent in an arena) is cut at
-    every boundary on the source, destination and bf16-image sides; a
-    strided segment always lies inside one tensor on each side.  Segments
-    that need no cut are mapped in bulk.
+    every boundary on the source, destination and second-destination (bf16
+    image or duplicate) sides; a strided segment always lies inside one
+    tensor on each side.  Segments that need no cut are mapped in bulk.
     """
     table = table[(table["len"] > 0)]
     n = len(table)
@@ -139,21 +139,22 @@ def rebase_on_tensors(table: np.ndarray, src: TensorBuffers, dst: TensorBuffers)
     ln = table["len"].astype(np.int64)
     rows = table["rows"].astype(np.int64)
     zero = (table["flags"] & SEG_ZERO_FILL) != 0
-    cast = (table["flags"] & SEG_CAST_BF16) != 0
+    aux = (table["flags"] & (SEG_CAST_BF16 | SEG_DUP)) != 0
     ext_s = np.where(rows > 1, (rows - 1) * table["src_stride"].astype(np.int64), 0) + ln
     ext_d = np.where(rows > 1, (rows - 1) * table["dst_stride"].astype(np.int64), 0) + ln
     ext_a = np.where(rows > 1, (rows - 1) * table["aux_stride"].astype(np.int64), 0) + ln
     sb, so, s_ok = src.locate_many(table["src_buf"], table["src_off"], ext_s)
     db, do, d_ok = dst.locate_many(table["dst_buf"], table["dst_off"], ext_d)
-    ab, ao, a_ok = dst.locate_many(np.full(n, ARENA_PARAM), table["aux_off"], ext_a)
-    fits = (zero | s_ok) & d_ok & (~cast | a_ok)
+    # The second destination's arena: the param arena for a bf16 image, the segment's own for a duplicate.
+    ab, ao, a_ok = dst.locate_many(np.where(aux, table["aux_buf"], ARENA_PARAM), table["aux_off"], ext_a)
+    fits = (zero | s_ok) & d_ok & (~aux | a_ok)
     out = table[fits].copy()
     f = np.flatnonzero(fits)
     out["src_buf"] = np.where(zero[f], 0, sb[f])
     out["src_off"] = np.where(zero[f], 0, so[f])
     out["dst_buf"], out["dst_off"] = db[f], do[f]
-    out["aux_buf"] = np.where(cast[f], ab[f], out["aux_buf"])
-    out["aux_off"] = np.where(cast[f], ao[f], out["aux_off"])
+    out["aux_buf"] = np.where(aux[f], ab[f], out["aux_buf"])
+    out["aux_off"] = np.where(aux[f], ao[f], out["aux_off"])
     rest = [_cut(s, src, dst) for s in table[~fits]]
     if rest:
         out = np.concatenate([out] + rest)
@@ -166,15 +167,15 @@ def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
     if rows > 1:
         raise AssertionError("a strided segment leaves its tensor")
     zero = bool(int(s["flags"]) & SEG_ZERO_FILL)
-    cast = bool(int(s["flags"]) & SEG_CAST_BF16)
-    sa, da = int(s["src_buf"]), int(s["dst_buf"])
+    aux = bool(int(s["flags"]) & (SEG_CAST_BF16 | SEG_DUP))
+    sa, da, aa = int(s["src_buf"]), int(s["dst_buf"]), int(s["aux_buf"])
     so, do, ao = int(s["src_off"]), int(s["dst_off"]), int(s["aux_off"])
     pts = {0, n}
     if not zero:
         pts.update(b - so for b in src.boundaries(sa, so, so + n))
     pts.update(b - do for b in dst.boundaries(da, do, do + n))
-    if cast:
-        pts.update(b - ao for b in dst.boundaries(ARENA_PARAM, ao, ao + n))
+    if aux:
+        pts.update(b - ao for b in dst.boundaries(aa, ao, ao + n))
     cuts = sorted(pts)
     out = np.zeros(len(cuts) - 1, dtype=SEGMENT_DTYPE)
     for i, (c0, c1) in enumerate(zip(cuts, cuts[1:])):
@@ -184,8 +185,8 @@ def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
         else:
             r["src_buf"], r["src_off"] = src.locate(sa, so + c0)
         r["dst_buf"], r["dst_off"] = dst.locate(da, do + c0)
-        if cast:
-            r["aux_buf"], r["aux_off"] = dst.locate(ARENA_PARAM, ao + c0)
+        if aux:
+            r["aux_buf"], r["aux_off"] = dst.locate(aa, ao + c0)
         r["len"] = c1 - c0
         out[i] = r
     return out

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 2
+#define EMRS_ABI_VERSION 3
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -70,13 +70,14 @@ extern "C" {
 /* emrs_segment flags */
 #define EMRS_SEG_CAST_BF16 1u /* fp32 segment that also writes its values as bf16 to aux */
 #define EMRS_SEG_ZERO_FILL 2u /* write zeros instead of copying: the source is not read */
+#define EMRS_SEG_DUP 4u       /* also write the values, unchanged, to aux (a second destination) */
 
 /* One strided copy.  Units: elements of elem_bytes bytes. */
 typedef struct emrs_segment {
   uint32_t src_buf;    /* index into the src_bases passed at execution */
   uint32_t dst_buf;    /* index into the dst_bases passed at execution */
   uint32_t elem_bytes; /* 1, 2, 4 or 8 */
-  uint32_t flags;      /* 0, EMRS_SEG_CAST_BF16, EMRS_SEG_ZERO_FILL or both */
+  uint32_t flags;      /* EMRS_SEG_* bits; CAST_BF16 and DUP exclude each other */
   uint64_t src_off;    /* first element of row 0 in the source buffer */
   uint64_t dst_off;    /* first element of row 0 in the destination buffer */
   uint64_t len;        /* elements per row */
@@ -88,11 +89,15 @@ typedef struct emrs_segment {
    * torch's float -> bfloat16 conversion), at bf16 element
    * aux_off + r*aux_stride + i of destination buffer aux_buf.  This is
    * Megatron's copy of main params into the bf16 model params
-   * (training_state.py:176-197) fused into the reshard. */
+   * (training_state.py:176-197) fused into the reshard.
+   * EMRS_SEG_DUP: every value is also written unchanged (elem_bytes wide) at
+   * element aux_off + r*aux_stride + i of destination buffer aux_buf: one
+   * read feeding two destinations, as a Group-ZeRO scale-up needs to fill
+   * two optimizer instances from one source shard (transfer.py:343-388). */
   uint32_t aux_buf;
   uint32_t reserved;   /* must be 0 */
   uint64_t aux_off;
-  uint64_t aux_stride; /* bf16 elements between aux row starts (rows > 1), >= len */
+  uint64_t aux_stride; /* aux elements between aux row starts (rows > 1), >= len */
 } emrs_segment;
 
 typedef struct emrs_plan emrs_plan;
@@ -100,10 +105,10 @@ typedef struct emrs_plan emrs_plan;
 typedef struct emrs_plan_stats {
   uint64_t n_segments;      /* segments as given */
   uint64_t n_device_segments; /* after alignment splitting */
-  uint64_t payload_bytes;   /* bytes written per execution, bf16 casts included */
+  uint64_t payload_bytes;   /* bytes written per execution, bf16 images and duplicates included */
   uint64_t read_bytes;      /* bytes read per execution */
-  uint64_t vector_bytes;    /* bytes written through 16-byte units (bf16 images excluded) */
-  uint64_t scalar_bytes;    /* bytes written element by element (bf16 images excluded) */
+  uint64_t vector_bytes;    /* bytes written through 16-byte units (second destinations excluded) */
+  uint64_t scalar_bytes;    /* bytes written element by element (second destinations excluded) */
   uint64_t n_chunks;        /* work chunks per execution */
   uint32_t n_src_bufs;
   uint32_t n_dst_bufs;

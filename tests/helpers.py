@@ -96,6 +96,8 @@ def execute_numpy(table, src, dst):
         if int(s["flags"]) & 1:
             aux = dst[int(s["aux_buf"])]
             _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"]))[...] = bf16_rne_bits(vals)
+        if int(s["flags"]) & 4:  # duplicate
+            _view(dst[int(s["aux_buf"])], int(s["aux_off"]), rows, n, int(s["aux_stride"]))[...] = vals
 
 
 def extract(layout, arenas, params=None):
@@ -220,4 +222,7 @@ def compare_numpy(table, groups, aux_groups, n_groups, src, dst):
             aux = dst[int(s["aux_buf"])].view(np.uint16)
             act_a = _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"])).reshape(-1)
             acc(int(ga), bf16_rne_bits(exp.view(np.uint32)), act_a, 2)
+        if int(s["flags"]) & 4:
+            aux = dst[int(s["aux_buf"])].view(udt[eb])
+            acc(int(ga), exp, _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"])).reshape(-1), eb)
     return out

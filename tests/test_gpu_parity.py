@@ -178,6 +178,7 @@ def _random_table(rng, n_segs, sizes):
             do = do - (do * eb) % 16 // eb + (so * eb) % 16 // eb
             do = max(0, min(do, nb[1] - dst_ext))
         cast = eb == 4 and rng.random() < 0.5
+        dup = not cast and rng.random() < 0.4
         zero = 2 if rng.random() < 0.2 else 0  # zero fill: the source offset is ignored
         if zero and rng.random() < 0.5:
             so = int(rng.integers(0, 1 << 40))
@@ -185,6 +186,14 @@ def _random_table(rng, n_segs, sizes):
             aux_s = ln + int(rng.integers(0, 9)) if r > 1 else 0
             ao = int(rng.integers(0, sizes[1] // 2 - ((r - 1) * aux_s + ln)))
             rows.append((0, 0, eb, 1 | zero, so, do, ln, r, ss, ds, 1, 0, ao, aux_s))
+        elif dup:  # unchanged copy into the second destination buffer
+            aux_s = (ds if rng.random() < 0.5 else ln + int(rng.integers(0, 9))) if r > 1 else 0
+            ext = (r - 1) * aux_s + ln
+            ao = int(rng.integers(0, sizes[1] // eb - ext))
+            if rng.random() < 0.6:  # co-aligned with the destination: vector and head/body/tail paths
+                ao = ao - (ao * eb) % 16 // eb + (do * eb) % 16 // eb
+                ao = max(0, min(ao, sizes[1] // eb - ext))
+            rows.append((0, 0, eb, 4 | zero, so, do, ln, r, ss, ds, 1, 0, ao, aux_s))
         else:
             rows.append((0, 0, eb, zero, so, do, ln, r, ss, ds, 0, 0, 0, 0))
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
@@ -194,7 +203,8 @@ def _random_table(rng, n_segs, sizes):
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_random_segments_match_numpy(gpu_device, seed):
-    """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills.
+    """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills,
+    bf16 images and duplicates.
 
     Segments are applied in order and may overlap in the destination here, so
     each segment runs as its own plan and the numpy model applies the same
@@ -225,6 +235,9 @@ def test_random_segments_match_numpy(gpu_device, seed):
             if int(s["flags"]) & 1:
                 ao = int(s["aux_off"]) + r * int(s["aux_stride"])
                 want_aux.view(np.uint16)[ao:ao + int(s["len"])] = bf16_rne_bits(vals)
+            if int(s["flags"]) & 4:
+                ao = int(s["aux_off"]) + r * int(s["aux_stride"])
+                want_aux.view(b.dtype)[ao:ao + int(s["len"])] = vals
     torch.cuda.synchronize()
     assert np.array_equal(dst.cpu().numpy(), want)
     assert np.array_equal(aux.cpu().numpy(), want_aux)

@@ -76,7 +76,7 @@ def test_compare_kernel_matches_numpy(gpu_device, factory, src, dst, bf16_source
 
 @pytest.mark.parametrize("seed", [0, 1])
 def test_compare_random_tables(gpu_device, seed):
-    """Every element width and path, zero fills and casts, random groups."""
+    """Every element width and path, zero fills, casts and duplicates, random groups."""
     rng = np.random.default_rng(seed)
     nbytes = 1 << 20
     table = _random_table(rng, 120, (nbytes, nbytes))
@@ -87,8 +87,9 @@ def test_compare_random_tables(gpu_device, seed):
         eb = int(s["elem_bytes"])
         spans = [(int(s["dst_off"]) * eb + r * int(s["dst_stride"]) * eb, int(s["len"]) * eb)
                  for r in range(int(s["rows"]))]
-        if int(s["flags"]) & 1:
-            spans += [(nbytes + (int(s["aux_off"]) + r * int(s["aux_stride"])) * 2, int(s["len"]) * 2)
+        if int(s["flags"]) & 5:
+            w = 2 if int(s["flags"]) & 1 else eb
+            spans += [(nbytes + (int(s["aux_off"]) + r * int(s["aux_stride"])) * w, int(s["len"]) * w)
                       for r in range(int(s["rows"]))]
         if any(used[o:o + n].any() for o, n in spans):
             continue

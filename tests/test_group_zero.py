@@ -1,0 +1,71 @@
+"""Group-ZeRO switches: the product's plan, executed on the CPU, against the oracle.
+
+The oracle restates the reference's redundant backup
+(elastic_megatron/transfer/transfer.py:343-388): on a scale-up every new
+optimizer instance receives instance 0's shard; on a scale-down each kept
+instance keeps its own.  The product reads each source shard once per pair
+of destination instances (duplicating segments), so the cases cover even and
+odd instance counts.
+"""
+
+import numpy as np
+import pytest
+
+from elasticmegatron_amd import ParallelStrategy as PS
+from elasticmegatron_amd.resharding.layout import SEG_DUP
+from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, payload_bytes, read_bytes
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from oracle import model
+from oracle import transfer as oracle1
+from tests.helpers import SEED, compare, execute_numpy, extract, new_arenas, piece_fill_numpy, small_llama2, strat
+
+CASES = [
+    ("1to2", PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
+    ("1to3_tp2", PS(4, 2, 1), PS(12, 2, 1, num_distributed_optimizer_instances=3)),
+    ("1to4_pp2", PS(4, 1, 2), PS(16, 1, 2, num_distributed_optimizer_instances=4)),
+]
+
+
+def _run(src, dst, scale_up):
+    spec = small_llama2()
+    inv = model.inventory(spec)
+    S, D = strat(src), strat(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, world, scale_up))
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    table = lower_redundant_backup(ls, ld, scale_up)
+    a, b = new_arenas(ls), new_arenas(ld)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    execute_numpy(table, a, b)
+    got, _ = extract(ld, b)
+    return table, got, want
+
+
+@pytest.mark.parametrize("name,small,big", CASES, ids=[c[0] for c in CASES])
+def test_scale_up_matches_oracle(name, small, big):
+    table, got, want = _run(small, big, True)
+    assert compare(got, {}, want, {}) == []
+    inst = big.num_distributed_optimizer_instances
+    dup = (table["flags"] & SEG_DUP) != 0
+    assert dup.any()
+    # Every shard read once per pair of instances: ceil(inst / 2) reads for inst writes.
+    assert read_bytes(table) * inst == payload_bytes(table) * ((inst + 1) // 2)
+
+
+@pytest.mark.parametrize("name,small,big", CASES, ids=[c[0] for c in CASES])
+def test_scale_down_matches_oracle(name, small, big):
+    table, got, want = _run(big, small, False)
+    assert compare(got, {}, want, {}) == []
+    assert not ((table["flags"] & SEG_DUP) != 0).any()
+    assert read_bytes(table) == payload_bytes(table)
+
+
+def test_duplicates_land_in_their_own_kind():
+    """A duplicating segment writes its second copy into the same optimizer kind's arena."""
+    spec = small_llama2()
+    space = build_virtual_model(spec)
+    table = lower_redundant_backup(space.layout(CASES[0][1]), space.layout(CASES[0][2]), True)
+    dup = table[(table["flags"] & SEG_DUP) != 0]
+    assert np.array_equal(dup["aux_buf"], dup["dst_buf"])
+    assert set(np.unique(dup["dst_buf"]).tolist()) == {0, 1, 2}

@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol():
     assert set(declared) == set(_native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.emrs_abi_version() == 2
+    assert lib.emrs_abi_version() == 3
 
 
 def test_record_layouts_match_header():
@@ -69,7 +69,12 @@ def _seg(**kw):
     (dict(src_off=250, len=16), -2),
     (dict(dst_off=1, len=256), -2),
     (dict(rows=3, len=10, src_stride=200, dst_stride=10), -2),
-    (dict(flags=4), -1),
+    (dict(flags=8), -1),
+    (dict(flags=5, aux_off=64), -1),                      # bf16 image and duplicate together
+    (dict(flags=4, aux_buf=1), -1),
+    (dict(flags=4, aux_off=250, len=16), -2),             # duplicate extent in 4-byte elements
+    (dict(flags=4, elem_bytes=8, aux_off=121, len=8), -2),  # ... and in 8-byte elements
+    (dict(flags=4, rows=2, src_stride=16, dst_stride=16, aux_stride=8), -1),
     (dict(flags=2, src_buf=1), -1),
     (dict(flags=2, dst_off=1000, len=16), -2),
     (dict(reserved=1), -1),
@@ -95,6 +100,18 @@ def test_plan_create_overlap_check():
                                                                                    aux_buf=1, aux_off=4)])
     with pytest.raises(_native.EmrsError) as e:
         _native.Plan(t, [1024], [1024, 1024], check_disjoint=True)
+    assert e.value.code == -4
+    # So do duplicates, over elem_bytes-wide elements: the duplicate's bytes [128, 192) meet the second
+    # row's destination bytes [160, 192).
+    _native.Plan(_seg(dst_off=0, len=8, flags=4, aux_off=64), [1024], [1024], check_disjoint=True)
+    t = np.concatenate([_seg(dst_off=0, len=8, flags=4, aux_off=16, elem_bytes=8),
+                        _seg(src_off=0, dst_off=20, len=4, elem_bytes=8)])
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(t, [1024], [1024], check_disjoint=True)
+    assert e.value.code == -4
+    t = np.concatenate([_seg(dst_off=0, len=8, flags=4, aux_off=4), _seg(dst_off=16, len=8)])
+    with pytest.raises(_native.EmrsError) as e:
+        _native.Plan(t, [1024], [1024], check_disjoint=True)  # duplicate meets its own destination
     assert e.value.code == -4
 
 

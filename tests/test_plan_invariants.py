@@ -11,6 +11,7 @@ import pytest
 from elasticmegatron_amd import _native
 from elasticmegatron_amd import ParallelStrategy as PS
 from elasticmegatron_amd.resharding import model_spec as ms
+from elasticmegatron_amd.resharding.layout import SEG_DUP
 from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 
@@ -56,13 +57,17 @@ def test_group_zero_plan_invariants():
     up = lower_redundant_backup(space.layout(a), space.layout(b), True)
     down = lower_redundant_backup(space.layout(b), space.layout(a), False)
     n = spec.num_params()
-    assert read_bytes(up) == payload_bytes(up) == 24 * n  # every shard written to both instances
+    # Scale-up: every shard is read once and written to both instances by one duplicating segment.
+    assert (up["flags"] == SEG_DUP).all()
+    assert read_bytes(up) == 12 * n and payload_bytes(up) == 24 * n
     assert read_bytes(down) == payload_bytes(down) == 12 * n
+    assert (down["flags"] == 0).all()
     for t, (x, y) in ((up, (a, b)), (down, (b, a))):
         lx, ly = space.layout(x), space.layout(y)
         st = _native.Plan(t, [lx.fp32_numel * 4] * 3 + [lx.bf16_numel * 2],
                           [ly.fp32_numel * 4] * 3 + [ly.bf16_numel * 2], check_disjoint=True).stats()
         assert st.scalar_bytes == 0
+        assert st.read_bytes == read_bytes(t) and st.payload_bytes == payload_bytes(t)
 
 
 @pytest.mark.parametrize("bf16_source", ["cast", "copy"])
