@@ -48,6 +48,31 @@ def test_separate_tensors_match_arena_path(gpu_device, factory, src, dst):
     assert bad == 0, first
 
 
+@pytest.mark.parametrize("n_inst", [2, 3])
+def test_group_zero_scale_up_over_separate_tensors(gpu_device, n_inst):
+    """Group-ZeRO 1 -> n instances with one allocation per tensor: duplicating segments whose second
+    copy lands in another tensor.  The bf16 model shards do not change and are carried over."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(4, 2, 1)), space.layout(PS(4 * n_inst, 2, 1, num_distributed_optimizer_instances=n_inst))
+    tm = TransferManager(check_disjoint=True)
+    tp = tm.compile_tensors(ls, ld, kind="backup_up")
+    assert (tp.segments["flags"] & 4).any()
+    print(f"case group zero 1 -> {n_inst}: {len(tp.src)} / {len(tp.dst)} tensors", flush=True)
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    src_t = [v.clone() for v in tp.src.views(a)]
+    dst_t = [torch.full((n,), float("nan"), dtype=torch.float32 if k[0] != "param" else torch.bfloat16,
+                        device=gpu_device) for n, k in zip(tp.dst.numel, tp.dst.keys)]
+    tm.execute_tensors(tp, src_t, dst_t)
+    b = TrainingState.allocate(ld, gpu_device)
+    for t, v, k in zip(dst_t, tp.dst.views(b), tp.dst.keys):
+        if k[0] != "param":
+            v.copy_(t)
+    b.arenas()[3].copy_(a.arenas()[3])
+    bad, first = b.verify_synthetic(SEED)
+    assert bad == 0, first
+
+
 def test_full_size_tensor_views(gpu_device):
     """Llama-2-7B TP1DP8 -> TP4DP2 over 2,838 / 3,516 tensor views: the device-table path at full size."""
     spec = ms.llama2_7b()

@@ -11,6 +11,7 @@ import pytest
 
 from elasticmegatron_amd import _native
 from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
+from elasticmegatron_amd.resharding.layout import SEG_DUP
 from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lower_transfer
 from elasticmegatron_amd.resharding.tensors import TensorBuffers, rebase_on_tensors
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
@@ -67,6 +68,11 @@ def test_group_zero_tensor_plan():
     table = lower_redundant_backup(ls, ld, scale_up=True)
     sb, db = TensorBuffers(ls), TensorBuffers(ld)
     tt = rebase_on_tensors(table, sb, db)
+    # Duplicates survive the re-basing: the second instance is another tensor of the same kind.
+    dup = tt[(tt["flags"] & SEG_DUP) != 0]
+    assert len(dup) and (dup["aux_buf"] != dup["dst_buf"]).all()
+    assert all(db.keys[int(a)][0] == db.keys[int(d)][0] for a, d in zip(dup["aux_buf"], dup["dst_buf"]))
+    _native.Plan(tt, sb.nbytes(), db.nbytes(), check_disjoint=True)
     a = new_arenas(ls)
     piece_fill_numpy(ls.pieces(), a, SEED)
     want = new_arenas(ld, fill=0)
