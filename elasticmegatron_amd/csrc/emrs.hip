@@ -3,11 +3,12 @@
 // One launch moves every segment of a plan.  The path is pure data movement
 // (no arithmetic), so the kernel is shaped for HBM streaming: 16-byte vector
 // loads and stores, eight of them in flight per lane before the first store,
-// a persistent grid whose workgroups each own a contiguous run of fixed-size
-// chunks, and a one-time binary search per workgroup for its first segment
-// followed by a forward walk.  Element sizes are irrelevant to the vector
-// path: offsets are converted to 16-byte units when the plan is created, so
-// bf16 parameters and fp32 optimizer state share one launch.
+// and a persistent grid that deals fixed-size chunks out to its workgroups in
+// short round-robin runs (each XCD sweeping its own eighth of the plan), with
+// one binary search per run for its first segment followed by a forward walk.
+// Element sizes are irrelevant to the vector path: offsets are converted to
+// 16-byte units when the plan is created, so bf16 parameters and fp32
+// optimizer state share one launch.
 //
 // The reference performs the same movement as per-parameter slicing plus
 // point-to-point messages (elastic_megatron/transfer/transfer.py:36-101,
@@ -75,7 +76,8 @@ static_assert(sizeof(Bases) <= 1024, "Bases travels in kernel arguments");
 // Segment as the kernel sees it.  Offsets and strides are in units of
 // (1 << unit_log2) bytes: 16 for the vector path, the element size otherwise.
 // A cast segment (fp32 only) also writes bf16 copies to aux, whose offset and
-// stride are in units of half that size (8 bytes, or one bf16).
+// stride are in units of half that size (8 bytes, or one bf16).  A duplicating
+// segment writes its values to aux as well, in the segment's own units.
 struct DevSeg {
   uint64_t src_off;
   uint64_t dst_off;
