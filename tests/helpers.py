@@ -41,6 +41,9 @@ SMALL_CASES = [
     ("llama2_dp8_dp6", small_llama2, [PS(8, 1, 1), PS(6, 1, 1)]),
     ("llama2_pp4_tp2", small_llama2, [PS(8, 1, 4), PS(8, 2, 1), PS(8, 2, 2)]),
     ("llama3_tp4_tp1pp2", small_llama3, [PS(8, 4, 1), PS(8, 1, 2)]),
+    # Context parallelism: the distributed optimizer shards over DP x CP ranks.
+    ("llama2_cp2tp2_cp2tp1_cp1tp2", small_llama2, [PS(8, 2, 1, context_parallel_size=2),
+                                                   PS(8, 1, 1, context_parallel_size=2), PS(8, 2, 1)]),
 ]
 
 

@@ -23,6 +23,9 @@ CASES = [
     ("1to2", PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
     ("1to3_tp2", PS(4, 2, 1), PS(12, 2, 1, num_distributed_optimizer_instances=3)),
     ("1to4_pp2", PS(4, 1, 2), PS(16, 1, 2, num_distributed_optimizer_instances=4)),
+    # The reference's own precondition for Group-ZeRO is CP > 1 (parallel_strategy.py:99-106).
+    ("1to2_cp2", PS(4, 1, 1, context_parallel_size=2),
+     PS(8, 1, 1, context_parallel_size=2, num_distributed_optimizer_instances=2)),
 ]
 
 

@@ -37,6 +37,20 @@ def _random_spec(rng, k):
         ddp_bucket_size=int(rng.choice([20_000, 60_000, 200_000])), overlap_grad_reduce=bool(rng.random() < 0.7))
 
 
+def _with_cp(rng, s, spec):
+    """``s`` with context parallelism 2 (half the DP ranks), when that is valid and the draw says so."""
+    if rng.random() >= 0.35:
+        return s
+    try:
+        c = PS(s.world_size, s.tensor_model_parallel_size, s.pipeline_model_parallel_size, context_parallel_size=2,
+               expert_model_parallel_size=s.expert_model_parallel_size,
+               expert_tensor_parallel_size=s.expert_tensor_parallel_size if spec.num_experts else None)
+        c.validate_for(spec.num_layers, spec.num_experts)
+    except (ValueError, AssertionError, RuntimeError):
+        return s
+    return c
+
+
 def _random_strategy(rng, spec):
     for _ in range(200):
         world = int(rng.choice([2, 4, 6, 8]))
@@ -62,16 +76,18 @@ def _random_strategy(rng, spec):
 
 def _cases():
     rng = np.random.default_rng(20261201)
+    cp_rng = np.random.default_rng(20261202)  # separate, so the other draws stay as they were
     out = []
     for k in range(N_CASES):
         spec = _random_spec(rng, k)
         a, b = _random_strategy(rng, spec), _random_strategy(rng, spec)
+        a, b = _with_cp(cp_rng, a, spec), _with_cp(cp_rng, b, spec)
         mode = "cast" if k % 2 == 0 else "copy"
         out.append(pytest.param(spec, a, b, mode, id=f"{k}-{'moe' if spec.num_experts else 'dense'}"
                                 f"-tp{a.tensor_model_parallel_size}pp{a.pipeline_model_parallel_size}"
-                                f"w{a.world_size}ep{a.expert_model_parallel_size}"
+                                f"w{a.world_size}ep{a.expert_model_parallel_size}cp{a.context_parallel_size}"
                                 f"-tp{b.tensor_model_parallel_size}pp{b.pipeline_model_parallel_size}"
-                                f"w{b.world_size}ep{b.expert_model_parallel_size}-{mode}"))
+                                f"w{b.world_size}ep{b.expert_model_parallel_size}cp{b.context_parallel_size}-{mode}"))
     return out
 
 
