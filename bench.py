@@ -301,7 +301,7 @@ def main():
             print(f"[bench] plan verification FAILED: {report.lines()[:3]}", file=sys.stderr)
             return 3
     if not args.no_copy_ceiling:
-        out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps)
+        out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps, plan.read_bytes, payload)
     views.clear()
     del b
     if not args.no_e2e:
@@ -314,34 +314,53 @@ def main():
     return 0
 
 
-def copy_ceiling(a, b, stream, traffic_gbps, reps=5):
-    """A plain contiguous copy, by the same kernel, from the source main arena to the destination
-    one: the copy speed of the very allocations the reshard ran on (physical placement moves
-    both together)."""
+def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
+    """What the very allocations the reshard ran on can do (physical placement moves every figure
+    together), with the same 16-byte non-temporal accesses:
+
+    - a plain contiguous copy of the source main arena into the destination one, by copy_plan_kernel;
+    - write-only: the same kernel zero-filling the destination main arena (no reads);
+    - read-only: emrs_xor_checksum over the source main arena (no writes);
+    - the workload's own read and write bytes moved one direction after the other at those two
+      rates, a figure a kernel that overlaps reads with writes can beat.
+    """
     import numpy as np
     import torch
 
     from elasticmegatron_amd import _native
-    from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
+    from elasticmegatron_amd.resharding.layout import SEG_ZERO_FILL, SEGMENT_DTYPE
 
     n = min(a.main.numel(), b.main.numel())
+
+    def timed(run):
+        for _ in range(2):
+            run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
     t = np.zeros(1, dtype=SEGMENT_DTYPE)
     t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0, 0, 0, 0, 0)
-    plan = _native.Plan(t, [n * 4], [n * 4])
-    run = lambda: plan.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream)  # noqa: E731
-    for _ in range(2):
-        run()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    copy = _native.Plan(t, [n * 4], [n * 4])
+    ms = timed(lambda: copy.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
+    t[0]["flags"] = SEG_ZERO_FILL
+    fill = _native.Plan(t, [n * 4], [n * 4])
+    w_ms = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
+    word = torch.zeros(1, dtype=torch.int32, device=a.main.device)
+    r_ms = timed(lambda: _native.xor_checksum(a.main.data_ptr(), n * 4, word.data_ptr(), stream.cuda_stream))
     gbps = 2 * n * 4 / (ms / 1e3) / 1e9
+    w_gbps, r_gbps = n * 4 / (w_ms / 1e3) / 1e9, n * 4 / (r_ms / 1e3) / 1e9
+    serial = (read_bytes + write_bytes) / (read_bytes / r_gbps + write_bytes / w_gbps)
     return {"gbps": round(gbps, 1), "bytes_per_launch": 2 * n * 4, "ms": round(ms, 4),
             "what": "one contiguous copy of the main arena by copy_plan_kernel, same allocations",
-            "reshard_frac_of_copy": round(traffic_gbps / gbps, 4)}
+            "reshard_frac_of_copy": round(traffic_gbps / gbps, 4),
+            "read_only_gbps": round(r_gbps, 1), "write_only_gbps": round(w_gbps, 1),
+            "serial_read_then_write_gbps": round(serial, 1),
+            "reshard_frac_of_serial": round(traffic_gbps / serial, 4)}
 
 
 def reshard_end_to_end(a, spec, src, dst, repad, tm, no_verify, reps=3):

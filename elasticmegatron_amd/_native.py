@@ -37,7 +37,7 @@ EMRS_ARG_BUFFERS = 128  # buffers per side passed in kernel arguments (more use 
 EXPORTS = (
     "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
     "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
-    "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare",
+    "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare", "emrs_xor_checksum",
 )
 
 # struct emrs_compare_stats
@@ -102,6 +102,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
     lib.emrs_plan_compare.restype = I
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
+    lib.emrs_xor_checksum.restype = I
+    lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
     if lib.emrs_abi_version() != 3:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
@@ -214,6 +216,14 @@ def synth_fill(pieces: np.ndarray, ptrs: Sequence[int], buf_bytes: Sequence[int]
     rc = load().emrs_synth_fill(pcs.ctypes.data if len(pcs) else None, len(pcs), _ptr_array(ptrs),
                                 _u64_array(buf_bytes), len(ptrs), int(seed), ctypes.c_void_p(int(stream)))
     _check(rc, "emrs_synth_fill")
+
+
+def xor_checksum(ptr: int, nbytes: int, out_ptr: int, stream: int = 0) -> None:
+    """Enqueue the XOR of every 32-bit word of device memory [ptr, ptr + nbytes) into the device
+    word at ``out_ptr``."""
+    rc = load().emrs_xor_checksum(ctypes.c_void_p(int(ptr)), int(nbytes), ctypes.c_void_p(int(out_ptr)),
+                                  ctypes.c_void_p(int(stream)))
+    _check(rc, "emrs_xor_checksum")
 
 
 def synth_verify(pieces: np.ndarray, ptrs: Sequence[int], buf_bytes: Sequence[int], seed: int,

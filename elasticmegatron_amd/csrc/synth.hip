@@ -245,6 +245,60 @@ int launch(bool verify, const emrs_piece *pieces, uint64_t n, void *const *bases
 
 }  // namespace
 
+namespace {
+
+// XOR of every 32-bit word of a buffer, read as the copy kernel reads: eight
+// 16-byte non-temporal loads in flight per lane, chunks of 256 lanes x 8
+// units dealt out grid-stride.  One atomic per wavefront at the end.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kXorUnroll = 8;
+constexpr uint64_t kXorChunk = (uint64_t)kThreads * kXorUnroll;
+
+__global__ __launch_bounds__(kThreads) void xor_checksum_kernel(const u32x4 *__restrict__ p, uint64_t n_units,
+                                                                 uint32_t *__restrict__ out) {
+  uint32_t acc = 0;
+  for (uint64_t base = (uint64_t)blockIdx.x * kXorChunk; base < n_units; base += (uint64_t)gridDim.x * kXorChunk) {
+    u32x4 v[kXorUnroll];
+#pragma unroll
+    for (int j = 0; j < kXorUnroll; ++j) {
+      const uint64_t i = base + (uint64_t)j * kThreads + threadIdx.x;
+      v[j] = i < n_units ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kXorUnroll; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  for (int off = 32; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off, 64);
+  if (threadIdx.x % 64 == 0 && acc) atomicXor(out, acc);
+}
+
+}  // namespace
+
+extern "C" int emrs_xor_checksum(const void *p, uint64_t bytes, uint32_t *out, void *stream) {
+  emrs_internal::clear_error();
+  if (!out || (bytes && !p)) return sfail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (reinterpret_cast<uintptr_t>(p) % 16 || bytes % 16)
+    return sfail(EMRS_ERR_MISALIGNED, "the buffer and its size must be multiples of 16 bytes");
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return sfail(EMRS_ERR_NO_DEVICE, "no HIP device is visible");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  e = hipMemsetAsync(out, 0, sizeof(uint32_t), st);
+  if (e != hipSuccess) return sfail(EMRS_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
+  const uint64_t n_units = bytes / 16;
+  if (n_units == 0) return EMRS_OK;
+  // Five resident workgroups per CU, as the copy kernel runs.
+  const uint64_t blocks = std::min<uint64_t>((n_units + kXorChunk - 1) / kXorChunk, (uint64_t)std::max(cus, 1) * 5);
+  hipLaunchKernelGGL(xor_checksum_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, st,
+                     static_cast<const u32x4 *>(p), n_units, out);
+  e = hipGetLastError();
+  if (e != hipSuccess) return sfail(EMRS_ERR_HIP, std::string("xor_checksum_kernel launch: ") + hipGetErrorString(e));
+  return EMRS_OK;
+}
+
 extern "C" int emrs_synth_fill(const emrs_piece *pieces, uint64_t n_pieces, void *const *bases,
                                const uint64_t *buf_bytes, uint32_t n_bufs, uint64_t seed, void *stream) {
   return launch(false, pieces, n_pieces, bases, buf_bytes, n_bufs, seed, stream, nullptr, nullptr);

@@ -273,6 +273,15 @@ int emrs_synth_verify(const emrs_piece *pieces, uint64_t n_pieces,
                       uint32_t n_bufs, uint64_t seed, void *stream,
                       uint64_t *mismatches, uint64_t *first_bad);
 
+/*
+ * XOR of every 32-bit word of the device buffer [p, p + bytes) into the
+ * device word *out (zeroed first), enqueued on `stream`.  p and bytes must be
+ * multiples of 16.  The buffer is read as the copy kernel reads its sources,
+ * so the call also measures this device's read-only HBM bandwidth.  No
+ * counterpart in the reference.
+ */
+int emrs_xor_checksum(const void *p, uint64_t bytes, uint32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -214,3 +214,16 @@ def test_alias_checks_before_any_device_work(n_bufs):
     with pytest.raises(_native.EmrsError) as e:
         plan.execute(bad, dst, 0)
     assert e.value.code == -3
+
+
+def test_xor_checksum_rejects_bad_arguments_before_touching_a_device():
+    with pytest.raises(_native.EmrsError) as e:
+        _native.xor_checksum(0x1000, 16, 0)               # no output word
+    assert e.value.code == -1
+    with pytest.raises(_native.EmrsError) as e:
+        _native.xor_checksum(0, 16, 0x2000)               # no buffer
+    assert e.value.code == -1
+    for ptr, n in ((0x1008, 16), (0x1000, 24)):            # 16-byte alignment of address and size
+        with pytest.raises(_native.EmrsError) as e:
+            _native.xor_checksum(ptr, n, 0x2000)
+        assert e.value.code == -3
