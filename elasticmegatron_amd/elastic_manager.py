@@ -140,6 +140,16 @@ class ElasticMegatronManager:
             logger.info(msg)
         return msg
 
+    def clear_meta_state(self, parallel_strategy: StrategyLike) -> int:
+        """Forget what a meta-device reshard pre-built for ``parallel_strategy``
+        (elastic_manager.py:180-187): here, the cached copy plans into or out of
+        it.  The live state's own strategy cannot be cleared.  Returns the
+        number of plans dropped."""
+        strategy = _as_strategy(parallel_strategy)
+        if strategy == self.training_state.parallel_strategy:
+            raise AssertionError("the live training state uses this strategy: it is not a meta state")
+        return self.transfer_manager.evict(strategy)
+
     def reshard(self, new_parallel_strategy: StrategyLike, logger: Optional[logging.Logger] = None,
                 is_meta_device: bool = False, save_ckpt: bool = False,
                 verify: bool = False) -> Optional[TrainingState]:

@@ -101,6 +101,17 @@ class TransferManager:
         """Plan without moving data (transfer.py:32-34)."""
         self.fake_transfer = fake
 
+    def evict(self, strategy: Optional[ParallelStrategy] = None) -> int:
+        """Drop the cached plans (copy and verification) that switch from or to ``strategy``, or every
+        cached plan when it is None; returns how many were dropped.  A dropped plan frees its device
+        segment tables once nothing else holds it."""
+        n = 0
+        for cache in (self._plans, self._verify_plans):
+            for key in [k for k in cache if strategy is None or any(x == strategy for x in k)]:
+                del cache[key]
+                n += 1
+        return n
+
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                 include_bf16: bool = True) -> CompiledPlan:
         key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16, self.bf16_source)

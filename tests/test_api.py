@@ -27,6 +27,20 @@ def test_meta_device_reshard_plans_without_touching_memory():
         mgr.reshard(SEQ[1], save_ckpt=True)
 
 
+def test_clear_meta_state_drops_the_prebuilt_plans():
+    """elastic_manager.py:180-187: a meta-device pre-build is forgotten; the live strategy is not a meta state."""
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
+    mgr.reshard(SEQ[1], is_meta_device=True)
+    mgr.reshard(SEQ[2], is_meta_device=True)
+    assert len(mgr.transfer_manager._plans) == 2
+    assert mgr.clear_meta_state(SEQ[1]) == 1
+    assert len(mgr.transfer_manager._plans) == 1   # the pre-build for SEQ[2] stays
+    assert mgr.clear_meta_state(SEQ[1]) == 0
+    with pytest.raises(AssertionError):
+        mgr.clear_meta_state(SEQ[0])
+    assert mgr.transfer_manager.evict() == 1 and not mgr.transfer_manager._plans
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a GPU")
 def test_reshard_without_gpu_raises():
     mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
