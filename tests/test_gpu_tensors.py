@@ -73,13 +73,22 @@ def test_group_zero_scale_up_over_separate_tensors(gpu_device, n_inst):
     assert bad == 0, first
 
 
-def test_full_size_tensor_views(gpu_device):
-    """Llama-2-7B TP1DP8 -> TP4DP2 over 2,838 / 3,516 tensor views: the device-table path at full size."""
-    spec = ms.llama2_7b()
+@pytest.mark.parametrize("factory,src,dst", [
+    (ms.llama2_7b, PS(8, 1, 1), PS(8, 4, 1)),
+    (ms.llama3_8b, PS(8, 2, 2), PS(8, 4, 1)),
+    (ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4), PS(8, 1, 1, expert_model_parallel_size=8)),
+    (ms.llama2_7b, PS(8, 1, 1), PS(6, 1, 1)),
+], ids=["llama2-7b-tp1dp8-tp4dp2", "llama3-8b-tp2pp2dp2-tp4pp1dp2", "mixtral-4l-ep4-ep8", "llama2-7b-dp8-dp6"])
+def test_full_size_tensor_views(gpu_device, factory, src, dst):
+    """Full-size switches over one tensor view per stored tensor (thousands per side): the device-table
+    path, checked against the generator and by the plan's own verification."""
+    spec = factory()
     space = build_virtual_model(spec)
-    ls, ld = space.layout(PS(8, 1, 1)), space.layout(PS(8, 4, 1))
+    ls, ld = space.layout(src), space.layout(dst)
     tm = TransferManager()
     tp = tm.compile_tensors(ls, ld)
+    print(f"case full size tensors {spec.name} {src} -> {dst}: {len(tp.src)} / {len(tp.dst)} tensors", flush=True)
+    a = b = None
     try:
         a = TrainingState.allocate(ls, gpu_device)
         b = TrainingState.allocate(ld, gpu_device)
