@@ -751,22 +751,22 @@ __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase
       ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
     }
     const uint32_t ops = s.ops();
-    const T e = (ops & 2) ? T{} : src[so];
-    const T g = dst[dof];
+    const T e = (ops & 2) ? T{} : ld<T, true>(src + so);
+    const T g = ld<T, true>(dst + dof);
     uint32_t ew[4] = {0, 0, 0, 0}, gw[4] = {0, 0, 0, 0};
     words_of(e, ew);
     words_of(g, gw);
     cmp_words(m, ew, gw, (uint32_t)sizeof(T), s.elem_log2());
     if (ops & 4) {
       uint32_t dw[4] = {0, 0, 0, 0};
-      words_of(reinterpret_cast<const T *>(abase)[ao], dw);
+      words_of(ld<T, true>(reinterpret_cast<const T *>(abase) + ao), dw);
       cmp_words(x, ew, dw, (uint32_t)sizeof(T), s.elem_log2());
     }
     if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
       if (ops & 1) {
         uint32_t ea[2] = {0, 0}, ga[2] = {0, 0};
         aux_words_of(C::cast(e), ea);
-        aux_words_of(aux[ao], ga);
+        aux_words_of(ld<A, true>(aux + ao), ga);
         cmp_words(x, ea, ga, (uint32_t)sizeof(A), 1);
       }
     }
@@ -815,46 +815,82 @@ __device__ void flush(const LaneAcc &a, GroupAcc *g) {
   if (a.max_rel > 0.0f) atomicMax(&g->max_rel_bits, __float_as_uint(a.max_rel));
 }
 
-// One workgroup per chunk, grid-stride over the chunks.  No early exit: every
-// thread reaches every barrier.
+// Add the workgroup's lane sums to their groups and clear them: the values
+// compared, and with `aux` the second destination's.  Every thread calls it.
+__device__ void flush_block(LaneAcc &m, LaneAcc &x, uint32_t g, uint32_t ga, bool aux, GroupAcc *acc,
+                            double *lds_d, uint32_t *lds_u, float *lds_f) {
+  block_reduce(m, lds_d, lds_u, lds_f);
+  if (threadIdx.x == 0) flush(m, acc + g);
+  if (aux) {
+    block_reduce(x, lds_d, lds_u, lds_f);
+    if (threadIdx.x == 0) flush(x, acc + ga);
+  }
+  __syncthreads();  // the LDS slots are reused by the next reduction
+  m = LaneAcc();
+  x = LaneAcc();
+}
+
+// Workgroups take runs of `run` consecutive chunks, each XCD sweeping its own
+// eighth of the plan (workgroup b runs on XCD b % 8; the grid is a multiple of
+// 8), as the copy kernel does.  Lane sums stay in registers while consecutive
+// chunks share their (group, aux group); they are reduced over the workgroup
+// only when that pair changes and at the end.  Every decision depends on the
+// segment alone, so it is uniform across the workgroup, and every thread
+// reaches every barrier.
 template <bool kTable>
 __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
-    uint32_t n_segs, uint64_t n_chunks, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
+    uint32_t n_segs, uint64_t n_chunks, uint32_t run, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
     const uint64_t *__restrict__ dst_tab, GroupAcc *__restrict__ acc) {
   __shared__ double lds_d[2 * kThreads / 64];
   __shared__ uint32_t lds_u[2 * kThreads / 64];
   __shared__ float lds_f[2 * kThreads / 64];
-  for (uint64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+  const uint64_t xcd = blockIdx.x & 7;
+  const uint64_t c1 = n_chunks * (xcd + 1) / 8;
+  const uint64_t step = (uint64_t)(gridDim.x >> 3) * run;
+  LaneAcc m, x;
+  uint32_t cur_g = 0, cur_ga = 0;
+  bool open = false, cur_aux = false;
+  for (uint64_t c = n_chunks * xcd / 8 + (uint64_t)(blockIdx.x >> 3) * run; c < c1; c += step) {
+    const uint64_t c_end = min(c + run, c1);
     uint32_t lo = 0, hi = n_segs - 1;
     while (lo < hi) {
       const uint32_t mid = (lo + hi + 1) >> 1;
       if (segs[mid].chunk_begin <= c) lo = mid;
       else hi = mid - 1;
     }
-    const DevSeg s = segs[lo];
-    const uint32_t total = s.len * s.rows;
-    const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
-    const uint32_t u_end = min(u0 + kChunkUnits, total);
-    const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
-    const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
-    const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
-    LaneAcc m, x;
-    switch (s.unit_log2()) {
-      case 4: compare_chunk<u32x4>(s, sb, db, ab, u0, u_end, m, x); break;
-      case 3: compare_chunk<uint64_t>(s, sb, db, ab, u0, u_end, m, x); break;
-      case 2: compare_chunk<uint32_t>(s, sb, db, ab, u0, u_end, m, x); break;
-      case 1: compare_chunk<uint16_t>(s, sb, db, ab, u0, u_end, m, x); break;
-      default: compare_chunk<uint8_t>(s, sb, db, ab, u0, u_end, m, x); break;
+    uint32_t si = lo;
+    uint64_t s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+    for (uint64_t q = c; q < c_end; ++q) {
+      while (q >= s_end) {
+        ++si;
+        s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+      }
+      const DevSeg s = segs[si];
+      const uint32_t g = groups[si], ga = aux_groups[si];
+      const bool aux = (s.ops() & 5) != 0;  // cast or duplicate
+      if (open && (g != cur_g || aux != cur_aux || (aux && ga != cur_ga)))
+        flush_block(m, x, cur_g, cur_ga, cur_aux, acc, lds_d, lds_u, lds_f);
+      open = true;
+      cur_g = g;
+      cur_ga = ga;
+      cur_aux = aux;
+      const uint32_t total = s.len * s.rows;
+      const uint32_t u0 = (uint32_t)(q - s.chunk_begin) * kChunkUnits;
+      const uint32_t u_end = min(u0 + kChunkUnits, total);
+      const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
+      const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
+      const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+      switch (s.unit_log2()) {
+        case 4: compare_chunk<u32x4>(s, sb, db, ab, u0, u_end, m, x); break;
+        case 3: compare_chunk<uint64_t>(s, sb, db, ab, u0, u_end, m, x); break;
+        case 2: compare_chunk<uint32_t>(s, sb, db, ab, u0, u_end, m, x); break;
+        case 1: compare_chunk<uint16_t>(s, sb, db, ab, u0, u_end, m, x); break;
+        default: compare_chunk<uint8_t>(s, sb, db, ab, u0, u_end, m, x); break;
+      }
     }
-    block_reduce(m, lds_d, lds_u, lds_f);
-    if (threadIdx.x == 0) flush(m, acc + groups[lo]);
-    if (s.ops() & 5) {  // cast or duplicate; uniform across the workgroup
-      block_reduce(x, lds_d, lds_u, lds_f);
-      if (threadIdx.x == 0) flush(x, acc + aux_groups[lo]);
-    }
-    __syncthreads();  // the LDS slots are reused by the next chunk
   }
+  if (open) flush_block(m, x, cur_g, cur_ga, cur_aux, acc, lds_d, lds_u, lds_f);
 }
 
 }  // namespace
@@ -1108,6 +1144,13 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   DevSeg *table = nullptr;
   rc = device_table(plan, dev, &table);
   if (rc) return rc;
+  int resident_cmp = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident_cmp, compare_plan_kernel<false>, kThreads, 0) !=
+          hipSuccess ||
+      resident_cmp <= 0) {
+    (void)hipGetLastError();
+    resident_cmp = 4;
+  }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
@@ -1123,14 +1166,19 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   uint64_t *tab = nullptr;
   if (e == hipSuccess && upload_pointer_table(rb, st, &tab) != EMRS_OK) e = hipErrorOutOfMemory;
   if (e == hipSuccess) {
-    const uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * 8);
+    // A persistent grid of resident workgroups, a multiple of 8 (one eighth
+    // of the plan per XCD), in runs of up to 32 chunks: at most a quarter of
+    // each workgroup's share, so that small plans still spread out.
+    uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * (uint32_t)resident_cmp);
+    blocks = std::max<uint64_t>(8, blocks / 8 * 8);
+    const uint32_t run = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32, plan->n_chunks / (blocks * 4)));
     const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
     if (rb.table)
       hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                         grp + nd, (uint32_t)nd, plan->n_chunks, rb.src, rb.dst, tab, dtab, acc);
+                         grp + nd, (uint32_t)nd, plan->n_chunks, run, rb.src, rb.dst, tab, dtab, acc);
     else
       hipLaunchKernelGGL(compare_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                         grp + nd, (uint32_t)nd, plan->n_chunks, rb.src, rb.dst, tab, dtab, acc);
+                         grp + nd, (uint32_t)nd, plan->n_chunks, run, rb.src, rb.dst, tab, dtab, acc);
     e = hipGetLastError();
   }
   if (tab) (void)hipFreeAsync(tab, st);
