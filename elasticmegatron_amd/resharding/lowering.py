@@ -40,6 +40,7 @@ import numpy as np
 
 from .layout import (ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, SEGMENT_DTYPE, Geometry, Holder, StrategyLayout,
                      view2d)
+from .resharding_tp import is_pow2
 
 
 @dataclass(frozen=True)
@@ -208,6 +209,11 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
     """
     if bf16_source not in ("cast", "copy"):
         raise ValueError(bf16_source)
+    # The reference computes every parameter's TP maps, and those accept powers of two only
+    # (resharding_tp.py:98-99), whatever path built the layouts.
+    for st in (src.strategy, dst.strategy):
+        if not is_pow2(st.tensor_model_parallel_size):
+            raise AssertionError("TP sizes must be powers of two")
     cast = include_bf16 and bf16_source == "cast"
     if cast and not include_fp32:
         raise ValueError("the bf16 cast rides on the fp32 main segments")

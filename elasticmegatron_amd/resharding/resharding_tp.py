@@ -29,7 +29,7 @@ class TensorParallelReshardingInfo:
     recv_info: Dict[int, Dict[int, ParamRange]]
 
 
-def _is_pow2(n: int) -> bool:
+def is_pow2(n: int) -> bool:
     return n >= 1 and (n & (n - 1)) == 0
 
 
@@ -67,7 +67,7 @@ class TensorParallelAttr:
         return self.get_model_param_range(parallel_group_size).to_shape()
 
     def reshard(self, src_size: int, dst_size: int) -> TensorParallelReshardingInfo:
-        assert _is_pow2(src_size) and _is_pow2(dst_size), "TP sizes must be powers of two"
+        assert is_pow2(src_size) and is_pow2(dst_size), "TP sizes must be powers of two"
         key = (src_size, dst_size)
         info = self._cache.get(key)
         if info is None:

@@ -180,3 +180,20 @@ def test_execute_tensors_checks_bytes():
     dst = [torch.empty(n, dtype=torch.int8) for n in tp.dst.numel]   # right numel, too few bytes
     with pytest.raises(ValueError, match="bytes"):
         tm.execute_tensors(tp, src, dst)
+
+
+@pytest.mark.parametrize("repad,padded,vocab", [(False, 768, 700), (True, 512, 500)])
+def test_non_power_of_two_tp_is_refused_on_every_path(repad, padded, vocab):
+    """resharding_tp.py:98-99: TP sizes must be powers of two, also when the vocabulary is re-padded
+    (500 pads to 512 at TP1 and 768 at TP3: a switch between two model spaces, which does not go
+    through register_reshard)."""
+    from elasticmegatron_amd.resharding.model_spec import ModelSpec
+
+    spec = ModelSpec(name="tp3", num_layers=2, hidden_size=384, num_attention_heads=6, kv_channels=64,
+                     ffn_hidden_size=768, padded_vocab_size=padded, vocab_size=vocab)
+    mgr = ElasticMegatronManager([dict(world_size=6, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+                                  dict(world_size=6, tensor_model_parallel_size=3, pipeline_model_parallel_size=1)],
+                                 spec, device="cpu", repad_vocab=repad)
+    with pytest.raises(AssertionError, match="powers of two"):
+        mgr.reshard(dict(world_size=6, tensor_model_parallel_size=3, pipeline_model_parallel_size=1),
+                    is_meta_device=True)
