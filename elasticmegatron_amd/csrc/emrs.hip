@@ -412,6 +412,10 @@ struct emrs_plan {
   emrs_plan_stats stats{};
   std::mutex mu;
   std::vector<DevSeg *> dev_tables;  // per device, uploaded on first use
+  // Plans with more than kArgBuffers buffers on a side: per device, the
+  // pointer table of the first execution and the base pointers it holds.
+  std::vector<uint64_t *> ptr_tables;
+  std::vector<std::vector<uint64_t>> ptr_contents;
 };
 
 namespace {
@@ -606,12 +610,44 @@ int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *ds
   return EMRS_OK;
 }
 
-// Stream-ordered device copy of the pointer table; freed after the launch
-// with free_pointer_table on the same stream.
-int upload_pointer_table(const ResolvedBases &rb, hipStream_t st, uint64_t **out) {
+// The device pointer table of an execution or comparison (nullptr when the
+// bases travel in kernel arguments).  The plan keeps, per device, the table of
+// the first call and reuses it while the bases are the same: it is uploaded
+// synchronously and never written again, so any stream may read it.  Calls
+// with other bases get a stream-ordered table of their own (*owned = true),
+// which the caller frees on the same stream after the launch.
+int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t st, uint64_t **out, bool *owned) {
   *out = nullptr;
+  *owned = false;
   if (!rb.table) return EMRS_OK;
   const size_t bytes = rb.ptrs.size() * sizeof(uint64_t);
+  {
+    std::lock_guard<std::mutex> lk(plan->mu);
+    if ((int)plan->ptr_tables.size() <= dev) {
+      plan->ptr_tables.resize(dev + 1, nullptr);
+      plan->ptr_contents.resize(dev + 1);
+    }
+    if (plan->ptr_tables[dev]) {
+      if (plan->ptr_contents[dev] == rb.ptrs) {
+        *out = plan->ptr_tables[dev];
+        return EMRS_OK;
+      }
+    } else {
+      uint64_t *t = nullptr;
+      hipError_t e = hipMalloc(reinterpret_cast<void **>(&t), bytes);
+      if (e != hipSuccess) return hip_fail(e, "hipMalloc(pointer table)");
+      e = hipMemcpy(t, rb.ptrs.data(), bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        (void)hipFree(t);
+        return hip_fail(e, "hipMemcpy(pointer table)");
+      }
+      plan->ptr_tables[dev] = t;
+      plan->ptr_contents[dev] = rb.ptrs;
+      *out = t;
+      return EMRS_OK;
+    }
+  }
+  *owned = true;
   hipError_t e = hipMallocAsync(reinterpret_cast<void **>(out), bytes, st);
   if (e != hipSuccess) {
     *out = nullptr;
@@ -1081,7 +1117,8 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint32_t xcd_stride = remap ? (uint32_t)(blocks / 8) : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint64_t *tab = nullptr;
-  rc = upload_pointer_table(rb, st, &tab);
+  bool tab_owned = false;
+  rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
   if (rc) return rc;
   const uint64_t *stab = tab, *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
   const dim3 grid((uint32_t)blocks), block(kThreads);
@@ -1099,7 +1136,7 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
     hipLaunchKernelGGL((copy_plan_kernel<false, false>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
                        xcd_stride, run, rb.src, rb.dst, stab, dtab);
   hipError_t le = hipGetLastError();
-  if (tab) (void)hipFreeAsync(tab, st);
+  if (tab_owned) (void)hipFreeAsync(tab, st);
   if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
   return EMRS_OK;
 }
@@ -1164,7 +1201,8 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   e = hipMemsetAsync(acc, 0, acc_bytes, st);
   if (e == hipSuccess) e = hipMemcpyAsync(grp, g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
   uint64_t *tab = nullptr;
-  if (e == hipSuccess && upload_pointer_table(rb, st, &tab) != EMRS_OK) e = hipErrorOutOfMemory;
+  bool tab_owned = false;
+  if (e == hipSuccess && pointer_table(plan, dev, rb, st, &tab, &tab_owned) != EMRS_OK) e = hipErrorOutOfMemory;
   if (e == hipSuccess) {
     // A persistent grid of resident workgroups, a multiple of 8 (one eighth
     // of the plan per XCD), in runs of up to 32 chunks: at most a quarter of
@@ -1181,7 +1219,7 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
                          grp + nd, (uint32_t)nd, plan->n_chunks, run, rb.src, rb.dst, tab, dtab, acc);
     e = hipGetLastError();
   }
-  if (tab) (void)hipFreeAsync(tab, st);
+  if (tab_owned) (void)hipFreeAsync(tab, st);
   if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   (void)hipFree(buf);
@@ -1202,12 +1240,15 @@ int emrs_plan_destroy(emrs_plan *plan) {
   if (!plan) return EMRS_OK;
   int prev = 0;
   (void)hipGetDevice(&prev);
-  for (size_t d = 0; d < plan->dev_tables.size(); ++d) {
-    if (plan->dev_tables[d]) {
+  for (size_t d = 0; d < std::max(plan->dev_tables.size(), plan->ptr_tables.size()); ++d) {
+    DevSeg *segs = d < plan->dev_tables.size() ? plan->dev_tables[d] : nullptr;
+    uint64_t *ptrs = d < plan->ptr_tables.size() ? plan->ptr_tables[d] : nullptr;
+    if (segs || ptrs) {
       (void)hipSetDevice((int)d);
-      // Launches enqueued on any stream may still read the table.
+      // Launches enqueued on any stream may still read the tables.
       (void)hipDeviceSynchronize();
-      (void)hipFree(plan->dev_tables[d]);
+      if (segs) (void)hipFree(segs);
+      if (ptrs) (void)hipFree(ptrs);
     }
   }
   (void)hipSetDevice(prev);

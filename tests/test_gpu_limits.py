@@ -46,6 +46,33 @@ def test_many_buffers(gpu_device, n):
         assert torch.equal(dsts[j], want), (i, j)
 
 
+def test_pointer_table_reuse_and_new_bases(gpu_device):
+    """A plan over more than 128 buffers keeps the pointer table of its first execution and reuses it
+    while the bases repeat; other bases get a table of their own.  Every call must land where its
+    own bases say, on the current stream and on a second one."""
+    n, size = 300, 1024
+    rng = np.random.default_rng(7)
+    srcs = [torch.from_numpy(rng.integers(0, 256, size, dtype=np.uint8)).to(gpu_device) for _ in range(n)]
+    sets = [[torch.zeros(size, dtype=torch.uint8, device=gpu_device) for _ in range(n)] for _ in range(2)]
+    t = np.zeros(n, dtype=SEGMENT_DTYPE)
+    t[:] = [(i, (i * 7) % n, 4, 0, 16, 32, 128, 1, 0, 0, 0, 0, 0, 0) for i in range(n)]
+    plan = _native.Plan(t, [size] * n, [size] * n, check_disjoint=True)
+    side = torch.cuda.Stream()
+    sp = [s.data_ptr() for s in srcs]
+    for k, (which, stream) in enumerate([(0, None), (0, None), (1, None), (0, side), (1, side), (0, None)]):
+        print(f"case pointer table call {k}: destination set {which}", flush=True)
+        for d in sets[which]:
+            d.zero_()
+        st = stream if stream is not None else torch.cuda.current_stream()
+        st.wait_stream(torch.cuda.current_stream())
+        plan.execute(sp, [d.data_ptr() for d in sets[which]], st.cuda_stream)
+        torch.cuda.synchronize()
+        for i in range(n):
+            got = sets[which][(i * 7) % n]
+            assert torch.equal(got[128:640], srcs[i][64:576]), (k, i)
+            assert int(got[:128].sum()) == 0 and int(got[640:].sum()) == 0, (k, i)
+
+
 def test_segments_beyond_two_to_the_thirty_units(gpu_device):
     nbytes = 3 << 29  # 1.5 GiB
     src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu_device)
