@@ -31,11 +31,12 @@ from typing import Callable, Dict, List, Optional, Union
 import torch
 
 from .megatron_manager.parallel_strategy import ParallelStrategy
-from .megatron_manager.training_state import TrainingState
+from .megatron_manager.training_state import ARENA_GRANULE_BYTES, TrainingState
 from .resharding.model_spec import ModelSpec
 from .resharding.util import Timer
 from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
 from .transfer.transfer import TransferManager
+from .transfer.verify import merge_stats, report_from_stats
 
 StrategyLike = Union[ParallelStrategy, Dict[str, int]]
 
@@ -49,11 +50,21 @@ class ElasticMegatronManager:
                  training_state: Optional[TrainingState] = None, device=None,
                  release_source: bool = True, repad_vocab: bool = False,
                  send_fn: Optional[Callable] = None, recv_fn: Optional[Callable] = None,
-                 broadcast_fn: Optional[Callable] = None, use_p2p_to_collective: bool = True):
+                 broadcast_fn: Optional[Callable] = None, use_p2p_to_collective: bool = True,
+                 low_memory: bool = False):
         """``model_spec`` and ``training_state`` stand in for the reference's live Megatron
         ``model`` / ``optimizer`` (elastic_manager.py:41-82).  ``send_fn``, ``recv_fn``,
         ``broadcast_fn`` and ``use_p2p_to_collective`` are accepted as the reference accepts
         them and handed to the TransferManager; on one device no message is sent.
+
+        ``low_memory=True`` runs each switch in three stages, one optimizer kind at a time: the
+        destination arena of a kind is allocated just before its stage and, with
+        ``release_source``, the source arena is released right after it, as the reference releases
+        every optimizer tensor once it is sent.  The peak is the source state plus one fp32 arena
+        and the bf16 params of the destination, instead of both whole states.  The fp32 arenas are
+        then allocated in 1 GiB granules, so that the memory a released source arena leaves serves
+        the next destination arena without a call to the driver (a state passed in
+        ``training_state`` should be allocated with ``granule_bytes=ARENA_GRANULE_BYTES`` too).
         """
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
@@ -77,10 +88,13 @@ class ElasticMegatronManager:
         self.transfer_manager = TransferManager(send_fn, recv_fn, broadcast_fn)
         self.use_p2p_to_collective = use_p2p_to_collective
         self.release_source = release_source
+        self.low_memory = low_memory
+        self.last_stage_ms: List[Dict[str, float]] = []   # staged switches: per stage, allocate / execute ms
         self.last_transfer_ms = 0.0
         self.last_verification = None
         if training_state is None:
-            training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device)
+            training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device,
+                                                    granule_bytes=ARENA_GRANULE_BYTES if low_memory else 0)
         self.training_state = training_state
 
     def _spec_for(self, strategy: ParallelStrategy) -> ModelSpec:
@@ -115,6 +129,42 @@ class ElasticMegatronManager:
         with Timer() as t:
             self.transfer_manager.execute(plan, src, dst)
         return t.elapsed
+
+    def transfer_staged(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
+                        verify: bool = False):
+        """The switch in three launches, one optimizer kind at a time (see ``low_memory``).
+
+        ``dst`` may start without fp32 arenas; each is allocated just before its stage.  With
+        ``release_source`` the source arena of each kind is released right after its stage, once
+        it has been checked when ``verify`` is set.  Returns (executor ms summed over the stages,
+        verification records or None).
+        """
+        if kind == "transfer":
+            space = src.layout.space
+            if space is dst.layout.space:
+                space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
+            space.src_state, space.dst_state = src, dst
+        stages = self.transfer_manager.compile_staged(src.layout, dst.layout, kind)
+        elapsed, stats, names = 0.0, None, None
+        self.last_stage_ms = []
+        for k, plan in enumerate(stages):
+            with Timer() as ta:
+                dst.allocate_kind(k)
+            with Timer() as te:
+                self.transfer_manager.execute(plan, src, dst)
+            elapsed += ta.elapsed + te.elapsed
+            self.last_stage_ms.append({"allocate": ta.elapsed, "execute": te.elapsed})
+            if verify:
+                part, names = self.transfer_manager.verify_stats(src, dst, kind, stage=k)
+                stats = merge_stats(stats, part)
+                if int(part["mismatches"].sum()):
+                    # Stop before this stage's source is released; earlier stages were checked.
+                    raise RuntimeError(f"reshard verification failed in stage {k} "
+                                       f"({('main', 'exp_avg', 'exp_avg_sq')[k]}): "
+                                       + "\n".join(report_from_stats(stats, names).lines()[:20]))
+            if self.release_source:
+                src.release_kind(k)
+        return elapsed, (stats, names) if verify else None
 
     def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool) -> float:
         plan = self.transfer_manager.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
@@ -182,19 +232,30 @@ class ElasticMegatronManager:
         else:
             plan = self.transfer_manager.compile(src_state.layout, dst_layout,
                                                  "backup_up" if backup else "backup_down")
+        kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+        if self.low_memory:
+            self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind)
         if is_meta_device:
             return None
-        if backup is None:
-            dst_state = TrainingState.allocate(dst_layout, src_state.device)
-            elapsed = self.transfer_params(src_state, dst_state)
+        # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over.
+        param = src_state.param if backup is not None else None
+        report = None
+        if self.low_memory:
+            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),
+                                               granule_bytes=ARENA_GRANULE_BYTES)
+            elapsed, checked = self.transfer_staged(src_state, dst_state, kind, verify)
+            if verify:
+                report = report_from_stats(*checked)
         else:
-            # Model-parallel shards are unchanged, so the bf16 params carry over as they are.
-            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=src_state.param)
-            elapsed = self.redundant_backup(src_state, dst_state, backup)
+            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param)
+            if backup is None:
+                elapsed = self.transfer_params(src_state, dst_state)
+            else:
+                elapsed = self.redundant_backup(src_state, dst_state, backup)
+            if verify:
+                report = self.transfer_manager.verify(src_state, dst_state, kind)
         self.last_transfer_ms = elapsed
         if verify:
-            kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
-            report = self.transfer_manager.verify(src_state, dst_state, kind)
             self.last_verification = report
             if not report.bit_exact:
                 lines = report.lines()

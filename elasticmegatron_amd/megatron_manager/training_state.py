@@ -37,29 +37,68 @@ class OptimizerTensorInfo:
         return [self.main_weight, self.exp_avg, self.exp_avg_sq]
 
 
+# Capacity granule of fp32 arenas that are allocated and released one at a time: arenas of two
+# layouts of one model differ by a few MB of padding, and rounding both up to this granule lets the
+# block a released source arena leaves in torch's caching allocator serve the next destination
+# arena, with no call to the driver.
+ARENA_GRANULE_BYTES = 1 << 30
+
+
 class TrainingState:
     def __init__(self, layout: StrategyLayout, main: torch.Tensor, exp_avg: torch.Tensor,
-                 exp_avg_sq: torch.Tensor, param: torch.Tensor):
+                 exp_avg_sq: torch.Tensor, param: torch.Tensor, granule_bytes: int = 0):
         self.layout = layout
         self.main = main
         self.exp_avg = exp_avg
         self.exp_avg_sq = exp_avg_sq
         self.param = param
+        self.granule_bytes = granule_bytes
 
     @property
     def parallel_strategy(self):
         return self.layout.strategy
 
     @classmethod
-    def allocate(cls, layout: StrategyLayout, device=None, param: Optional[torch.Tensor] = None) -> "TrainingState":
-        """Uninitialised arenas for ``layout``; ``param`` may alias an existing bf16 arena."""
+    def allocate(cls, layout: StrategyLayout, device=None, param: Optional[torch.Tensor] = None,
+                 kinds: Tuple[int, ...] = (0, 1, 2), granule_bytes: int = 0) -> "TrainingState":
+        """Uninitialised arenas for ``layout``; ``param`` may alias an existing bf16 arena.
+
+        ``kinds``: the fp32 arenas to allocate now (0 main, 1 exp_avg,
+        2 exp_avg_sq); the others start empty and are allocated later with
+        :meth:`allocate_kind`, as a staged switch does.  ``granule_bytes``:
+        round each fp32 arena's capacity up to a multiple of it (see
+        ``ARENA_GRANULE_BYTES``); the arena itself is a view of the exact size.
+        """
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        f32 = [torch.empty(layout.fp32_numel, dtype=torch.float32, device=dev) for _ in range(3)]
         if param is None:
             param = torch.empty(layout.bf16_numel, dtype=torch.bfloat16, device=dev)
         elif param.numel() != layout.bf16_numel or param.dtype != torch.bfloat16:
             raise ValueError("aliased param arena does not match the layout")
-        return cls(layout, f32[0], f32[1], f32[2], param)
+        empty = torch.empty(0, dtype=torch.float32, device=dev)
+        st = cls(layout, empty, empty, empty, param, granule_bytes)
+        for k in kinds:
+            st.allocate_kind(k)
+        return st
+
+    _KINDS = ("main", "exp_avg", "exp_avg_sq")
+
+    def allocate_kind(self, kind: int) -> None:
+        """Allocate fp32 arena ``kind`` (0 main, 1 exp_avg, 2 exp_avg_sq) if it is empty."""
+        name, n = self._KINDS[kind], self.layout.fp32_numel
+        if getattr(self, name).numel() == 0 and n:
+            g = max(1, self.granule_bytes // 4)
+            cap = (n + g - 1) // g * g
+            setattr(self, name, torch.empty(cap, dtype=torch.float32, device=self.device)[:n])
+
+    def release_kind(self, kind: int) -> None:
+        """Free fp32 arena ``kind``, as the reference releases each optimizer tensor once it has been
+        sent (resharding_metadata.py:58-65): its storage is resized to nothing, so the memory goes
+        back to torch's caching allocator even where views of it are still held."""
+        name = self._KINDS[kind]
+        t = getattr(self, name)
+        if t.numel():
+            t.untyped_storage().resize_(0)
+        setattr(self, name, torch.empty(0, dtype=torch.float32, device=self.device))
 
     # ----- arenas -----
     def arenas(self) -> List[torch.Tensor]:
@@ -73,12 +112,12 @@ class TrainingState:
 
     @property
     def device(self) -> torch.device:
-        return self.main.device
+        return self.param.device
 
     def release_optimizer(self) -> None:
         """Drop the fp32 arenas (training_state.py:313-315)."""
-        empty = torch.empty(0, dtype=torch.float32, device=self.device)
-        self.main = self.exp_avg = self.exp_avg_sq = empty
+        for k in range(3):
+            self.release_kind(k)
 
     # ----- per-(rank, parameter) views -----
     def optimizer_tensor_info(self, vp, rank: int) -> Optional[OptimizerTensorInfo]:

@@ -180,6 +180,14 @@ def llama2_7b() -> ModelSpec:
                      overlap_grad_reduce=True)
 
 
+def llama2_13b() -> ModelSpec:
+    """40 layers, hidden 5120, 40 heads, SwiGLU FFN 13824, vocab 32000: 13.0e9 parameters, whose
+    state (182 GB) does not fit twice in one GPU's HBM."""
+    return ModelSpec(name="llama2-13b", num_layers=40, hidden_size=5120, num_attention_heads=40,
+                     ffn_hidden_size=13824, padded_vocab_size=32000, ddp_bucket_size=40_000_000,
+                     overlap_grad_reduce=True)
+
+
 def llama3_8b() -> ModelSpec:
     return ModelSpec(name="llama3-8b", num_layers=32, hidden_size=4096, num_attention_heads=32,
                      num_query_groups=8, ffn_hidden_size=14336, vocab_size=128256,

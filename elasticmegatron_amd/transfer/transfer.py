@@ -25,7 +25,7 @@ from ..megatron_manager.parallel_strategy import ParallelStrategy
 from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
-from ..resharding.layout import StrategyLayout
+from ..resharding.layout import ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, StrategyLayout
 from ..resharding.tensors import TensorBuffers, rebase_on_tensors
 from .verify import VerifyReport, report_from_stats
 
@@ -41,6 +41,8 @@ class CompiledPlan:
     reference_comm_bytes: int = 0   # the reference's per-rank cross-rank volume, max over ranks
     src_buf_bytes: Tuple[int, ...] = ()   # arena sizes the plan was checked against
     dst_buf_bytes: Tuple[int, ...] = ()
+    src_refs: Tuple[int, ...] = (0, 1, 2, 3)   # arenas the plan reads
+    dst_refs: Tuple[int, ...] = (0, 1, 2, 3)   # arenas the plan writes
 
     @property
     def traffic_bytes(self) -> int:
@@ -59,6 +61,26 @@ def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
         if all(space.spec.padded_vocab_size % t == 0 for t in tps):
             return space
     return None
+
+
+def _arena_refs(table: np.ndarray) -> Tuple[Tuple[int, ...], Tuple[int, ...]]:
+    """(source arenas read, destination arenas written) by a segment table."""
+    reads = (table["flags"] & SEG_ZERO_FILL) == 0
+    second = (table["flags"] & (SEG_CAST_BF16 | SEG_DUP)) != 0
+    src = sorted(set(table["src_buf"][reads].tolist()))
+    dst = sorted(set(table["dst_buf"].tolist()) | set(table["aux_buf"][second].tolist()))
+    return tuple(int(x) for x in src), tuple(int(x) for x in dst)
+
+
+def _stage_mask(table: np.ndarray, kind: int) -> np.ndarray:
+    """Rows of stage ``kind`` of a staged switch: those writing fp32 arena ``kind``, and with the
+    first stage the bf16 param rows (the bf16 image rides on the main rows)."""
+    d = table["dst_buf"]
+    return ((d == kind) | (d == ARENA_PARAM)) if kind == 0 else (d == kind)
+
+
+def _stage_rows(table: np.ndarray, kind: int) -> np.ndarray:
+    return table[_stage_mask(table, kind)]
 
 
 @dataclass
@@ -135,9 +157,35 @@ class TransferManager:
         else:  # param_migrate is a local copy (training_state.py:40-60)
             comm = 0
         cp = CompiledPlan(table, _native.Plan(table, sb, db, self.check_disjoint), payload_bytes(table),
-                          read_bytes(table), src.strategy, dst.strategy, comm, tuple(sb), tuple(db))
+                          read_bytes(table), src.strategy, dst.strategy, comm, tuple(sb), tuple(db),
+                          *_arena_refs(table))
         self._plans[key] = cp
         return cp
+
+    def compile_staged(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
+                       include_bf16: bool = True) -> Tuple[CompiledPlan, CompiledPlan, CompiledPlan]:
+        """The switch as three launches, one per optimizer kind: ``main`` (with the bf16 params),
+        ``exp_avg``, ``exp_avg_sq``.  Stage k reads source arena k only and writes destination arena
+        k only (and the param arena), so a caller can allocate each destination arena just before its
+        stage and release the source arena right after it, as the reference releases every
+        optimizer tensor once it is sent (transfer.py:182-228, resharding_metadata.py:58-65).  The
+        three together write exactly what :meth:`compile` writes."""
+        key = ("staged", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
+               self.bf16_source)
+        stages = self._plans.get(key)
+        if stages is not None:
+            return stages
+        full = self.compile(src, dst, kind, include_bf16)
+        out = []
+        for k in range(3):
+            t = _stage_rows(full.segments, k)
+            out.append(CompiledPlan(t, _native.Plan(t, full.src_buf_bytes, full.dst_buf_bytes, self.check_disjoint),
+                                    payload_bytes(t), read_bytes(t), full.src, full.dst,
+                                    full.reference_comm_bytes if k == 0 else 0, full.src_buf_bytes,
+                                    full.dst_buf_bytes, *_arena_refs(t)))
+        stages = tuple(out)
+        self._plans[key] = stages
+        return stages
 
     def compile_tensors(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                         include_bf16: bool = True) -> CompiledTensorPlan:
@@ -188,11 +236,15 @@ class TransferManager:
         if src.device.type != "cuda":
             raise RuntimeError("training states must live in GPU memory: the reshard has no CPU path")
         # The kernel trusts the sizes the plan was built for; a state laid out for another model
-        # (another padded vocabulary, say) must not reach it.
-        for have, need in zip(src.arena_bytes() + dst.arena_bytes(), plan.src_buf_bytes + plan.dst_buf_bytes):
-            if need and have < need:
-                raise ValueError("a training state's arena is smaller than the plan's buffer: "
-                                 "it was laid out for another model")
+        # (another padded vocabulary, say) must not reach it.  Arenas the plan does not touch may
+        # be empty (a staged switch allocates and releases them one at a time).
+        have = src.arena_bytes(), dst.arena_bytes()
+        need = plan.src_buf_bytes, plan.dst_buf_bytes
+        for side, refs in enumerate((plan.src_refs, plan.dst_refs)):
+            for a in refs:
+                if need[side] and have[side][a] < need[side][a]:
+                    raise ValueError("a training state's arena is smaller than the plan's buffer: it is "
+                                     "released, not yet allocated, or laid out for another model")
         st = stream if stream is not None else torch.cuda.current_stream(src.device)
         with torch.cuda.device(src.device):
             plan.native.execute(src.arena_ptrs(), dst.arena_ptrs(), st.cuda_stream)
@@ -208,10 +260,19 @@ class TransferManager:
         bits that differ and compare_ckpt's max-abs / max-rel / RMS / relative
         RMS.  ``src`` must still hold the state it was resharded from.
         """
+        stats, names = self.verify_stats(src, dst, kind, include_bf16, stream)
+        return report_from_stats(stats, names)
+
+    def verify_stats(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
+                     include_bf16: bool = True, stream: Optional[torch.cuda.Stream] = None,
+                     stage: Optional[int] = None):
+        """The records behind :meth:`verify` and the parameter names they index; with ``stage`` only
+        what stage ``stage`` of :meth:`compile_staged` writes, so that a staged switch can check each
+        stage before it releases that stage's source arena (:func:`.verify.merge_stats` adds them)."""
         if src.device.type != "cuda" or dst.device.type != "cuda":
             raise RuntimeError("training states must live in GPU memory: verification has no CPU path")
         sl, dl = src.layout, dst.layout
-        key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source)
+        key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source, stage)
         vp = self._verify_plans.get(key)
         if vp is None:
             if kind == "transfer":
@@ -222,6 +283,9 @@ class TransferManager:
                                                                    with_groups=True)
             else:
                 raise ValueError(kind)
+            if stage is not None:
+                m = _stage_mask(table, stage)
+                table, groups, aux_groups = table[m], groups[m], aux_groups[m]
             sb = [sl.fp32_numel * 4] * 3 + [sl.bf16_numel * 2]
             db = [dl.fp32_numel * 4] * 3 + [dl.bf16_numel * 2]
             names = [p.name for p in dl.space.all_virtual_params]
@@ -232,7 +296,7 @@ class TransferManager:
         with torch.cuda.device(src.device):
             stats = plan.compare(src.arena_ptrs(), dst.arena_ptrs(), groups, aux_groups, 4 * len(names),
                                  st.cuda_stream)
-        return report_from_stats(stats, names)
+        return stats, names
 
     def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
                                    dst: Optional[TrainingState] = None, include_bf16: bool = True,

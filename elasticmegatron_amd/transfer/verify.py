@@ -85,6 +85,19 @@ class VerifyReport:
         return out
 
 
+def merge_stats(a: Optional[np.ndarray], b: np.ndarray) -> np.ndarray:
+    """emrs_plan_compare records of two disjoint parts of one destination, combined: counts and sums
+    add, maxima take the larger."""
+    if a is None:
+        return b.copy()
+    out = a.copy()
+    for f in ("elements", "mismatches", "nonfinite", "sum_sq_diff", "sum_sq_expected"):
+        out[f] = a[f] + b[f]
+    for f in ("max_abs_diff", "max_rel_diff"):
+        out[f] = np.maximum(a[f], b[f])
+    return out
+
+
 def report_from_stats(stats: np.ndarray, names: List[str]) -> VerifyReport:
     """Build the report from emrs_plan_compare records indexed by ``4 * parameter index + kind``."""
     tensors = {}
