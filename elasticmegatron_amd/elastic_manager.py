@@ -124,10 +124,15 @@ class ElasticMegatronManager:
         space = src.layout.space
         if space is dst.layout.space:
             space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
-        space.src_state, space.dst_state = src, dst
         plan = self.transfer_manager.compile(src.layout, dst.layout)
-        with Timer() as t:
-            self.transfer_manager.execute(plan, src, dst)
+        # The states are the space's for the duration of the transfer only: the space outlives the
+        # switch, and holding them would keep a released state's memory alive.
+        space.src_state, space.dst_state = src, dst
+        try:
+            with Timer() as t:
+                self.transfer_manager.transfer_optimizer_tensors(space)
+        finally:
+            space.src_state = space.dst_state = None
         return t.elapsed
 
     def transfer_staged(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
@@ -139,11 +144,8 @@ class ElasticMegatronManager:
         it has been checked when ``verify`` is set.  Returns (executor ms summed over the stages,
         verification records or None).
         """
-        if kind == "transfer":
-            space = src.layout.space
-            if space is dst.layout.space:
-                space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
-            space.src_state, space.dst_state = src, dst
+        if kind == "transfer" and src.layout.space is dst.layout.space:
+            src.layout.space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
         stages = self.transfer_manager.compile_staged(src.layout, dst.layout, kind)
         elapsed, stats, names = 0.0, None, None
         self.last_stage_ms = []

@@ -137,6 +137,10 @@ class VirtualParamSpace:
         self._stages: Dict[int, List[List[VirtualParam]]] = {}
         self._built: set = set()
         self._layouts: Dict[ParallelStrategy, "object"] = {}
+        # The training states of a transfer in progress, read by
+        # TransferManager.transfer_optimizer_tensors(space); None between transfers.
+        self.src_state = None
+        self.dst_state = None
 
     @property
     def tied_embeddings(self) -> bool:

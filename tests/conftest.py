@@ -22,3 +22,18 @@ def gpu_device():
 
     _native.load()  # the native path must be present: no fallback
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _free_device_memory(request):
+    """Before each GPU test, free what earlier tests left: full-size states are hundreds of GB."""
+    if "gpu_device" in request.fixturenames:
+        import gc
+
+        import torch
+
+        gc.collect()
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+    yield

@@ -197,3 +197,19 @@ def test_non_power_of_two_tp_is_refused_on_every_path(repad, padded, vocab):
     with pytest.raises(AssertionError, match="powers of two"):
         mgr.reshard(dict(world_size=6, tensor_model_parallel_size=3, pipeline_model_parallel_size=1),
                     is_meta_device=True)
+
+
+@pytest.mark.gpu
+def test_space_does_not_keep_states_alive(gpu_device):
+    """The virtual model outlives a switch; it must not hold the states of the last transfer."""
+    import weakref
+
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device=gpu_device)
+    old = weakref.ref(mgr.training_state)
+    mgr.reshard(SEQ[1])
+    space = mgr.virtual_param_space
+    assert space.src_state is None and space.dst_state is None
+    import gc
+
+    gc.collect()
+    assert old() is None
