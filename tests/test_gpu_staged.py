@@ -59,6 +59,8 @@ def test_llama2_13b_switch_fits_in_one_gpu(gpu_device):
     peak_bound = state + ld.bf16_numel * 2 + ld.fp32_numel * 4 + 4 * (1 << 30)
     print(f"case staged llama2-13b: state {state / 1e9:.1f} GB, bound {peak_bound / 1e9:.1f} GB, "
           f"device {total / 1e9:.1f} GB", flush=True)
+    if peak_bound > 0.95 * total:
+        pytest.skip("the device is too small even for the staged switch")
     assert state + 3 * ld.fp32_numel * 4 + ld.bf16_numel * 2 > total   # the unstaged switch cannot fit
     try:
         mgr.training_state.fill_synthetic(SEED)
