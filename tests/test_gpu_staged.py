@@ -17,6 +17,7 @@ import torch
 from elasticmegatron_amd import ElasticMegatronManager
 from elasticmegatron_amd import ParallelStrategy as PS
 from elasticmegatron_amd.resharding import model_spec as ms
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from tests.helpers import SEED, small_llama2, small_llama3
 
 pytestmark = pytest.mark.gpu
@@ -51,17 +52,20 @@ def test_llama2_13b_switch_fits_in_one_gpu(gpu_device):
     total = torch.cuda.get_device_properties(gpu_device).total_memory
     spec = ms.llama2_13b()
     src, dst = PS(8, 1, 1), PS(8, 4, 1)
-    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device, low_memory=True)
-    ls, ld = mgr.space_for(src).layout(src), mgr.space_for(dst).layout(dst)
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
     state = 3 * ls.fp32_numel * 4 + ls.bf16_numel * 2
     # Source state, destination bf16 params and one destination fp32 arena; each of the four fp32
     # arenas alive at once is rounded up to a 1 GiB granule.
     peak_bound = state + ld.bf16_numel * 2 + ld.fp32_numel * 4 + 4 * (1 << 30)
+    both = state + 3 * ld.fp32_numel * 4 + ld.bf16_numel * 2
     print(f"case staged llama2-13b: state {state / 1e9:.1f} GB, bound {peak_bound / 1e9:.1f} GB, "
           f"device {total / 1e9:.1f} GB", flush=True)
     if peak_bound > 0.95 * total:
         pytest.skip("the device is too small even for the staged switch")
-    assert state + 3 * ld.fp32_numel * 4 + ld.bf16_numel * 2 > total   # the unstaged switch cannot fit
+    del space, ls, ld
+    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device, low_memory=True)
+    assert both > total   # the unstaged switch cannot fit
     try:
         mgr.training_state.fill_synthetic(SEED)
         torch.cuda.synchronize()
