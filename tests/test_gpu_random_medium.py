@@ -11,7 +11,6 @@ import numpy as np
 import pytest
 import torch
 
-from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
 from elasticmegatron_amd.megatron_manager.training_state import TrainingState
 from elasticmegatron_amd.resharding import model_spec as ms
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
