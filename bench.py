@@ -238,15 +238,7 @@ def main():
     gbps = payload / (ms / 1e3) / 1e9
     traffic_gbps = plan.traffic_bytes / (ms / 1e3) / 1e9
 
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"{args.workload}.traffic.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            rec = json.load(f)
-        same_source = rec.get("bf16_source", "cast") == (tm.bf16_source if backup is None else None) or backup is not None
-        # Counters measured on another plan (a different lowering of this workload) do not apply.
-        if same_source and rec.get("algorithmic_bytes_per_launch") == plan.traffic_bytes:
-            traffic = rec.get("hbm_bytes_per_launch")
+    traffic = committed_traffic(args.workload, tm.bf16_source if backup is None else None, plan.traffic_bytes)
 
     out = {
         "metric": METRIC,
@@ -320,6 +312,20 @@ def main():
         out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup, full_payload=payload)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def committed_traffic(workload: str, bf16_source, algorithmic_bytes: int):
+    """HBM bytes per launch from the committed PMC summary of ``workload`` (profiles/), or None when
+    there is none for this bf16 source (None: fp32-only Group-ZeRO plans) or it was measured on a
+    plan with other algorithmic bytes."""
+    tf = os.path.join(ROOT, "profiles", f"{workload}.traffic.json")
+    if not os.path.exists(tf):
+        return None
+    with open(tf) as f:
+        rec = json.load(f)
+    if rec.get("bf16_source", "cast") != bf16_source or rec.get("algorithmic_bytes_per_launch") != algorithmic_bytes:
+        return None
+    return rec.get("hbm_bytes_per_launch")
 
 
 def bench_low_memory(args, desc, spec_fn, src, dst, dev):

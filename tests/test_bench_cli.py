@@ -1,0 +1,71 @@
+"""bench.py on the CPU: the parts of its contract that need no GPU."""
+
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy  # noqa: E402
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model  # noqa: E402
+from elasticmegatron_amd.transfer.transfer import TransferManager  # noqa: E402
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                          timeout=300)
+
+
+def test_more_than_one_gpu_is_refused_with_a_reason():
+    r = _run("--gpus", "2")
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="checks the behaviour without a GPU")
+def test_without_a_gpu_it_says_so():
+    r = _run("--steps", "1", "--warmup", "0")
+    assert r.returncode == 1 and "needs a GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.parametrize("name", sorted(bench.workloads()))
+def test_every_workload_lays_out(name):
+    desc, spec_fn, src, dst, *opt = bench.workloads()[name]
+    spec = spec_fn()
+    if opt and opt[0]:   # re-padded: one model space per padded vocabulary
+        spec_src = spec.with_padded_vocab(spec.padded_vocab_for_tp(src.tensor_model_parallel_size))
+        spec_dst = spec.with_padded_vocab(spec.padded_vocab_for_tp(dst.tensor_model_parallel_size))
+        ls, ld = build_virtual_model(spec_src).layout(src), build_virtual_model(spec_dst).layout(dst)
+    else:
+        space = build_virtual_model(spec)
+        ls, ld = space.layout(src), space.layout(dst)
+    assert ls.fp32_numel > 0 and ld.fp32_numel > 0 and desc
+
+
+@pytest.mark.parametrize("traffic_file", sorted(f for f in os.listdir(os.path.join(ROOT, "profiles"))
+                                                if f.endswith(".traffic.json")))
+def test_committed_traffic_describes_the_current_plan(traffic_file):
+    """Each committed PMC summary was measured on the plan its workload lowers to today (same
+    algorithmic bytes), so bench.py quotes it; a stale one would be ignored, and this fails first."""
+    name = traffic_file[:-len(".traffic.json")]
+    desc, spec_fn, src, dst, *opt = bench.workloads()[name]
+    spec = spec_fn()
+    backup = ParallelStrategy.is_redundant_backup(src, dst)
+    if opt and opt[0]:
+        ls = build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(src.tensor_model_parallel_size))).layout(src)
+        ld = build_virtual_model(spec.with_padded_vocab(spec.padded_vocab_for_tp(dst.tensor_model_parallel_size))).layout(dst)
+    else:
+        space = build_virtual_model(spec)
+        ls, ld = space.layout(src), space.layout(dst)
+    kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+    plan = TransferManager().compile(ls, ld, kind)
+    with open(os.path.join(ROOT, "profiles", traffic_file)) as f:
+        rec = json.load(f)
+    assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes) == \
+        rec["hbm_bytes_per_launch"]
+    assert abs(rec["hbm_bytes_per_launch"] / plan.traffic_bytes - 1) < 1e-3   # within 0.1% of the algorithmic bytes
+    assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes + 1) is None
