@@ -1,14 +1,20 @@
-"""Full-size switches on one GPU, checked through size-independent properties.
+"""Full-size switches on one GPU.
 
-At these sizes the CPU oracle cannot run, so every destination element is
-checked on the device against the seeded generator (its expected value is a
-closed form of (parameter, kind, full-tensor index)), and the switch back to
-the source layout must reproduce the source exactly (round trip = identity).
-Peak memory is two layouts' worth of state.
+Every destination element is checked on the device against the seeded
+generator (its expected value is a closed form of (parameter, kind,
+full-tensor index)), the plan's own verification compares the destination
+with the source, and the switch back to the source layout must reproduce the
+source exactly (round trip = identity).  The CPU oracle cannot run a whole
+model at these sizes, but it runs one layer: for the transfer switches,
+Oracle-1 (the reference's three-pass executor, transfer.py:36-341, restated
+on CPU tensors) runs the parameters of the last transformer layer, about
+250M elements, and the GPU result must equal it bit for bit.  Peak memory is
+two layouts' worth of state.
 """
 
 import gc
 
+import numpy as np
 import pytest
 import torch
 
@@ -37,6 +43,43 @@ def _release():
     gc.collect()
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+
+
+def _check_layer_against_oracle1(spec, src, dst, layout, state, budget=250_000_000):
+    """Oracle-1 on the last transformer layer's parameters (in order, up to ``budget`` elements), and
+    the same pieces of the device state copied back, compared bit for bit."""
+    from oracle import model
+    from oracle import transfer as oracle1
+    from oracle.plan import Strat
+    from tests.helpers import compare
+
+    inv = model.inventory(spec)
+    last = spec.num_layers - 1
+    params, total = set(), 0
+    for p in inv:
+        if p["layer"] == last and (not params or total + model.numel(p["shape"]) <= budget):
+            params.add(p["id"])
+            total += model.numel(p["shape"])
+    S, D = Strat.of(src), Strat.of(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED, params)
+    dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
+    want32 = oracle1.flatten(dw)
+    got32, gotbf = {}, {}
+    space = layout.space
+    for pid in params:
+        vp = space.all_virtual_params[pid]
+        for h in layout.fp32_holders(vp):
+            n = h.hi - h.lo
+            got32[(h.rank, pid)] = {k: t[h.offset:h.offset + n].cpu().numpy()
+                                    for k, t in zip(("main", "exp_avg", "exp_avg_sq"),
+                                                    (state.main, state.exp_avg, state.exp_avg_sq))}
+        for h in layout.bf16_holders(vp):
+            n = h.hi - h.lo
+            gotbf[(layout.shard_keys[h.rank], pid)] = \
+                state.param[h.offset:h.offset + n].view(torch.int16).cpu().numpy().view(np.uint16)
+    print(f"oracle-1 on layer {last}: {len(params)} params, {total} elements", flush=True)
+    assert got32 and gotbf
+    assert compare(got32, gotbf, want32, dbf) == []
 
 
 @pytest.mark.parametrize("factory,src,dst,repad", [p if len(p.values) == 4 else
@@ -68,6 +111,8 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
         assert bad == 0, first
         report = tm.verify(a, b, kind)  # the plan's own check, against the source state
         assert report.bit_exact, report.lines()[:5]
+        if kind == "transfer" and not repad:  # the reference keeps the padded vocabulary fixed
+            _check_layer_against_oracle1(spec, src, dst, ld, b)
         # Round trip into fresh storage: must reproduce every source element.
         param = a.param
         del a
