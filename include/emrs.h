@@ -148,7 +148,12 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
  * be 16-byte aligned (EMRS_ERR_MISALIGNED) and must not overlap a referenced
  * buffer of the other side or another referenced destination buffer
  * (EMRS_ERR_ALIAS): the copy is out of place.  Unreferenced buffers are not
- * checked and may be NULL.  Replaces one call of TransferManager.transfer_optimizer_tensors
+ * checked and may be NULL.  The first call on a device uploads the plan's
+ * table (and, beyond 128 buffers a side, its pointer table for these bases)
+ * synchronously; later calls with the same bases enqueue one kernel launch
+ * and nothing else, so they may be captured into a HIP graph.  Calls with
+ * other bases than the first beyond 128 buffers allocate a stream-ordered
+ * pointer table.  Replaces one call of TransferManager.transfer_optimizer_tensors
  * (transfer.py:291-341) together with the bf16 rebuild of
  * TrainingState.update_model_weight (training_state.py:176-197).
  */
