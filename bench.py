@@ -80,10 +80,13 @@ def parse():
                     help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
-    ap.add_argument("--blocks-per-cu", type=int, default=0, help="0: as many as can be resident")
+    ap.add_argument("--persistent", type=int, default=0,
+                    help="0: one workgroup per chunk of 256 units; 1: persistent grid (the next three flags)")
+    ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
     ap.add_argument("--nontemporal", type=int, default=1)
-    ap.add_argument("--xcd-remap", type=int, default=1)
-    ap.add_argument("--run", type=int, default=4, help="0: contiguous chunk run per workgroup; N: round-robin runs of N")
+    ap.add_argument("--xcd-remap", type=int, default=1, help="persistent grid")
+    ap.add_argument("--run", type=int, default=4,
+                    help="persistent grid; 0: contiguous chunk run per workgroup; N: round-robin runs of 8N chunks")
     ap.add_argument("--low-memory", action="store_true",
                     help="time staged switches through ElasticMegatronManager(low_memory=True), alternating "
                          "directions: one optimizer kind per launch, arenas allocated and released as it goes")
@@ -165,7 +168,8 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _native.load()
-    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run)
+    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run,
+                       bool(args.persistent))
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:

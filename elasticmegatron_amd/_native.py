@@ -63,7 +63,8 @@ class PlanStats(ctypes.Structure):
 
 class Tuning(ctypes.Structure):
     _fields_ = [("blocks_per_cu", ctypes.c_uint32), ("nontemporal", ctypes.c_uint32),
-                ("xcd_remap", ctypes.c_uint32), ("run", ctypes.c_uint32)]
+                ("xcd_remap", ctypes.c_uint32), ("run", ctypes.c_uint32), ("persistent", ctypes.c_uint32),
+                ("lanes", ctypes.c_uint32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -104,7 +105,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
     lib.emrs_xor_checksum.restype = I
     lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
-    if lib.emrs_abi_version() != 3:
+    if lib.emrs_abi_version() != 4:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib
@@ -139,8 +140,12 @@ def get_tuning() -> Tuning:
     return t
 
 
-def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True, run: int = 4) -> None:
-    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run)
+def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True, run: int = 4,
+               persistent: bool = False, lanes: int = 0) -> None:
+    """Launch shape of every later execution.  The default runs one workgroup of ``lanes`` lanes
+    (0: 64) per chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu``,
+    ``xcd_remap`` and ``run`` shape."""
+    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run, 1 if persistent else 0, lanes)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 
 

@@ -1,14 +1,17 @@
 // Copy-plan executor for the reshard repack on MI355X (gfx950, CDNA4).
 //
 // One launch moves every segment of a plan.  The path is pure data movement
-// (no arithmetic), so the kernel is shaped for HBM streaming: 16-byte vector
-// loads and stores, eight of them in flight per lane before the first store,
-// and a persistent grid that deals fixed-size chunks out to its workgroups in
-// short round-robin runs (each XCD sweeping its own eighth of the plan), with
-// one binary search per run for its first segment followed by a forward walk.
-// Element sizes are irrelevant to the vector path: offsets are converted to
-// 16-byte units when the plan is created, so bf16 parameters and fp32
-// optimizer state share one launch.
+// (no arithmetic), so the kernel is shaped for HBM streaming: the plan is cut
+// into chunks of 256 units (4 KB of 16-byte units), and every chunk is a
+// workgroup of its own, one wave of 64 lanes with four units each, that finds
+// its segment by one binary search, issues its four loads, stores and exits.
+// The hardware dispatches workgroups in order, so the in-flight ones always
+// cover one narrow window of the plan that sweeps through memory; a
+// persistent grid, whose workgroups drift apart, writes up to 20% slower on
+// most physical placements of the same buffers.  The persistent grid remains
+// as a tuning option.  Element sizes are irrelevant to the vector path:
+// offsets are converted to 16-byte units when the plan is created, so bf16
+// parameters and fp32 optimizer state share one launch.
 //
 // The reference performs the same movement as per-parameter slicing plus
 // point-to-point messages (elastic_megatron/transfer/transfer.py:36-101,
@@ -54,11 +57,14 @@ int hip_fail(hipError_t e, const char *what) {
 #define EMRS_COPY_THREADS 256  // lanes per workgroup
 #endif
 #ifndef EMRS_COPY_UNROLL
-#define EMRS_COPY_UNROLL 8  // 16-byte loads in flight per lane
+#define EMRS_COPY_UNROLL 8  // chunks of one segment per step of the persistent and compare kernels
 #endif
 constexpr int kThreads = EMRS_COPY_THREADS;
 constexpr int kUnroll = EMRS_COPY_UNROLL;
-constexpr uint32_t kChunkUnits = kThreads * kUnroll;  // units per work chunk
+constexpr uint32_t kChunkUnits = kThreads;  // units per work chunk: one per lane
+constexpr uint32_t kStepUnits = kThreads * kUnroll;  // units per step of a persistent workgroup
+constexpr uint64_t kMaxGridY = 65535;                     // rows of a one-workgroup-per-chunk grid
+constexpr uint64_t kMaxGridX = 0xffffffffull / kThreads;  // a grid dimension holds fewer than 2^32 lanes
 constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 bits
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -127,10 +133,12 @@ __host__ __device__ __forceinline__ uint32_t magic_div(uint32_t n, uint32_t m, u
 }
 
 struct Tuning {
-  std::atomic<uint32_t> blocks_per_cu{0};  // 0: as many as can be resident
+  std::atomic<uint32_t> blocks_per_cu{0};  // persistent grid: 0 = as many as can be resident
   std::atomic<uint32_t> nontemporal{1};
-  std::atomic<uint32_t> xcd_remap{1};
-  std::atomic<uint32_t> run{4};  // round-robin runs of 4 chunks
+  std::atomic<uint32_t> xcd_remap{1};      // persistent grid
+  std::atomic<uint32_t> run{4};            // persistent grid: round-robin runs of 4 x kUnroll chunks
+  std::atomic<uint32_t> persistent{0};     // 0: one workgroup per chunk
+  std::atomic<uint32_t> lanes{64};         // lanes per workgroup of one chunk: 64, 128 or 256
 };
 Tuning g_tuning;
 
@@ -174,7 +182,7 @@ struct CastOf<uint32_t> {
   __device__ static type cast(uint32_t v) { return (uint16_t)bf16_rne(v); }
 };
 
-// Copy units [u0, u_end) of segment s, 0 < u_end - u0 <= kChunkUnits; with
+// Copy units [u0, u_end) of segment s, 0 < u_end - u0 <= kStepUnits; with
 // kCast also store each unit's bf16 image to aux.  In a partial chunk, lanes
 // past the end load the last unit again (in bounds) so that every load is
 // unconditional; only their stores are masked off.
@@ -199,7 +207,7 @@ __device__ __forceinline__ void copy_chunk(const DevSeg &s, const char *sbase, c
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j) v[j] = T{};
     }
-    if (n == kChunkUnits) {
+    if (n == kStepUnits) {
 #pragma unroll
       for (int j = 0; j < kUnroll; ++j)
         if constexpr (!kZero) v[j] = ld<T, kNT>(sp + j * kThreads + tid);
@@ -264,7 +272,8 @@ __device__ __forceinline__ char *base_of(const Bases &b, const uint64_t *tab, ui
   else return b.p[i];
 }
 
-// Copy chunks [c, c_end), starting from the segment that contains chunk c.
+// Copy chunks [c, c_end), starting from the segment that contains chunk c
+// (persistent grid).
 template <bool kNT, bool kTable>
 __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
                                                uint64_t c, uint64_t c_end, const Bases &src, const Bases &dst,
@@ -280,15 +289,17 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
   DevSeg s = segs[si];
   uint64_t s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
 
-  for (; c < c_end; ++c) {
+  for (uint64_t nq; c < c_end; c += nq) {
     while (c >= s_end) {
       ++si;
       s = segs[si];
       s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
     }
+    // Up to kUnroll chunks of this segment in one step.
+    nq = min(min(c_end, s_end) - c, (uint64_t)kUnroll);
     const uint32_t total = s.len * s.rows;
     const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
-    const uint32_t u_end = min(u0 + kChunkUnits, total);
+    const uint32_t u_end = min(u0 + (uint32_t)nq * kChunkUnits, total);
     const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
     char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
     char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
@@ -316,15 +327,15 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
   }
 }
 
-// Persistent grid.  With run == 0 every workgroup takes one contiguous run of
-// chunks_per_block chunks (xcd_stride != 0: each XCD's workgroups cover one
-// contiguous slice).  With run > 0 the chunks are dealt out round-robin in
-// runs of `run` chunks, so the workgroups sweep the plan together; with
-// xcd_stride != 0 as well (the grid is then a multiple of 8, and workgroup b
-// runs on XCD b % 8), each XCD sweeps its own contiguous eighth, so that no
-// page is touched from two XCDs' translation caches.
+// Persistent grid (a tuning option).  With run == 0 every workgroup takes one
+// contiguous run of chunks_per_block chunks (xcd_stride != 0: each XCD's
+// workgroups cover one contiguous slice).  With run > 0 the chunks are dealt
+// out round-robin in runs of `run` chunks, so the workgroups sweep the plan
+// together; with xcd_stride != 0 as well (the grid is then a multiple of 8,
+// and workgroup b runs on XCD b % 8), each XCD sweeps its own contiguous
+// eighth, so that no page is touched from two XCDs' translation caches.
 template <bool kNT, bool kTable>
-__global__ __launch_bounds__(kThreads) void copy_plan_kernel(
+__global__ __launch_bounds__(kThreads) void copy_plan_persistent_kernel(
     const DevSeg *__restrict__ segs, uint32_t n_segs, uint64_t n_chunks,
     uint64_t chunks_per_block, uint32_t xcd_stride, uint32_t run, Bases src, Bases dst,
     const uint64_t *__restrict__ src_tab, const uint64_t *__restrict__ dst_tab) {
@@ -349,22 +360,127 @@ __global__ __launch_bounds__(kThreads) void copy_plan_kernel(
                               dst_tab);
 }
 
+// Chunk [u0, u0 + kChunkUnits) of segment s (clipped to its `total` units) by
+// a workgroup of L lanes, kChunkUnits / L units per lane: every load is issued
+// before the first store.
+template <typename T, bool kNT, bool kCast, bool kZero, bool kDup, int L>
+__device__ __forceinline__ void copy_units(const DevSeg &s, const char *sbase, char *dbase, char *abase, uint32_t u0,
+                                           uint32_t total) {
+  typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
+  constexpr int U = kChunkUnits / L;
+  const T *src = reinterpret_cast<const T *>(sbase);
+  T *dst = reinterpret_cast<T *>(dbase);
+  A *aux = reinterpret_cast<A *>(abase);
+  T *dup = reinterpret_cast<T *>(abase);
+  T v[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * L + threadIdx.x;
+    v[j] = T{};
+    if constexpr (!kZero) {
+      uint64_t so = s.src_off + u;
+      if (s.rows > 1) {
+        const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2());
+        so = s.src_off + (uint64_t)row * s.src_stride + (u - row * s.len);
+      }
+      if (u < total) v[j] = ld<T, kNT>(src + so);
+    }
+  }
+  // Destination offsets are recomputed rather than kept from the loads:
+  // fewer registers, so that eight waves fit on each SIMD.
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * L + threadIdx.x;
+    if (u < total) {
+      uint64_t dof = s.dst_off + u, ao = s.aux_off + u;
+      if (s.rows > 1) {
+        const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2()), col = u - row * s.len;
+        dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
+        ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
+      }
+      st<T, kNT>(dst + dof, v[j]);
+      if constexpr (kCast) st<A, kNT>(aux + ao, C::cast(v[j]));
+      if constexpr (kDup) st<T, kNT>(dup + ao, v[j]);
+    }
+  }
+}
+
+template <bool kNT, bool kZero, bool kDup, int L>
+__device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, const char *sb, char *db, char *ab,
+                                               uint32_t u0, uint32_t total) {
+  switch (ul) {
+    case 4: copy_units<u32x4, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+    case 3: copy_units<uint64_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+    case 2: copy_units<uint32_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+    case 1: copy_units<uint16_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+    default: copy_units<uint8_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+  }
+}
+
+// One workgroup of L lanes per chunk (the default schedule).  The grid is
+// two-dimensional (chunk = blockIdx.y * gridDim.x + blockIdx.x) because one
+// dimension holds fewer than 2^32 lanes; workgroups past the last chunk exit
+// at once.  The segment search depends on the chunk alone, so it runs on the
+// scalar unit, once per wave, and the upper levels of the search stay in the
+// scalar cache for every workgroup in flight.  With L = 64 (the default) a
+// chunk is one wave: one search per 4 KB, four loads in flight per lane.
+// With 256 lanes four waves repeat the same search for one 16-byte load each,
+// and the launch runs about 20% slower.
+template <bool kNT, bool kTable, int L>
+__global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint32_t n_segs,
+                                                      uint64_t n_chunks, Bases src, Bases dst,
+                                                      const uint64_t *__restrict__ src_tab,
+                                                      const uint64_t *__restrict__ dst_tab) {
+  const uint64_t c = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  if (c >= n_chunks) return;
+  uint32_t lo = 0, hi = n_segs - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (segs[mid].chunk_begin <= c) lo = mid;
+    else hi = mid - 1;
+  }
+  const DevSeg s = segs[lo];
+  const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits, total = s.len * s.rows;
+  const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
+  char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
+  char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+  const uint32_t ops = s.ops(), ul = s.unit_log2();
+  if (ops & 4) {  // duplicate to aux, with or without zero fill
+    if (ops & 2) dispatch_chunk<kNT, true, true, L>(ul, s, sb, db, ab, u0, total);
+    else dispatch_chunk<kNT, false, true, L>(ul, s, sb, db, ab, u0, total);
+  } else if (ops & 1) {  // with the bf16 image (fp32 only: 16- or 4-byte units), with or without zero fill
+    if (ops & 2) {
+      if (ul == 4) copy_units<u32x4, kNT, true, true, false, L>(s, sb, db, ab, u0, total);
+      else copy_units<uint32_t, kNT, true, true, false, L>(s, sb, db, ab, u0, total);
+    } else {
+      if (ul == 4) copy_units<u32x4, kNT, true, false, false, L>(s, sb, db, ab, u0, total);
+      else copy_units<uint32_t, kNT, true, false, false, L>(s, sb, db, ab, u0, total);
+    }
+  } else if (ops & 2) {
+    dispatch_chunk<kNT, true, false, L>(ul, s, sb, db, ab, u0, total);
+  } else {
+    dispatch_chunk<kNT, false, false, L>(ul, s, sb, db, ab, u0, total);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Device bookkeeping
 // ---------------------------------------------------------------------------
 
 struct DeviceProps {
   int cus = 0;
-  int resident_blocks[2] = {0, 0};  // copy_plan_kernel<false/true> blocks per CU
+  int resident_blocks[2] = {0, 0};  // copy_plan_persistent_kernel<false/true> blocks per CU
 };
 
 std::mutex g_dev_mu;
 std::vector<DeviceProps> g_dev_props;
 
 template <bool kNT>
-void copy_plan_kernel_occupancy(int *out) {
+void persistent_occupancy(int *out) {
   int v = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, copy_plan_kernel<kNT, false>, kThreads, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, copy_plan_persistent_kernel<kNT, false>, kThreads, 0) !=
+          hipSuccess ||
       v <= 0) {
     (void)hipGetLastError();
     v = 4;
@@ -388,8 +504,8 @@ int current_device(int *dev, int *cus, int *resident_nt, int *resident_t) {
     e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, *dev);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
     g_dev_props[*dev].cus = v > 0 ? v : 1;
-    copy_plan_kernel_occupancy<false>(&g_dev_props[*dev].resident_blocks[0]);
-    copy_plan_kernel_occupancy<true>(&g_dev_props[*dev].resident_blocks[1]);
+    persistent_occupancy<false>(&g_dev_props[*dev].resident_blocks[0]);
+    persistent_occupancy<true>(&g_dev_props[*dev].resident_blocks[1]);
   }
   *cus = g_dev_props[*dev].cus;
   *resident_t = g_dev_props[*dev].resident_blocks[0];
@@ -765,8 +881,8 @@ __device__ __forceinline__ void aux_words_of(const A &v, uint32_t *w) {
   }
 }
 
-// Compare units [u0, u_end) of segment s; with a cast, also its bf16 image;
-// with a duplicate, also the second copy.
+// Compare units [u0, u_end) of segment s (at most kStepUnits); with a cast,
+// also its bf16 image; with a duplicate, also the second copy.
 template <typename T>
 __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase, const char *dbase,
                                               const char *abase, uint32_t u0, uint32_t u_end, LaneAcc &m,
@@ -868,7 +984,8 @@ __device__ void flush_block(LaneAcc &m, LaneAcc &x, uint32_t g, uint32_t ga, boo
 
 // Workgroups take runs of `run` consecutive chunks, each XCD sweeping its own
 // eighth of the plan (workgroup b runs on XCD b % 8; the grid is a multiple of
-// 8), as the copy kernel does.  Lane sums stay in registers while consecutive
+// 8), and compare up to kUnroll chunks of one segment per step, so that every
+// lane has several loads in flight.  Lane sums stay in registers while consecutive
 // chunks share their (group, aux group); they are reduced over the workgroup
 // only when that pair changes and at the end.  Every decision depends on the
 // segment alone, so it is uniform across the workgroup, and every thread
@@ -897,11 +1014,12 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     }
     uint32_t si = lo;
     uint64_t s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
-    for (uint64_t q = c; q < c_end; ++q) {
+    for (uint64_t q = c, nq; q < c_end; q += nq) {
       while (q >= s_end) {
         ++si;
         s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
       }
+      nq = min(min(c_end, s_end) - q, (uint64_t)kUnroll);  // chunks of this segment in this step
       const DevSeg s = segs[si];
       const uint32_t g = groups[si], ga = aux_groups[si];
       const bool aux = (s.ops() & 5) != 0;  // cast or duplicate
@@ -913,7 +1031,7 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
       cur_aux = aux;
       const uint32_t total = s.len * s.rows;
       const uint32_t u0 = (uint32_t)(q - s.chunk_begin) * kChunkUnits;
-      const uint32_t u_end = min(u0 + kChunkUnits, total);
+      const uint32_t u_end = min(u0 + (uint32_t)nq * kChunkUnits, total);
       const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
       const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
       const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
@@ -1077,6 +1195,30 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   return EMRS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+template <int L>
+void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table, uint32_t nseg,
+                   uint64_t n_chunks, const uint64_t *stab, const uint64_t *dtab) {
+  const dim3 block(L);
+  if (nt && rb.table)
+    hipLaunchKernelGGL((copy_plan_kernel<true, true, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+                       stab, dtab);
+  else if (nt)
+    hipLaunchKernelGGL((copy_plan_kernel<true, false, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+                       stab, dtab);
+  else if (rb.table)
+    hipLaunchKernelGGL((copy_plan_kernel<false, true, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+                       stab, dtab);
+  else
+    hipLaunchKernelGGL((copy_plan_kernel<false, false, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src,
+                       rb.dst, stab, dtab);
+}
+}  // namespace
+
+extern "C" {
+
 int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out) {
   if (!plan || !out) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
   *out = plan->stats;
@@ -1100,10 +1242,38 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   if (rc) return rc;
 
   const bool nt = g_tuning.nontemporal.load() != 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint32_t nseg = (uint32_t)plan->segs.size();
+  const dim3 block(kThreads);
+  if (!g_tuning.persistent.load()) {
+    // One workgroup per chunk, on a grid of at most 65535 rows.
+    const uint64_t gx = std::min<uint64_t>(
+        plan->n_chunks, std::max<uint64_t>(1ull << 16, (plan->n_chunks + kMaxGridY - 1) / kMaxGridY));
+    if (gx > kMaxGridX) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan has too many chunks for one launch");
+    const dim3 grid((uint32_t)gx, (uint32_t)((plan->n_chunks + gx - 1) / gx));
+    uint64_t *tab = nullptr;
+    bool tab_owned = false;
+    rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
+    if (rc) return rc;
+    const uint64_t *stab = tab, *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
+    const uint32_t lanes = g_tuning.lanes.load();
+    if (lanes == 256)
+      launch_chunks<256>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+    else if (lanes == 128)
+      launch_chunks<128>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+    else
+      launch_chunks<64>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+    hipError_t le = hipGetLastError();
+    if (tab_owned) (void)hipFreeAsync(tab, st);
+    if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
+    return EMRS_OK;
+  }
+
+  // Persistent grid.  A run of N counts N steps of kUnroll chunks.
   const uint32_t bpc = g_tuning.blocks_per_cu.load();
   const uint64_t max_blocks = (uint64_t)cus * (bpc ? bpc : (uint32_t)(nt ? resident_nt : resident_t));
   uint64_t blocks = std::min<uint64_t>(plan->n_chunks, max_blocks);
-  uint32_t run = g_tuning.run.load();
+  uint32_t run = g_tuning.run.load() * kUnroll;
   const bool remap = g_tuning.xcd_remap.load() != 0;
   if (run) {
     // Round-robin runs: at most a quarter of each workgroup's share, so that
@@ -1115,29 +1285,27 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint64_t cpb = (plan->n_chunks + blocks - 1) / blocks;
   if (!remap && !run) blocks = (plan->n_chunks + cpb - 1) / cpb;
   const uint32_t xcd_stride = remap ? (uint32_t)(blocks / 8) : 0;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   uint64_t *tab = nullptr;
   bool tab_owned = false;
   rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
   if (rc) return rc;
   const uint64_t *stab = tab, *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
-  const dim3 grid((uint32_t)blocks), block(kThreads);
-  const uint32_t nseg = (uint32_t)plan->segs.size();
+  const dim3 grid((uint32_t)blocks);
   if (nt && rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<true, true>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
-                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+    hipLaunchKernelGGL((copy_plan_persistent_kernel<true, true>), grid, block, 0, st, table, nseg, plan->n_chunks,
+                       cpb, xcd_stride, run, rb.src, rb.dst, stab, dtab);
   else if (nt)
-    hipLaunchKernelGGL((copy_plan_kernel<true, false>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
-                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+    hipLaunchKernelGGL((copy_plan_persistent_kernel<true, false>), grid, block, 0, st, table, nseg, plan->n_chunks,
+                       cpb, xcd_stride, run, rb.src, rb.dst, stab, dtab);
   else if (rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<false, true>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
-                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+    hipLaunchKernelGGL((copy_plan_persistent_kernel<false, true>), grid, block, 0, st, table, nseg, plan->n_chunks,
+                       cpb, xcd_stride, run, rb.src, rb.dst, stab, dtab);
   else
-    hipLaunchKernelGGL((copy_plan_kernel<false, false>), grid, block, 0, st, table, nseg, plan->n_chunks, cpb,
-                       xcd_stride, run, rb.src, rb.dst, stab, dtab);
+    hipLaunchKernelGGL((copy_plan_persistent_kernel<false, false>), grid, block, 0, st, table, nseg, plan->n_chunks,
+                       cpb, xcd_stride, run, rb.src, rb.dst, stab, dtab);
   hipError_t le = hipGetLastError();
   if (tab_owned) (void)hipFreeAsync(tab, st);
-  if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
+  if (le != hipSuccess) return hip_fail(le, "copy_plan_persistent_kernel launch");
   return EMRS_OK;
 }
 
@@ -1209,7 +1377,8 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
     // each workgroup's share, so that small plans still spread out.
     uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * (uint32_t)resident_cmp);
     blocks = std::max<uint64_t>(8, blocks / 8 * 8);
-    const uint32_t run = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32, plan->n_chunks / (blocks * 4)));
+    const uint32_t run =
+        (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32 * kUnroll, plan->n_chunks / (blocks * 4)));
     const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
     if (rb.table)
       hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
@@ -1262,16 +1431,23 @@ int emrs_get_tuning(emrs_tuning *out) {
   out->nontemporal = g_tuning.nontemporal.load();
   out->xcd_remap = g_tuning.xcd_remap.load();
   out->run = g_tuning.run.load();
+  out->persistent = g_tuning.persistent.load();
+  out->lanes = g_tuning.lanes.load();
   return EMRS_OK;
 }
 
 int emrs_set_tuning(const emrs_tuning *t) {
   if (!t) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
   if (t->blocks_per_cu > 64) return fail(EMRS_ERR_INVALID_ARGUMENT, "blocks_per_cu must be in [0, 64]");
+  if (t->run > (1u << 20)) return fail(EMRS_ERR_INVALID_ARGUMENT, "run must be in [0, 2^20]");
+  if (t->lanes != 0 && t->lanes != 64 && t->lanes != 128 && t->lanes != 256)
+    return fail(EMRS_ERR_INVALID_ARGUMENT, "lanes must be 0, 64, 128 or 256");
   g_tuning.blocks_per_cu.store(t->blocks_per_cu);
   g_tuning.nontemporal.store(t->nontemporal ? 1 : 0);
   g_tuning.xcd_remap.store(t->xcd_remap ? 1 : 0);
   g_tuning.run.store(t->run);
+  g_tuning.persistent.store(t->persistent ? 1 : 0);
+  g_tuning.lanes.store(t->lanes ? t->lanes : 64);
   return EMRS_OK;
 }
 

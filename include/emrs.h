@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 3
+#define EMRS_ABI_VERSION 4
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -212,17 +212,22 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
 
 /*
  * Launch-shape knobs of emrs_plan_execute, process-wide.  Results never
- * depend on them; only speed does.
+ * depend on them; only speed does.  By default every chunk of 256 units is
+ * a workgroup of its own; persistent = 1 selects a persistent grid, which
+ * the other three fields shape.
  */
 typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
                              0 (default): as many as can be resident at once */
   uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
-  uint32_t xcd_remap;     /* 1 (default): each XCD works through one contiguous eighth of the chunks
-                             (workgroup b runs on XCD b % 8) */
-  uint32_t run;           /* 0: each workgroup copies one contiguous run of chunks;
-                             N > 0: chunks are dealt out round-robin in runs of N, capped at a
-                             quarter of a workgroup's share (default 4) */
+  uint32_t xcd_remap;     /* persistent grid, 1 (default): each XCD works through one contiguous
+                             eighth of the chunks (workgroup b runs on XCD b % 8) */
+  uint32_t run;           /* persistent grid, 0: each workgroup copies one contiguous run of
+                             chunks; N in [1, 2^20]: chunks are dealt out round-robin in runs of
+                             8N, capped at a quarter of a workgroup's share (default 4) */
+  uint32_t persistent;    /* 0 (default): one workgroup per chunk; 1: persistent grid */
+  uint32_t lanes;         /* one workgroup per chunk: lanes per workgroup, 64, 128 or 256
+                             (0: the default, 64, four 16-byte units per lane) */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);

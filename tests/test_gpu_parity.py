@@ -129,9 +129,15 @@ def test_manager_repad_round_trip(gpu_device):
     assert st.verify_synthetic(SEED)[0] == 0
 
 
-@pytest.mark.parametrize("tuning", [dict(run=0), dict(run=0, xcd_remap=False), dict(run=1), dict(run=64),
-                                    dict(blocks_per_cu=1), dict(nontemporal=False), dict(blocks_per_cu=3, run=7),
-                                    dict(run=4, xcd_remap=False), dict(run=1, blocks_per_cu=1, xcd_remap=False)])
+@pytest.mark.parametrize("tuning", [dict(nontemporal=False), dict(lanes=128), dict(lanes=256),
+                                    dict(lanes=256, nontemporal=False), dict(persistent=True),
+                                    dict(persistent=True, run=0), dict(persistent=True, run=0, xcd_remap=False),
+                                    dict(persistent=True, run=1), dict(persistent=True, run=64),
+                                    dict(persistent=True, blocks_per_cu=1),
+                                    dict(persistent=True, nontemporal=False),
+                                    dict(persistent=True, blocks_per_cu=3, run=7),
+                                    dict(persistent=True, run=4, xcd_remap=False),
+                                    dict(persistent=True, run=1, blocks_per_cu=1, xcd_remap=False)])
 def test_launch_shape_does_not_change_results(gpu_device, tuning):
     """Every launch shape of emrs_set_tuning writes the same bits."""
     from elasticmegatron_amd.resharding.model_spec import tiny_llama2
@@ -155,7 +161,7 @@ def test_launch_shape_does_not_change_results(gpu_device, tuning):
         _native.set_tuning()
     for x, y in zip(*outs):
         assert np.array_equal(x, y)
-    assert _native.get_tuning().run == 4
+    assert _native.get_tuning().run == 4 and _native.get_tuning().persistent == 0
 
 
 def _random_table(rng, n_segs, sizes):
@@ -201,15 +207,25 @@ def _random_table(rng, n_segs, sizes):
     return t
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
-def test_random_segments_match_numpy(gpu_device, seed):
+@pytest.mark.parametrize("seed,tuning", [(0, {}), (1, {}), (2, {}), (3, dict(lanes=128)), (4, dict(lanes=256)),
+                                         (5, dict(persistent=True)), (6, dict(lanes=256, nontemporal=False))])
+def test_random_segments_match_numpy(gpu_device, seed, tuning):
     """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills,
-    bf16 images and duplicates.
+    bf16 images and duplicates, under each launch shape.
 
     Segments are applied in order and may overlap in the destination here, so
     each segment runs as its own plan and the numpy model applies the same
     sequence.
     """
+    print(f"case random segments seed {seed} tuning {tuning}", flush=True)
+    try:
+        _native.set_tuning(**tuning)
+        _random_segments_match_numpy(gpu_device, seed)
+    finally:
+        _native.set_tuning()
+
+
+def _random_segments_match_numpy(gpu_device, seed):
     rng = np.random.default_rng(seed)
     nbytes = 1 << 20
     src_h = rng.integers(0, 256, nbytes, dtype=np.uint8)
@@ -272,8 +288,19 @@ def test_bf16_cast_rounding_special_values(gpu_device):
     assert (want[~np.concatenate([finite[:n // 2], [True], finite[n // 2:n - 1]])] == 0x7FC0).all()
 
 
-def test_large_multichunk_plan(gpu_device):
-    """Many chunks per workgroup, 2-D segments with > 2^16 rows, segments split at 2^30 units."""
+@pytest.mark.parametrize("tuning", [{}, dict(persistent=True)])
+def test_large_multichunk_plan(gpu_device, tuning):
+    """More chunks than one grid row holds, 2-D segments with > 2^16 rows, segments split at 2^30
+    units, and (persistent grid) many chunks per workgroup."""
+    print(f"case large plan tuning {tuning}", flush=True)
+    try:
+        _native.set_tuning(**tuning)
+        _large_multichunk_plan(gpu_device)
+    finally:
+        _native.set_tuning()
+
+
+def _large_multichunk_plan(gpu_device):
     n = (1 << 26) + 12  # fp32 elements (256 MiB + 48 B)
     src = torch.arange(n, dtype=torch.int32, device=gpu_device)
     dst = torch.full((n,), -1, dtype=torch.int32, device=gpu_device)
@@ -281,12 +308,14 @@ def test_large_multichunk_plan(gpu_device):
         (0, 0, 4, 0, 0, 0, 1 << 24, 1, 0, 0, 0, 0, 0, 0),                      # contiguous 64 MiB
         (0, 0, 4, 0, 1 << 24, (1 << 24) + 4, 1000, 20000, 1000, 1004, 0, 0, 0, 0),  # strided, co-aligned
         (0, 0, 4, 0, 45_000_000, 45_000_001, 3_000_001, 1, 0, 0, 0, 0, 0, 0),  # misaligned by 4 bytes
+        (0, 0, 1, 0, 200_000_001, 200_000_003, 8_000_000, 1, 0, 0, 0, 0, 0, 0),  # bytes, misaligned by 2
     ]
     t = np.zeros(len(rows), dtype=SEGMENT_DTYPE)
     t[:] = rows
     plan = _native.Plan(t, [n * 4], [n * 4], check_disjoint=True)
     st = plan.stats()
-    assert st.payload_bytes == 4 * ((1 << 24) + 1000 * 20000 + 3_000_001)
+    assert st.payload_bytes == 4 * ((1 << 24) + 1000 * 20000 + 3_000_001) + 8_000_000
+    assert st.n_chunks > 65536  # two rows of the one-workgroup-per-chunk grid
     plan.execute([src.data_ptr()], [dst.data_ptr()], torch.cuda.current_stream().cuda_stream)
     want = np.full(n, -1, dtype=np.int32)
     base = np.arange(n, dtype=np.int32)
@@ -295,6 +324,7 @@ def test_large_multichunk_plan(gpu_device):
         so, do = (1 << 24) + r * 1000, (1 << 24) + 4 + r * 1004
         want[do:do + 1000] = base[so:so + 1000]
     want[45_000_001:48_000_002] = base[45_000_000:48_000_001]
+    want.view(np.uint8)[200_000_003:208_000_003] = base.view(np.uint8)[200_000_001:208_000_001]
     assert np.array_equal(dst.cpu().numpy(), want)
 
 
