@@ -80,6 +80,8 @@ def parse():
                     help="re-allocate the destination state this many times and time 5 launches each")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
+    ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
+                    help="one workgroup per chunk of 256 units: lanes per workgroup (0: the default, 64)")
     ap.add_argument("--persistent", type=int, default=0,
                     help="0: one workgroup per chunk of 256 units; 1: persistent grid (the next three flags)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
@@ -169,7 +171,7 @@ def main():
     torch.cuda.set_device(dev)
     _native.load()
     _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run,
-                       bool(args.persistent))
+                       bool(args.persistent), args.lanes)
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:
