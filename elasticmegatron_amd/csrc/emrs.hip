@@ -532,6 +532,10 @@ struct emrs_plan {
   // pointer table of the first execution and the base pointers it holds.
   std::vector<uint64_t *> ptr_tables;
   std::vector<std::vector<uint64_t>> ptr_contents;
+  // For those same bases: the segment table with every offset made absolute
+  // (units from abs_base, the lowest referenced base), per device.
+  std::vector<DevSeg *> abs_tables;
+  std::vector<uint64_t> abs_base;
 };
 
 namespace {
@@ -775,6 +779,58 @@ int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t
     *out = nullptr;
     return hip_fail(e, "hipMemcpyAsync(pointer table)");
   }
+  return EMRS_OK;
+}
+
+// The plan's segment table on device `dev` resolved against the bases of its
+// cached pointer table: every offset counts units from *common, the lowest
+// referenced base, and every buffer id is 0, so the copy kernel looks up no
+// base pointer at all.  Built and uploaded synchronously on first use, like
+// the pointer table, and never written again.  *out = nullptr when the bases
+// are not the cached ones (the caller then uses the pointer table).
+int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, DevSeg **out, char **common) {
+  *out = nullptr;
+  std::lock_guard<std::mutex> lk(plan->mu);
+  if ((int)plan->ptr_tables.size() <= dev || !plan->ptr_tables[dev] || plan->ptr_contents[dev] != rb.ptrs)
+    return EMRS_OK;
+  if ((int)plan->abs_tables.size() <= dev) {
+    plan->abs_tables.resize(dev + 1, nullptr);
+    plan->abs_base.resize(dev + 1, 0);
+  }
+  if (!plan->abs_tables[dev]) {
+    const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
+    uint64_t lo = ~0ull;
+    for (uint32_t i = 0; i < ns; ++i)
+      if (plan->src_used[i]) lo = std::min(lo, rb.ptrs[i]);
+    for (uint32_t i = 0; i < nd; ++i)
+      if (plan->dst_used[i]) lo = std::min(lo, rb.ptrs[ns + i]);
+    // Referenced bases are 16-byte aligned, so every difference is a whole
+    // number of units.  Unreferenced buffers (a zero fill's source) may be
+    // NULL; their offsets are never used.
+    auto units_from_lo = [lo](uint64_t p, uint32_t log2) -> uint64_t { return p >= lo ? (p - lo) >> log2 : 0; };
+    std::vector<DevSeg> segs = plan->segs;
+    for (DevSeg &d : segs) {
+      const uint32_t ul = d.unit_log2(), ops = d.ops();
+      const uint32_t aux_log2 = (ops & 1) ? ul - 1 : ul;  // a bf16 image unit is half a unit
+      d.src_off = (ops & 2) ? 0 : d.src_off + units_from_lo(rb.ptrs[d.src_buf], ul);
+      d.dst_off += units_from_lo(rb.ptrs[ns + d.dst_buf], ul);
+      d.aux_off += units_from_lo(rb.ptrs[ns + d.aux_buf], aux_log2);
+      d.src_buf = d.dst_buf = d.aux_buf = 0;
+    }
+    const size_t bytes = segs.size() * sizeof(DevSeg);
+    DevSeg *t = nullptr;
+    hipError_t e = hipMalloc(&t, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(resolved plan table)");
+    e = hipMemcpy(t, segs.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(t);
+      return hip_fail(e, "hipMemcpy(resolved plan table)");
+    }
+    plan->abs_tables[dev] = t;
+    plan->abs_base[dev] = lo;
+  }
+  *out = plan->abs_tables[dev];
+  *common = reinterpret_cast<char *>(plan->abs_base[dev]);
   return EMRS_OK;
 }
 
@@ -1256,13 +1312,29 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
     rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
     if (rc) return rc;
     const uint64_t *stab = tab, *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
+    // The bases of the cached pointer table also have a resolved segment
+    // table: no per-workgroup base lookup.
+    const ResolvedBases *lb = &rb;
+    ResolvedBases flat;
+    if (rb.table && !tab_owned) {
+      DevSeg *abs = nullptr;
+      char *common = nullptr;
+      rc = resolved_table(plan, dev, rb, &abs, &common);
+      if (rc) return rc;
+      if (abs) {
+        table = abs;
+        flat.src.p[0] = flat.dst.p[0] = common;
+        lb = &flat;
+        stab = dtab = nullptr;
+      }
+    }
     const uint32_t lanes = g_tuning.lanes.load();
     if (lanes == 256)
-      launch_chunks<256>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<256>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
     else if (lanes == 128)
-      launch_chunks<128>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<128>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
     else
-      launch_chunks<64>(nt, rb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<64>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
     hipError_t le = hipGetLastError();
     if (tab_owned) (void)hipFreeAsync(tab, st);
     if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
@@ -1409,15 +1481,18 @@ int emrs_plan_destroy(emrs_plan *plan) {
   if (!plan) return EMRS_OK;
   int prev = 0;
   (void)hipGetDevice(&prev);
-  for (size_t d = 0; d < std::max(plan->dev_tables.size(), plan->ptr_tables.size()); ++d) {
+  const size_t n_dev = std::max({plan->dev_tables.size(), plan->ptr_tables.size(), plan->abs_tables.size()});
+  for (size_t d = 0; d < n_dev; ++d) {
     DevSeg *segs = d < plan->dev_tables.size() ? plan->dev_tables[d] : nullptr;
     uint64_t *ptrs = d < plan->ptr_tables.size() ? plan->ptr_tables[d] : nullptr;
-    if (segs || ptrs) {
+    DevSeg *abs = d < plan->abs_tables.size() ? plan->abs_tables[d] : nullptr;
+    if (segs || ptrs || abs) {
       (void)hipSetDevice((int)d);
       // Launches enqueued on any stream may still read the tables.
       (void)hipDeviceSynchronize();
       if (segs) (void)hipFree(segs);
       if (ptrs) (void)hipFree(ptrs);
+      if (abs) (void)hipFree(abs);
     }
   }
   (void)hipSetDevice(prev);

@@ -61,9 +61,10 @@ extern "C" {
 /* Maximum number of source (and, separately, destination) buffers.  Up to
  * 128 per side travel in kernel arguments; a plan with more on either side
  * passes its base pointers through a device table.  The plan keeps, per
- * device, the table of its first call and reuses it while the base pointers
- * repeat; a call with other pointers uploads a table of its own and frees it
- * on its stream (hipMallocAsync / hipFreeAsync). */
+ * device, the table of its first call, and its segment table resolved against
+ * those pointers, and reuses both while the base pointers repeat; a call with
+ * other pointers uploads a pointer table of its own and frees it on its
+ * stream (hipMallocAsync / hipFreeAsync). */
 #define EMRS_MAX_BUFFERS 65535
 
 /* emrs_plan_create flags */

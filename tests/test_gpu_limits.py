@@ -73,6 +73,91 @@ def test_pointer_table_reuse_and_new_bases(gpu_device):
             assert int(got[:128].sum()) == 0 and int(got[640:].sum()) == 0, (k, i)
 
 
+def _kind_table(rng, n, size):
+    """Segment i: source buffer i -> destination buffer i, second destination (cast image or
+    duplicate) in destination buffer n + i.  Kinds cycle: copy (every element width, aligned or
+    not, 1-D or strided), zero fill, fp32 with its bf16 image, duplicate."""
+    rows = []
+    for i in range(n):
+        kind = i % 4
+        eb = 4 if kind == 2 else int(rng.choice([1, 2, 4, 8]))
+        ln = int(rng.integers(1, 60))  # the largest extent, 3 rows of 8-byte elements, fits in 4 KB
+        r = int(rng.choice([1, 1, 3]))
+        ss = ds = 0
+        if r > 1:
+            ss, ds = ln + int(rng.integers(0, 9)), ln + int(rng.integers(0, 9))
+        if rng.random() < 0.5:  # 16-byte friendly
+            unit = 16 // eb
+            ln = (ln // unit + 1) * unit
+            if r > 1:
+                ss, ds = 2 * ln, 2 * ln
+        nb = size // eb
+        so = int(rng.integers(0, nb - ((r - 1) * ss + ln)))
+        do = int(rng.integers(0, nb - ((r - 1) * ds + ln)))
+        if rng.random() < 0.5:
+            so, do = so - so % (16 // eb), do - do % (16 // eb)
+        flags, ao, astr = 0, 0, 0
+        if kind == 1:
+            flags = 2
+        elif kind == 2:
+            flags, ao, astr = 1, do, ds
+        elif kind == 3:
+            flags, ao, astr = 4, do, ds
+        rows.append((i, i, eb, flags, so, do, ln, r, ss, ds, n + i if kind in (2, 3) else 0, 0, ao, astr))
+    t = np.zeros(n, dtype=SEGMENT_DTYPE)
+    t[:] = rows
+    return t
+
+
+def _expected(t, srcs_h, n, size):
+    from tests.helpers import bf16_rne_bits
+
+    out = [np.zeros(size, dtype=np.uint8) for _ in range(2 * n)]
+    for s in t:
+        eb, i = int(s["elem_bytes"]), int(s["src_buf"])
+        dt = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[eb]
+        a, b, x = srcs_h[i].view(dt), out[i].view(dt), out[n + i]
+        for r in range(int(s["rows"])):
+            so = int(s["src_off"]) + r * int(s["src_stride"])
+            do = int(s["dst_off"]) + r * int(s["dst_stride"])
+            vals = np.zeros(int(s["len"]), dtype=dt) if int(s["flags"]) & 2 else a[so:so + int(s["len"])]
+            b[do:do + int(s["len"])] = vals
+            ao = int(s["aux_off"]) + r * int(s["aux_stride"])
+            if int(s["flags"]) & 1:
+                x.view(np.uint16)[ao:ao + int(s["len"])] = bf16_rne_bits(vals)
+            if int(s["flags"]) & 4:
+                x.view(dt)[ao:ao + int(s["len"])] = vals
+    return out
+
+
+@pytest.mark.parametrize("lanes", [64, 256])
+def test_table_bases_every_segment_kind(gpu_device, lanes):
+    """A plan over 200 source and 400 destination buffers, with every kind of segment, run on the
+    bases of its first call (the segment table resolved against them, no base lookup in the
+    kernel), on other bases (the pointer table), and on the first bases again."""
+    n, size = 200, 4096
+    rng = np.random.default_rng(11)
+    srcs_h = [rng.integers(0, 256, size, dtype=np.uint8) for _ in range(n)]
+    srcs = [torch.from_numpy(h).to(gpu_device) for h in srcs_h]
+    sets = [[torch.zeros(size, dtype=torch.uint8, device=gpu_device) for _ in range(2 * n)] for _ in range(2)]
+    t = _kind_table(rng, n, size)
+    plan = _native.Plan(t, [size] * n, [size] * (2 * n), check_disjoint=True)
+    want = _expected(t, srcs_h, n, size)
+    sp = [s.data_ptr() for s in srcs]
+    try:
+        _native.set_tuning(lanes=lanes)
+        for k, which in enumerate([0, 0, 1, 0, 1]):
+            print(f"case table bases lanes {lanes} call {k}: destination set {which}", flush=True)
+            for d in sets[which]:
+                d.zero_()
+            plan.execute(sp, [d.data_ptr() for d in sets[which]], torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            for j in range(2 * n):
+                assert np.array_equal(sets[which][j].cpu().numpy(), want[j]), (k, j)
+    finally:
+        _native.set_tuning()
+
+
 def test_segments_beyond_two_to_the_thirty_units(gpu_device):
     nbytes = 3 << 29  # 1.5 GiB
     src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu_device)
