@@ -227,3 +227,26 @@ def test_xor_checksum_rejects_bad_arguments_before_touching_a_device():
         with pytest.raises(_native.EmrsError) as e:
             _native.xor_checksum(ptr, n, 0x2000)
         assert e.value.code == -3
+
+
+def test_tuning_defaults_and_rejections():
+    """emrs_tuning: the default launch shape reads back, settings round-trip, and values outside the
+    documented ranges are refused without changing the current setting (no device needed)."""
+    assert ctypes.sizeof(_native.Tuning) == 24  # six uint32 fields, as in emrs.h
+    t = _native.get_tuning()
+    assert (t.persistent, t.lanes, t.nontemporal, t.run) == (0, 64, 1, 4)
+    try:
+        _native.set_tuning(lanes=128, persistent=True, run=7, blocks_per_cu=3)
+        t = _native.get_tuning()
+        assert (t.persistent, t.lanes, t.run, t.blocks_per_cu) == (1, 128, 7, 3)
+        for kw in (dict(lanes=96), dict(lanes=512), dict(run=(1 << 20) + 1), dict(blocks_per_cu=65)):
+            with pytest.raises(_native.EmrsError) as e:
+                _native.set_tuning(**kw)
+            assert e.value.code == -1
+            assert _native.get_tuning().lanes == 128  # unchanged
+        _native.set_tuning(lanes=0)  # 0 selects the default lane count
+        assert _native.get_tuning().lanes == 64
+    finally:
+        _native.set_tuning()
+    t = _native.get_tuning()
+    assert (t.persistent, t.lanes, t.run, t.blocks_per_cu) == (0, 64, 4, 0)
