@@ -79,6 +79,17 @@ struct Bases {
 };
 static_assert(sizeof(Bases) <= 1024, "Bases travels in kernel arguments");
 
+// Where a chunk's segment search starts and ends: chunk c lies in one of the
+// segments first[c >> shift] .. first[(c >> shift) + 1], so the search spans
+// a few dozen segments of the plan instead of all of them.  Travels in
+// kernel arguments beside the two Bases.
+constexpr uint32_t kHintBuckets = 256;
+struct SegHint {
+  uint32_t first[kHintBuckets + 1];
+  uint32_t shift;
+};
+static_assert(2 * sizeof(Bases) + sizeof(SegHint) + 64 <= 4096, "kernel arguments stay under 4 KB");
+
 // Segment as the kernel sees it.  Offsets and strides are in units of
 // (1 << unit_log2) bytes: 16 for the vector path, the element size otherwise.
 // A cast segment (fp32 only) also writes bf16 copies to aux, whose offset and
@@ -428,13 +439,14 @@ __device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, con
 // With 256 lanes four waves repeat the same search for one 16-byte load each,
 // and the launch runs about 20% slower.
 template <bool kNT, bool kTable, int L>
-__global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint32_t n_segs,
-                                                      uint64_t n_chunks, Bases src, Bases dst,
+__global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint64_t n_chunks,
+                                                      SegHint hint, Bases src, Bases dst,
                                                       const uint64_t *__restrict__ src_tab,
                                                       const uint64_t *__restrict__ dst_tab) {
   const uint64_t c = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
   if (c >= n_chunks) return;
-  uint32_t lo = 0, hi = n_segs - 1;
+  const uint32_t b = (uint32_t)(c >> hint.shift);
+  uint32_t lo = hint.first[b], hi = hint.first[b + 1];
   while (lo < hi) {
     const uint32_t mid = (lo + hi + 1) >> 1;
     if (segs[mid].chunk_begin <= c) lo = mid;
@@ -523,6 +535,7 @@ struct emrs_plan {
   std::vector<DevSeg> segs;
   std::vector<uint32_t> origin;              // input segment of each device segment
   uint64_t n_chunks = 0;
+  SegHint hint{};                            // search bounds of the one-workgroup-per-chunk kernel
   std::vector<uint64_t> src_bytes, dst_bytes;
   std::vector<uint8_t> src_used, dst_used;  // buffers referenced by a non-empty segment
   emrs_plan_stats stats{};
@@ -620,6 +633,26 @@ struct Builder {
     origin.push_back(cur_origin);
   }
 };
+
+// Search bounds per bucket of 2^shift chunks, with at most kHintBuckets
+// buckets: first[b] is the segment holding chunk b << shift (the last segment
+// past the end).
+void make_hint(const std::vector<DevSeg> &segs, uint64_t n_chunks, SegHint *h) {
+  const uint32_t last = segs.empty() ? 0 : (uint32_t)segs.size() - 1;
+  h->shift = 0;
+  while (n_chunks && ((n_chunks - 1) >> h->shift) >= kHintBuckets) ++h->shift;
+  for (uint32_t b = 0; b <= kHintBuckets; ++b) {
+    const uint64_t c = (uint64_t)b << h->shift;
+    if (c >= n_chunks) {
+      h->first[b] = last;
+      continue;
+    }
+    // Last segment whose first chunk is <= c.
+    auto it = std::upper_bound(segs.begin(), segs.end(), c,
+                               [](uint64_t v, const DevSeg &d) { return v < d.chunk_begin; });
+    h->first[b] = (uint32_t)(it - segs.begin()) - 1;
+  }
+}
 
 int log2_of(uint32_t eb) {
   switch (eb) {
@@ -1234,6 +1267,7 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
   p->segs = std::move(bld.out);
   p->origin = std::move(bld.origin);
   p->n_chunks = bld.chunks;
+  make_hint(p->segs, p->n_chunks, &p->hint);
   p->src_bytes.assign(src_buf_bytes, src_buf_bytes + n_src_bufs);
   p->dst_bytes.assign(dst_buf_bytes, dst_buf_bytes + n_dst_bufs);
   p->src_used = std::move(src_used);
@@ -1255,20 +1289,20 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
 
 namespace {
 template <int L>
-void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table, uint32_t nseg,
-                   uint64_t n_chunks, const uint64_t *stab, const uint64_t *dtab) {
+void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table,
+                   uint64_t n_chunks, const SegHint &hint, const uint64_t *stab, const uint64_t *dtab) {
   const dim3 block(L);
   if (nt && rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<true, true, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+    hipLaunchKernelGGL((copy_plan_kernel<true, true, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
                        stab, dtab);
   else if (nt)
-    hipLaunchKernelGGL((copy_plan_kernel<true, false, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+    hipLaunchKernelGGL((copy_plan_kernel<true, false, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
                        stab, dtab);
   else if (rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<false, true, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src, rb.dst,
+    hipLaunchKernelGGL((copy_plan_kernel<false, true, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
                        stab, dtab);
   else
-    hipLaunchKernelGGL((copy_plan_kernel<false, false, L>), grid, block, 0, st, table, nseg, n_chunks, rb.src,
+    hipLaunchKernelGGL((copy_plan_kernel<false, false, L>), grid, block, 0, st, table, n_chunks, hint, rb.src,
                        rb.dst, stab, dtab);
 }
 }  // namespace
@@ -1330,11 +1364,11 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
     }
     const uint32_t lanes = g_tuning.lanes.load();
     if (lanes == 256)
-      launch_chunks<256>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<256>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
     else if (lanes == 128)
-      launch_chunks<128>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<128>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
     else
-      launch_chunks<64>(nt, *lb, grid, st, table, nseg, plan->n_chunks, stab, dtab);
+      launch_chunks<64>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
     hipError_t le = hipGetLastError();
     if (tab_owned) (void)hipFreeAsync(tab, st);
     if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
