@@ -26,6 +26,13 @@ def test_more_than_one_gpu_is_refused_with_a_reason():
     assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
 
 
+def test_launch_shape_flags_are_checked_before_any_device_work():
+    r = _run("--lanes", "96")
+    assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""
+    r = _run("--help")
+    assert r.returncode == 0 and "--lanes" in r.stdout and "--persistent" in r.stdout
+
+
 @pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="checks the behaviour without a GPU")
 def test_without_a_gpu_it_says_so():
     r = _run("--steps", "1", "--warmup", "0")
