@@ -28,6 +28,7 @@ ERRORS = {
     -6: "EMRS_ERR_NO_DEVICE",
     -7: "EMRS_ERR_TOO_MANY_BUFFERS",
     -8: "EMRS_ERR_ALIAS",
+    -9: "EMRS_ERR_CAPTURE",
 }
 EMRS_PLAN_CHECK_DISJOINT = 1
 EMRS_MAX_BUFFERS = 65535
@@ -105,7 +106,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
     lib.emrs_xor_checksum.restype = I
     lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
-    if lib.emrs_abi_version() != 4:
+    if lib.emrs_abi_version() != 5:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib

@@ -1,4 +1,4 @@
-"""In-tree build of the native library (and the oracle's C generator).
+"""In-tree build of the native library.
 
     python -m elasticmegatron_amd.build
 
@@ -44,13 +44,8 @@ def build_native(verbose: bool = False) -> str:
     return LIB
 
 
-def build_oracle() -> None:
-    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
-
-
 def main() -> int:
     print(build_native(verbose=True))
-    build_oracle()
     return 0
 
 

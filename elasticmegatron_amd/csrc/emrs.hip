@@ -53,6 +53,23 @@ int hip_fail(hipError_t e, const char *what) {
   return fail(EMRS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// A call that has to allocate device memory or upload a table cannot be
+// recorded into a HIP graph: the captured copy would read host memory that is
+// gone when the graph replays, and the allocation would not be replayed at
+// all.  Such calls are refused while `st` is capturing; the caller runs the
+// same call once outside the capture first, after which calls with the same
+// base pointers need neither.
+int refuse_capture(hipStream_t st, const char *what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(EMRS_ERR_CAPTURE, std::string(what) +
+                                      " would allocate or upload while the stream is capturing a graph; "
+                                      "run the call once before the capture, with the same base pointers");
+  return EMRS_OK;
+}
+
 #ifndef EMRS_COPY_THREADS
 #define EMRS_COPY_THREADS 256  // lanes per workgroup
 #endif
@@ -398,8 +415,9 @@ __device__ __forceinline__ void copy_units(const DevSeg &s, const char *sbase, c
       if (u < total) v[j] = ld<T, kNT>(src + so);
     }
   }
-  // Destination offsets are recomputed rather than kept from the loads:
-  // fewer registers, so that eight waves fit on each SIMD.
+  // Destination offsets are recomputed rather than kept from the loads: that
+  // holds the kernel at 66 VGPRs instead of 74, so seven waves fit on each
+  // SIMD instead of six.
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     const uint32_t u = u0 + j * L + threadIdx.x;
@@ -786,6 +804,7 @@ int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t
         return EMRS_OK;
       }
     } else {
+      if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
       uint64_t *t = nullptr;
       hipError_t e = hipMalloc(reinterpret_cast<void **>(&t), bytes);
       if (e != hipSuccess) return hip_fail(e, "hipMalloc(pointer table)");
@@ -800,6 +819,9 @@ int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t
       return EMRS_OK;
     }
   }
+  // Other bases than the cached ones: a table of this call's own, which a
+  // captured graph could not replay (its host copy is this call's).
+  if (int rc = refuse_capture(st, "a call whose base pointers differ from the plan's first call")) return rc;
   *owned = true;
   hipError_t e = hipMallocAsync(reinterpret_cast<void **>(out), bytes, st);
   if (e != hipSuccess) {
@@ -821,7 +843,8 @@ int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t
 // base pointer at all.  Built and uploaded synchronously on first use, like
 // the pointer table, and never written again.  *out = nullptr when the bases
 // are not the cached ones (the caller then uses the pointer table).
-int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, DevSeg **out, char **common) {
+int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t st, DevSeg **out,
+                   char **common) {
   *out = nullptr;
   std::lock_guard<std::mutex> lk(plan->mu);
   if ((int)plan->ptr_tables.size() <= dev || !plan->ptr_tables[dev] || plan->ptr_contents[dev] != rb.ptrs)
@@ -831,6 +854,7 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, DevSeg **o
     plan->abs_base.resize(dev + 1, 0);
   }
   if (!plan->abs_tables[dev]) {
+    if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
     const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
     uint64_t lo = ~0ull;
     for (uint32_t i = 0; i < ns; ++i)
@@ -868,10 +892,11 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, DevSeg **o
 }
 
 // The plan's segment table on device `dev`, uploaded on first use.
-int device_table(emrs_plan *plan, int dev, DevSeg **table) {
+int device_table(emrs_plan *plan, int dev, hipStream_t st, DevSeg **table) {
   std::lock_guard<std::mutex> lk(plan->mu);
   if ((int)plan->dev_tables.size() <= dev) plan->dev_tables.resize(dev + 1, nullptr);
   if (!plan->dev_tables[dev]) {
+    if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
     const size_t bytes = plan->segs.size() * sizeof(DevSeg);
     DevSeg *t = nullptr;
     hipError_t e = hipMalloc(&t, bytes);
@@ -1327,12 +1352,12 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
   rc = current_device(&dev, &cus, &resident_nt, &resident_t);
   if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
   DevSeg *table = nullptr;
-  rc = device_table(plan, dev, &table);
+  rc = device_table(plan, dev, st, &table);
   if (rc) return rc;
 
   const bool nt = g_tuning.nontemporal.load() != 0;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const uint32_t nseg = (uint32_t)plan->segs.size();
   const dim3 block(kThreads);
   if (!g_tuning.persistent.load()) {
@@ -1353,7 +1378,7 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
     if (rb.table && !tab_owned) {
       DevSeg *abs = nullptr;
       char *common = nullptr;
-      rc = resolved_table(plan, dev, rb, &abs, &common);
+      rc = resolved_table(plan, dev, rb, st, &abs, &common);
       if (rc) return rc;
       if (abs) {
         table = abs;
@@ -1452,8 +1477,12 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
   rc = current_device(&dev, &cus, &resident_nt, &resident_t);
   if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // The comparison allocates its accumulators and waits for the stream.
+  rc = refuse_capture(st, "emrs_plan_compare");
+  if (rc) return rc;
   DevSeg *table = nullptr;
-  rc = device_table(plan, dev, &table);
+  rc = device_table(plan, dev, st, &table);
   if (rc) return rc;
   int resident_cmp = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident_cmp, compare_plan_kernel<false>, kThreads, 0) !=
@@ -1463,7 +1492,6 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
     resident_cmp = 4;
   }
 
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
   const size_t grp_bytes = g_host.size() * sizeof(uint32_t);
   char *buf = nullptr;
@@ -1476,8 +1504,9 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   if (e == hipSuccess) e = hipMemcpyAsync(grp, g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
   uint64_t *tab = nullptr;
   bool tab_owned = false;
-  if (e == hipSuccess && pointer_table(plan, dev, rb, st, &tab, &tab_owned) != EMRS_OK) e = hipErrorOutOfMemory;
-  if (e == hipSuccess) {
+  int table_rc = EMRS_OK;  // a pointer-table failure keeps its own message
+  if (e == hipSuccess) table_rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
+  if (e == hipSuccess && table_rc == EMRS_OK) {
     // A persistent grid of resident workgroups, a multiple of 8 (one eighth
     // of the plan per XCD), in runs of up to 32 chunks: at most a quarter of
     // each workgroup's share, so that small plans still spread out.
@@ -1495,9 +1524,10 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
     e = hipGetLastError();
   }
   if (tab_owned) (void)hipFreeAsync(tab, st);
-  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess && table_rc == EMRS_OK) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   (void)hipFree(buf);
+  if (table_rc != EMRS_OK) return table_rc;
   if (e != hipSuccess) return hip_fail(e, "compare_plan_kernel");
   for (uint32_t g = 0; g < n_groups; ++g) {
     stats[g].mismatches = host[g].mismatches;

@@ -26,10 +26,12 @@ class ParallelStrategy:
     num_distributed_optimizer_instances: int = 1
     expert_model_parallel_size: int = 1
     expert_tensor_parallel_size: Optional[int] = None
-    sequence_parallel: Optional[bool] = None
-    order: str = "tp-cp-ep-dp-pp"
-    # Not part of the identity of a strategy (the reference hashes str(self),
-    # parallel_strategy.py:223-232, which omits them).
+    # The fields below are not part of a strategy's identity: the reference
+    # compares and hashes str(self), which prints only the seven sizes above
+    # (parallel_strategy.py:223-232).  Strategies that differ only here are
+    # equal, hash alike and share every plan and layout cache.
+    sequence_parallel: Optional[bool] = field(default=None, compare=False)
+    order: str = field(default="tp-cp-ep-dp-pp", compare=False)
     ranks: Optional[Tuple[int, ...]] = field(default=None, compare=False)
 
     def __post_init__(self):

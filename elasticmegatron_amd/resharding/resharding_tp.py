@@ -113,6 +113,5 @@ class TensorParallelAttr:
         return isinstance(other, TensorParallelAttr) and hash(self) == hash(other)
 
     def __str__(self):
-        return (f"TensorParallelAttr(tensor_model_parallel={self.tensor_model_parallel}, "
-                f"partition_dim={self.partition_dim}, partition_stride={self.partition_stride}), "
-                f"model_param_range_in_group={self.model_param_range_in_group}")
+        split = f"split on dim {self.partition_dim}" if self.tensor_model_parallel else "replicated"
+        return f"<TP {split}, full {'x'.join(map(str, self.full_shape))}>"

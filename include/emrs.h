@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 4
+#define EMRS_ABI_VERSION 5
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -57,6 +57,7 @@ extern "C" {
 #define EMRS_ERR_NO_DEVICE (-6)
 #define EMRS_ERR_TOO_MANY_BUFFERS (-7)
 #define EMRS_ERR_ALIAS (-8)
+#define EMRS_ERR_CAPTURE (-9) /* the call would allocate or upload while its stream captures a graph */
 
 /* Maximum number of source (and, separately, destination) buffers.  Up to
  * 128 per side travel in kernel arguments; a plan with more on either side
@@ -154,7 +155,9 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
  * synchronously; later calls with the same bases enqueue one kernel launch
  * and nothing else, so they may be captured into a HIP graph.  Calls with
  * other bases than the first beyond 128 buffers allocate a stream-ordered
- * pointer table.  Replaces one call of TransferManager.transfer_optimizer_tensors
+ * pointer table.  Neither the first call nor such a call may be captured:
+ * while `stream` is capturing they return EMRS_ERR_CAPTURE and enqueue
+ * nothing.  Replaces one call of TransferManager.transfer_optimizer_tensors
  * (transfer.py:291-341) together with the bf16 rebuild of
  * TrainingState.update_model_weight (training_state.py:176-197).
  */
@@ -203,9 +206,10 @@ typedef struct emrs_compare_stats {
  *   stats:         n_groups host records, filled when the call returns
  * Base pointers follow emrs_plan_execute's rules.  The call runs on `stream`
  * and waits for it.  It allocates and frees a small device buffer (the
- * group tables and accumulators), so it is not for capture into a graph.
+ * group tables and accumulators), so it is not for capture into a graph:
+ * while `stream` is capturing it returns EMRS_ERR_CAPTURE.
  * Errors: INVALID_ARGUMENT (n_groups == 0, a group id >= n_groups), the
- * base-pointer errors of emrs_plan_execute, NO_DEVICE, HIP.
+ * base-pointer errors of emrs_plan_execute, CAPTURE, NO_DEVICE, HIP.
  */
 int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
                       const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,

@@ -10,6 +10,22 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X)")
+    _build_oracle_generator()
+
+
+def _build_oracle_generator():
+    """The oracle's C generator (oracle/Makefile), built when missing and a compiler is here.
+
+    The oracle falls back to its numpy generator without it, so a failed build is not an error.
+    """
+    import shutil
+    import subprocess
+
+    lib = os.path.join(ROOT, "oracle", "build", "libsynth_ref.so")
+    if os.path.exists(lib) or not (shutil.which("make") and shutil.which("gcc")):
+        return
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=False,
+                   stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
 
 
 @pytest.fixture(scope="session")

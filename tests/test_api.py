@@ -213,3 +213,22 @@ def test_space_does_not_keep_states_alive(gpu_device):
 
     gc.collect()
     assert old() is None
+
+
+def test_dict_strategies_share_the_cached_plan():
+    """A strategy passed as a dict, or with only sequence_parallel changed, is the same strategy
+    (parallel_strategy.py:223-232): the plan a meta-device reshard built is the one reused."""
+    listed = [ParallelStrategy(8, 2, 1, sequence_parallel=False), ParallelStrategy(8, 4, 1)]
+    mgr = ElasticMegatronManager(listed, tiny_llama2(), device="cpu")
+    assert mgr.reshard(dict(world_size=8, tensor_model_parallel_size=4, pipeline_model_parallel_size=1),
+                       is_meta_device=True) is None
+    assert len(mgr.transfer_manager._plans) == 1
+    plan = next(iter(mgr.transfer_manager._plans.values()))
+    mgr.reshard(ParallelStrategy(8, 4, 1, sequence_parallel=False), is_meta_device=True)
+    mgr.reshard(listed[1], is_meta_device=True)
+    assert len(mgr.transfer_manager._plans) == 1
+    assert next(iter(mgr.transfer_manager._plans.values())) is plan
+    # A state laid out for the dict form of the first strategy is adopted as its state.
+    state = TrainingState.allocate(mgr.virtual_param_space.layout(ParallelStrategy(8, 2, 1)), "cpu")
+    ElasticMegatronManager([dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1,
+                                 sequence_parallel=False)], tiny_llama2(), training_state=state)

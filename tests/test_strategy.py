@@ -79,3 +79,20 @@ def test_is_redundant_backup():
         PS.is_redundant_backup(PS(6, 2, 1), b)
     with pytest.raises(AssertionError):
         PS.is_redundant_backup(PS(8, 1, 1), b)
+
+
+def test_identity_is_the_seven_sizes():
+    """parallel_strategy.py:223-232: equality and hash go through str(self), which prints the
+    world size and the six parallel sizes only; sequence parallelism and the rank order do not count."""
+    a = PS(8, 4, 1)
+    b = PS(8, 4, 1, sequence_parallel=False)
+    assert a.sequence_parallel is True and b.sequence_parallel is False
+    assert a == b and hash(a) == hash(b) and len({a, b}) == 1
+    assert PS(8, 2, 1, ranks=tuple(range(8))) == PS(8, 2, 1)
+    # Every size still counts.
+    assert PS(8, 4, 1) != PS(8, 4, 2)
+    assert PS(8, 1, 1, expert_model_parallel_size=2) != PS(8, 1, 1)
+    assert PS(8, 2, 1, expert_tensor_parallel_size=1) != PS(8, 2, 1)
+    assert PS(8, 1, 1, context_parallel_size=2) != PS(8, 1, 1)
+    assert (PS(8, 1, 1, context_parallel_size=2, num_distributed_optimizer_instances=2)
+            != PS(8, 1, 1, context_parallel_size=2))
