@@ -133,6 +133,12 @@ def dp_distribution(layout: BufferLayout) -> Dict[int, Dict[int, Tuple[int, int]
         s = layout.shard_size(bid)
         for p in b.params:
             ps, pe, _ = layout.param_index_map[p]
+            if ps < b.start:
+                # A shared-embedding parameter placed in the padding its predecessor bucket claimed
+                # (its start is 64-aligned but the closed bucket's end was padded past it): its first
+                # elements would belong to no shard.  The reference stops here too, when it makes the
+                # parameter's range relative to its bucket (resharding_dp.py:276-278, Range.normalize).
+                raise AssertionError(f"parameter {p} starts at {ps}, before its bucket at {b.start}")
             for r in range(dp):
                 lo = max(ps, b.start + r * s)
                 hi = min(pe, b.start + (r + 1) * s)

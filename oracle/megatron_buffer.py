@@ -53,6 +53,9 @@ def distribution(numels, dp, bucket_size, shared=None, dist_opt=True):
     ranges, buckets = layout(numels, dp, bucket_size, shared, dist_opt)
     out = {i: {} for i in ranges}
     for bs, be, members in buckets:
+        # resharding_dp.py:276-278 makes each member's range relative to its bucket start, which
+        # Range.normalize (util.py:65-69) refuses for a member starting before it.
+        assert all(ranges[i][0] >= bs for i in members), "a parameter starts before its bucket"
         s = (be - bs) // dp
         for r in range(dp):
             lo_r, hi_r = bs + r * s, bs + (r + 1) * s

@@ -19,6 +19,8 @@ void oracle_synth(uint64_t seed, uint32_t param_id, uint32_t kind, const uint64_
   const uint64_t key = mix(mix(seed + G) + (4ull * param_id + stream + 1) * G);
   float scale;
   memcpy(&scale, &SCALE[stream], 4);
+  /* Every element is independent: large requests are split over the host's threads. */
+#pragma omp parallel for schedule(static) if (n > (1u << 16))
   for (uint64_t i = 0; i < n; ++i) {
     const uint64_t h = mix(key + (idx[i] + 1) * G);
     const int32_t s = (int32_t)((h & 0xffff) + ((h >> 16) & 0xffff) + ((h >> 32) & 0xffff) + (h >> 48)) - 131070;

@@ -278,13 +278,15 @@ def rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst):
     return out
 
 
-def redundant_backup(inv, hp, src, dst, src_world, scale_up):
-    """Group-ZeRO switch (transfer.py:343-388): migrate on the master, broadcast to the instances."""
+def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None):
+    """Group-ZeRO switch (transfer.py:343-388): migrate on the master, broadcast to the instances.
+
+    ``params``: the parameter ids to move (default: all); ``src_world`` must hold them."""
     dist = dp_distributions(inv, dst, hp)
     out = {}
     for p in inv:
         pid = p["id"]
-        if pid not in dist:
+        if pid not in dist or (params is not None and pid not in params):
             continue
         T = dst.tp
         for t in range(T):

@@ -155,6 +155,18 @@ SMALL_CASES.append(("llama2_tied_pp1_pp2_pp4_tp2pp1",
                     small_llama2_tied, [PS(8, 1, 1), PS(8, 1, 2), PS(8, 2, 4), PS(8, 2, 1)]))
 
 
+def small_ragged():
+    """Shapes that are not multiples of 64 or 8 (hidden 200, FFN 520, vocabulary 1000) and small
+    buckets: parameter starts, bucket ends and DP shards land on padding, rows on odd offsets."""
+    return ms.ModelSpec(name="small-ragged", num_layers=2, hidden_size=200, num_attention_heads=4,
+                        ffn_hidden_size=520, padded_vocab_size=1000, ddp_bucket_size=40_000,
+                        overlap_grad_reduce=True)
+
+
+SMALL_CASES.append(("ragged_tp2dp4_dp6_tp4dp2_tp2dp3",
+                    small_ragged, [PS(8, 2, 1), PS(6, 1, 1), PS(8, 4, 1), PS(6, 2, 1)]))
+
+
 # Vocabulary re-padding switches: (spec factory, vocab size, src strategy, dst strategy).
 REPAD_CASES = [
     (small_llama3, 2300, PS(8, 2, 2), PS(8, 4, 1)),        # 2304 -> 2560, PP merge
@@ -229,3 +241,90 @@ def compare_numpy(table, groups, aux_groups, n_groups, src, dst):
             aux = dst[int(s["aux_buf"])].view(udt[eb])
             acc(int(ga), exp, _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"])).reshape(-1), eb)
     return out
+
+
+# Bit patterns written into destination arenas before a switch: every element the layout does not
+# store (rank alignment, bucket and parameter-start padding, shard alignment) must still hold them
+# afterwards.  Neither is a value the generator produces for its kind.
+CANARY32 = -559038737     # 0xDEADBEEF as int32
+CANARY16 = -16657         # 0xBEEF as int16
+
+
+def stored_runs(layout):
+    """([start, end) runs of the fp32 arenas, runs of the bf16 arena) holding state, merged and sorted.
+
+    The three fp32 arenas share one layout.  Everything outside the runs is padding."""
+    space = layout.space
+    r32, r16 = [], []
+    for g in sorted(layout.place):
+        vp = space.all_virtual_params[g]
+        r32 += [(h.offset, h.offset + h.hi - h.lo) for h in layout.fp32_holders(vp)]
+        r16 += [(h.offset, h.offset + h.hi - h.lo) for h in layout.bf16_holders(vp)]
+
+    def merge(runs):
+        out = []
+        for a, b in sorted(runs):
+            if b <= a:
+                continue
+            if out and a <= out[-1][1]:
+                assert a == out[-1][1], "two holders overlap"
+                out[-1][1] = max(out[-1][1], b)
+            else:
+                out.append([a, b])
+        return [tuple(r) for r in out]
+
+    return merge(r32), merge(r16)
+
+
+def fill_canaries(state):
+    """Write the canary into every element of a state's arenas (torch tensors, any device)."""
+    import torch
+
+    for t in (state.main, state.exp_avg, state.exp_avg_sq):
+        t.view(torch.int32).fill_(CANARY32)
+    state.param.view(torch.int16).fill_(CANARY16)
+
+
+def padding_damage(state, bf16=True):
+    """Number of padding elements of a state's arenas (the bf16 one only with ``bf16``) that no
+    longer hold the canary."""
+    import torch
+
+    r32, r16 = stored_runs(state.layout)
+    bad = 0
+    checks = [((state.main, state.exp_avg, state.exp_avg_sq), r32, CANARY32, torch.int32)]
+    if bf16:
+        checks.append(((state.param,), r16, CANARY16, torch.int16))
+    for arenas, runs, canary, dt in checks:
+        n = arenas[0].numel()
+        keep = torch.zeros(n, dtype=torch.bool, device=arenas[0].device)
+        for a, b in runs:
+            keep[a:b] = True
+        for t in arenas:
+            bad += int(torch.count_nonzero(~keep & (t.view(dt) != canary)))
+    return bad
+
+
+def perturb_per_rank(state_or_world, layout=None):
+    """Make every rank's fp32 shard distinct: XOR the low mantissa bits of rank g's elements of kind k
+    with (g * 3 + k + 1) & 0x7F.  Takes a TrainingState (device arenas, in place) or an Oracle-1 world
+    ({pid: {rank: OptInfo}}, in place), so that both sides start from the same per-rank values."""
+    import torch
+
+    def mask(g, k):
+        return (g * 3 + k + 1) & 0x7F
+
+    if isinstance(state_or_world, dict):
+        for infos in state_or_world.values():
+            for g, info in infos.items():
+                info.tensors = [(t.view(torch.int32) ^ mask(g, k)).view(torch.float32)
+                                for k, t in enumerate(info.tensors)]
+                info.orig = info.tensors
+        return
+    st = state_or_world
+    lay = st.layout
+    for g in range(lay.strategy.world_size):
+        a, b = lay.rank_fp32_slice(g)
+        for k, t in enumerate((st.main, st.exp_avg, st.exp_avg_sq)):
+            v = t.view(torch.int32)[a:b]
+            v.bitwise_xor_(mask(g, k))

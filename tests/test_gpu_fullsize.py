@@ -4,12 +4,20 @@ Every destination element is checked on the device against the seeded
 generator (its expected value is a closed form of (parameter, kind,
 full-tensor index)), the plan's own verification compares the destination
 with the source, and the switch back to the source layout must reproduce the
-source exactly (round trip = identity).  The CPU oracle cannot run a whole
-model at these sizes, but it runs one layer: for the transfer switches,
+source exactly (round trip = identity).  The destination starts filled with a
+canary pattern, and every element the layout does not store (padding) must
+still hold it afterwards.
+
+The CPU oracle cannot run a whole model at these sizes, but it runs the
+parameters where placement is hardest: the word embedding and the output
+layer (the largest tensors, whose DP shards cross bucket boundaries), the
+final norm, and the last transformer layer.  For the transfer switches
 Oracle-1 (the reference's three-pass executor, transfer.py:36-341, restated
-on CPU tensors) runs the parameters of the last transformer layer, about
-250M elements, and the GPU result must equal it bit for bit.  Peak memory is
-two layouts' worth of state.
+on CPU tensors) runs them; for the Group-ZeRO switch Oracle-1's redundant
+backup (transfer.py:343-388) does, after every source rank's shard has been
+made distinct so that the instance -> rank mapping shows.  The GPU's pieces
+of those parameters must equal the oracle bit for bit.  Peak memory is two
+layouts' worth of state.
 """
 
 import gc
@@ -23,6 +31,7 @@ from elasticmegatron_amd.megatron_manager.training_state import TrainingState
 from elasticmegatron_amd.resharding import model_spec as ms
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.transfer import TransferManager
+from tests.helpers import CANARY32, fill_canaries, padding_damage, perturb_per_rank
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -45,25 +54,27 @@ def _release():
     torch.cuda.empty_cache()
 
 
-def _check_layer_against_oracle1(spec, src, dst, layout, state, budget=250_000_000):
-    """Oracle-1 on the last transformer layer's parameters (in order, up to ``budget`` elements), and
-    the same pieces of the device state copied back, compared bit for bit."""
+ORACLE_NAMES = ("embedding.word_embeddings.weight", "decoder.final_layernorm.weight", "output_layer.weight")
+
+
+def _oracle_params(spec, budget=250_000_000):
+    """Ids of the word embedding, final norm and output layer, and of the last transformer layer's
+    parameters in order up to ``budget`` elements (Mixtral's experts exceed it)."""
     from oracle import model
-    from oracle import transfer as oracle1
-    from oracle.plan import Strat
-    from tests.helpers import compare
 
     inv = model.inventory(spec)
     last = spec.num_layers - 1
-    params, total = set(), 0
+    params, total = {p["id"] for p in inv if p["name"] in ORACLE_NAMES}, 0
+    layer = False
     for p in inv:
-        if p["layer"] == last and (not params or total + model.numel(p["shape"]) <= budget):
+        if p["layer"] == last and (not layer or total + model.numel(p["shape"]) <= budget):
             params.add(p["id"])
             total += model.numel(p["shape"])
-    S, D = Strat.of(src), Strat.of(dst)
-    world = oracle1.build_src_world(inv, spec, S, SEED, params)
-    dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
-    want32 = oracle1.flatten(dw)
+            layer = True
+    return inv, params
+
+
+def _device_pieces(layout, state, params, bf16=True):
     got32, gotbf = {}, {}
     space = layout.space
     for pid in params:
@@ -73,13 +84,58 @@ def _check_layer_against_oracle1(spec, src, dst, layout, state, budget=250_000_0
             got32[(h.rank, pid)] = {k: t[h.offset:h.offset + n].cpu().numpy()
                                     for k, t in zip(("main", "exp_avg", "exp_avg_sq"),
                                                     (state.main, state.exp_avg, state.exp_avg_sq))}
-        for h in layout.bf16_holders(vp):
-            n = h.hi - h.lo
-            gotbf[(layout.shard_keys[h.rank], pid)] = \
-                state.param[h.offset:h.offset + n].view(torch.int16).cpu().numpy().view(np.uint16)
-    print(f"oracle-1 on layer {last}: {len(params)} params, {total} elements", flush=True)
+        if bf16:
+            for h in layout.bf16_holders(vp):
+                n = h.hi - h.lo
+                gotbf[(layout.shard_keys[h.rank], pid)] = \
+                    state.param[h.offset:h.offset + n].view(torch.int16).cpu().numpy().view(np.uint16)
+    return got32, gotbf
+
+
+def _check_against_oracle1(spec, src, dst, layout, state):
+    """Oracle-1's transfer of the word embedding, final norm, output layer and last layer, against
+    the same pieces of the device state, bit for bit."""
+    from oracle import model
+    from oracle import transfer as oracle1
+    from oracle.plan import Strat
+    from tests.helpers import compare
+
+    inv, params = _oracle_params(spec)
+    S, D = Strat.of(src), Strat.of(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED, params)
+    dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
+    want32 = oracle1.flatten(dw)
+    del world, dw
+    got32, gotbf = _device_pieces(layout, state, params)
+    total = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
+    print(f"oracle-1: {len(params)} params, {total} elements", flush=True)
     assert got32 and gotbf
     assert compare(got32, gotbf, want32, dbf) == []
+
+
+def _check_backup_against_oracle1(spec, src, dst, a, b, tm, plan, scale_up):
+    """Oracle-1's redundant backup from a source whose ranks hold distinct shards, against the
+    device.  The source and destination are restored afterwards."""
+    from oracle import model
+    from oracle import transfer as oracle1
+    from oracle.plan import Strat
+    from tests.helpers import compare
+
+    perturb_per_rank(a)
+    tm.execute(plan, a, b)
+    inv, params = _oracle_params(spec)
+    S, D = Strat.of(src), Strat.of(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED, params)
+    perturb_per_rank(world)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, world, scale_up, params))
+    del world
+    got, _ = _device_pieces(b.layout, b, params, bf16=False)
+    total = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
+    print(f"oracle-1 redundant backup: {len(params)} params, {total} elements", flush=True)
+    assert got
+    assert compare(got, {}, want, {}) == []
+    perturb_per_rank(a)  # XOR again: the seeded values are back
+    tm.execute(plan, a, b)
 
 
 @pytest.mark.parametrize("factory,src,dst,repad", [p if len(p.values) == 4 else
@@ -106,13 +162,22 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
         a = TrainingState.allocate(ls, gpu_device)
         b = TrainingState.allocate(ld, gpu_device, param=a.param if backup is not None else None)
         a.fill_synthetic(SEED)
+        if backup is None:
+            fill_canaries(b)
+        else:  # the bf16 arena is shared with the source: only the fp32 arenas start as canaries
+            for t in (b.main, b.exp_avg, b.exp_avg_sq):
+                t.view(torch.int32).fill_(CANARY32)
         tm.execute(fwd, a, b)
         bad, first = b.verify_synthetic(SEED, vocab_rows=vocab_rows)
         assert bad == 0, first
+        assert padding_damage(b, bf16=backup is None) == 0, "padding was written"
         report = tm.verify(a, b, kind)  # the plan's own check, against the source state
         assert report.bit_exact, report.lines()[:5]
         if kind == "transfer" and not repad:  # the reference keeps the padded vocabulary fixed
-            _check_layer_against_oracle1(spec, src, dst, ld, b)
+            _check_against_oracle1(spec, src, dst, ld, b)
+        elif backup is not None:
+            _check_backup_against_oracle1(spec, src, dst, a, b, tm, fwd, backup)
+            assert b.verify_synthetic(SEED)[0] == 0
         # Round trip into fresh storage: must reproduce every source element.
         param = a.param
         del a

@@ -68,3 +68,68 @@ def test_captured_reshard_replays_bit_exact(gpu_device, per_tensor):
     torch.cuda.synchronize()
     bad, first = b.verify_synthetic(SEED + 1)
     assert bad == 0, first
+
+
+def test_capture_refuses_calls_that_would_allocate(gpu_device):
+    """A first call on the device (table upload) or a call whose base pointers differ from the
+    plan's first call (its own pointer table) cannot be replayed from a graph: under capture it
+    fails with EMRS_ERR_CAPTURE and records nothing; the same calls run eagerly afterwards."""
+    from elasticmegatron_amd import _native
+
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 1, 1)), space.layout(PS(8, 4, 1))
+    space.register_reshard(ls.strategy, ld.strategy)
+    tm = TransferManager()
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    b2 = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    tm.execute(tm.compile(ls, ld), a, b2)   # the library has met the device outside any capture
+    plan = tm.compile_tensors(ls, ld)
+    assert len(plan.src) > 128   # the pointer-table path
+    src_v, dst_v, dst2_v = plan.src.views(a), plan.dst.views(b), plan.dst.views(b2)
+    for st in (b, b2):
+        _scramble(st)
+    marker = torch.zeros(1, device=gpu_device)  # each graph records one fill, so it is not empty
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    print("case capture of a first call", flush=True)
+    with torch.cuda.graph(graph):
+        marker.fill_(1.0)
+        with pytest.raises(_native.EmrsError) as e:
+            tm.execute_tensors(plan, src_v, dst_v)
+    assert e.value.code == -9 and "capturing" in str(e.value)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] > 0   # nothing was recorded
+
+    tm.execute_tensors(plan, src_v, dst_v)   # eager first call: tables for these bases
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] == 0
+
+    graph2 = torch.cuda.CUDAGraph()
+    print("case capture with other base pointers", flush=True)
+    with torch.cuda.graph(graph2):
+        marker.fill_(2.0)
+        with pytest.raises(_native.EmrsError) as e:
+            tm.execute_tensors(plan, src_v, dst2_v)
+    assert e.value.code == -9
+    graph2.replay()
+    torch.cuda.synchronize()
+    assert b2.verify_synthetic(SEED)[0] > 0
+    tm.execute_tensors(plan, src_v, dst2_v)  # eagerly, a stream-ordered table of its own
+    torch.cuda.synchronize()
+    assert b2.verify_synthetic(SEED)[0] == 0
+
+    # The compare entry point allocates: refused under capture as well.
+    graph3 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph3):
+        marker.fill_(3.0)
+        with pytest.raises(_native.EmrsError) as e:
+            tm.verify(a, b)
+    assert e.value.code == -9
+    graph3.replay()
+    torch.cuda.synchronize()
+    assert float(marker) == 3.0
+    assert tm.verify(a, b).bit_exact

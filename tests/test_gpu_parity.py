@@ -17,8 +17,8 @@ from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.transfer import TransferManager
 from oracle import model
 from oracle import transfer as oracle1
-from tests.helpers import (REPAD_CASES, SEED, SMALL_CASES, bf16_rne_bits, compare, extract, new_arenas,
-                           piece_fill_numpy, repad_spaces, strat)
+from tests.helpers import (REPAD_CASES, SEED, SMALL_CASES, bf16_rne_bits, compare, extract, fill_canaries,
+                           new_arenas, padding_damage, piece_fill_numpy, repad_spaces, strat)
 
 pytestmark = pytest.mark.gpu
 
@@ -69,11 +69,11 @@ def test_kernel_matches_oracle1(gpu_device, factory, src, dst, bf16_source):
     a = TrainingState.allocate(ls, gpu_device)
     b = TrainingState.allocate(ld, gpu_device)
     a.fill_synthetic(SEED)
-    for t in b.arenas():
-        t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
+    fill_canaries(b)  # every stored element must be overwritten, every padding element kept
     tm = TransferManager(check_disjoint=True, bf16_source=bf16_source)
     tm.transfer_optimizer_tensors(space, a, b)
     got32, gotbf = extract(ld, _host_arenas(b))
+    assert padding_damage(b) == 0
 
     inv = model.inventory(spec)
     S, D = strat(src), strat(dst)

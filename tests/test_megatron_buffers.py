@@ -1,0 +1,88 @@
+"""MegatronBuffers: the per-tensor views of Megatron-shaped flat buffers, on the CPU.
+
+Each (rank, parameter, kind) piece must sit in its rank's flat shard where the
+distributed optimizer keeps it (bucket shard prefix + the piece's offset in
+its bucket shard), and each bf16 parameter at its ``param_index_map`` start of
+its shard's flat param buffer: both derived here from the oracle's own
+restatement of Megatron's buffer rules, not from the product's layout.  The
+views must not overlap, and what they leave uncovered is exactly the padding.
+"""
+
+import pytest
+import torch
+
+from elasticmegatron_amd import ParallelStrategy as PS
+from elasticmegatron_amd.resharding.megatron_buffers import MegatronBuffers
+from elasticmegatron_amd.resharding.tensors import TensorBuffers
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from oracle import megatron_buffer, model
+from oracle.plan import stage, tp_size, local_shape
+from tests.helpers import small_llama2, small_mixtral, small_ragged, strat
+
+CASES = [(small_llama2, PS(8, 2, 2)), (small_mixtral, PS(8, 1, 1, expert_model_parallel_size=4)),
+         (small_ragged, PS(6, 1, 1)), (small_ragged, PS(8, 4, 1))]
+
+
+@pytest.mark.parametrize("factory,ps", CASES, ids=lambda x: getattr(x, "__name__", str(x))[:40])
+def test_views_sit_where_megatron_keeps_them(factory, ps):
+    spec = factory()
+    space = build_virtual_model(spec)
+    lay = space.layout(ps)
+    mb = MegatronBuffers(lay)
+    tb = TensorBuffers(lay)
+    bufs = {k: torch.zeros(n, dtype=torch.int16 if d == "bf16" else torch.int32) for k, d, n in mb.specs}
+    views = mb.tensor_views(tb, bufs)
+    # No two views overlap; record where each lies.
+    where = {}
+    for key, v in zip(tb.keys, views):
+        buf = next(k for k, t in bufs.items() if t.untyped_storage().data_ptr() == v.untyped_storage().data_ptr())
+        v += 1
+        where[key] = (buf, v.storage_offset())
+    for t in bufs.values():
+        assert int(t.max()) <= 1
+
+    # Expected positions from the oracle's restatement of the buffer rules.
+    S = strat(ps)
+    inv = model.inventory(spec)
+    byname = {p["name"]: p for p in inv}
+    for key, (buf, off) in where.items():
+        p = byname[key[2]]
+        s = stage(p, S.pp, spec.num_layers)
+        stage_params = [q for q in inv if stage(q, S.pp, spec.num_layers) == s and
+                        (q["expert"] is None) == (p["expert"] is None)]
+        if p["expert"] is not None:   # EP rank 0's experts define the expert buffer
+            per = spec.num_experts // S.ep
+            ep = p["expert"] // per
+            stage_params = [q for q in stage_params if q["expert"] // per == 0]
+            idx = [q for q in inv if stage(q, S.pp, spec.num_layers) == s and q["expert"] is not None
+                   and q["expert"] // per == ep].index(p)
+            dp = S.edp
+        else:
+            idx = stage_params.index(p)
+            dp = S.pdp * S.cp
+        numels = [model.numel(local_shape(q, tp_size(S, q))) for q in stage_params]
+        bucket = None if (s > 0 or not spec.overlap_grad_reduce) else spec.ddp_bucket_size
+        ranges, buckets = megatron_buffer.layout(numels, dp, bucket,
+                                                 shared=[q.get("shared", False) for q in stage_params])
+        if key[0] == "param":
+            assert buf == ("param", key[1]) and off == ranges[idx][0], key
+            continue
+        g = key[1]
+        part = "expert" if p["expert"] is not None else "dense"
+        assert buf == (key[0], g, part), key
+        # The rank's DP rank in this buffer, and the bucket shard holding the piece's start.
+        h = next(h for h in lay.fp32_holders(space.all_virtual_params[p["id"]]) if h.rank == g)
+        dpr = [r for r, (lo, hi) in megatron_buffer.distribution(
+            numels, dp, bucket, shared=[q.get("shared", False) for q in stage_params])[idx].items()
+            if lo == h.lo and hi == h.hi]
+        assert len(dpr) == 1, key
+        prefix = 0
+        for bs, be, members in buckets:
+            sz = (be - bs) // dp
+            if idx in members:
+                assert off == prefix + ranges[idx][0] + h.lo - (bs + dpr[0] * sz), key
+                break
+            prefix += sz
+    # Uncovered elements are exactly the padding: buffer sizes minus stored elements.
+    stored = sum(int(t.sum()) for t in bufs.values())
+    assert stored == sum(tb.numel)
