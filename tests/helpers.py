@@ -285,9 +285,21 @@ def fill_canaries(state):
     state.param.view(torch.int16).fill_(CANARY16)
 
 
+def padding_gaps(runs, n):
+    """The [start, end) ranges of [0, n) outside the sorted, merged ``runs``."""
+    gaps, at = [], 0
+    for a, b in runs:
+        if a > at:
+            gaps.append((at, a))
+        at = b
+    if at < n:
+        gaps.append((at, n))
+    return gaps
+
+
 def padding_damage(state, bf16=True):
     """Number of padding elements of a state's arenas (the bf16 one only with ``bf16``) that no
-    longer hold the canary."""
+    longer hold the canary.  Only the gaps are read, so full-size arenas need no mask."""
     import torch
 
     r32, r16 = stored_runs(state.layout)
@@ -296,12 +308,9 @@ def padding_damage(state, bf16=True):
     if bf16:
         checks.append(((state.param,), r16, CANARY16, torch.int16))
     for arenas, runs, canary, dt in checks:
-        n = arenas[0].numel()
-        keep = torch.zeros(n, dtype=torch.bool, device=arenas[0].device)
-        for a, b in runs:
-            keep[a:b] = True
-        for t in arenas:
-            bad += int(torch.count_nonzero(~keep & (t.view(dt) != canary)))
+        for a, b in padding_gaps(runs, arenas[0].numel()):
+            for t in arenas:
+                bad += int(torch.count_nonzero(t.view(dt)[a:b] != canary))
     return bad
 
 
