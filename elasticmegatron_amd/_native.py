@@ -29,16 +29,19 @@ ERRORS = {
     -7: "EMRS_ERR_TOO_MANY_BUFFERS",
     -8: "EMRS_ERR_ALIAS",
     -9: "EMRS_ERR_CAPTURE",
+    -10: "EMRS_ERR_TOO_LARGE",
 }
 EMRS_PLAN_CHECK_DISJOINT = 1
 EMRS_MAX_BUFFERS = 65535
 EMRS_ARG_BUFFERS = 128  # buffers per side passed in kernel arguments (more use a device table)
+EMRS_STATIC_SCRATCH_BYTES = 4 << 20  # device scratch of emrs_plan_compare_static
 
 # Every function include/emrs.h declares.
 EXPORTS = (
     "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
     "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
     "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare", "emrs_xor_checksum",
+    "emrs_plan_compare_static",
 )
 
 # struct emrs_compare_stats
@@ -104,6 +107,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_synth_verify.argtypes = [P, U64, P, P, U32, U64, P, ctypes.POINTER(U64), ctypes.POINTER(U64)]
     lib.emrs_plan_compare.restype = I
     lib.emrs_plan_compare.argtypes = [P, P, P, P, P, U32, P, P]
+    lib.emrs_plan_compare_static.restype = I
+    lib.emrs_plan_compare_static.argtypes = [P, P, P, P, P, U32, P, P]
     lib.emrs_xor_checksum.restype = I
     lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
     if lib.emrs_abi_version() != 5:
@@ -179,11 +184,14 @@ class Plan:
         _check(rc, "emrs_plan_execute")
 
     def compare(self, src_ptrs: Sequence[int], dst_ptrs: Sequence[int], groups: Optional[np.ndarray] = None,
-                aux_groups: Optional[np.ndarray] = None, n_groups: int = 1, stream: int = 0) -> np.ndarray:
+                aux_groups: Optional[np.ndarray] = None, n_groups: int = 1, stream: int = 0,
+                no_alloc: bool = False) -> np.ndarray:
         """emrs_plan_compare: per group, how the destination differs from what the plan writes.
 
         ``groups`` / ``aux_groups`` hold one group id per input segment.
         Returns ``n_groups`` records of :data:`COMPARE_DTYPE`.  Waits for ``stream``.
+        ``no_alloc``: run emrs_plan_compare_static, which allocates no device memory (its
+        working set must fit in EMRS_STATIC_SCRATCH_BYTES).
         """
         if len(src_ptrs) != self.n_src or len(dst_ptrs) != self.n_dst:
             raise ValueError("wrong number of base pointers")
@@ -198,11 +206,12 @@ class Plan:
                 raise ValueError(f"need one group id per segment ({n_in})")
             arrs.append(g)
         out = np.zeros(max(1, n_groups), dtype=COMPARE_DTYPE)
-        rc = load().emrs_plan_compare(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
-                                      arrs[0].ctypes.data if arrs[0] is not None and n_in else None,
-                                      arrs[1].ctypes.data if arrs[1] is not None and n_in else None,
-                                      int(n_groups), out.ctypes.data, ctypes.c_void_p(int(stream)))
-        _check(rc, "emrs_plan_compare")
+        fn = load().emrs_plan_compare_static if no_alloc else load().emrs_plan_compare
+        rc = fn(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
+                arrs[0].ctypes.data if arrs[0] is not None and n_in else None,
+                arrs[1].ctypes.data if arrs[1] is not None and n_in else None,
+                int(n_groups), out.ctypes.data, ctypes.c_void_p(int(stream)))
+        _check(rc, "emrs_plan_compare_static" if no_alloc else "emrs_plan_compare")
         return out
 
     def close(self) -> None:

@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -36,6 +37,12 @@
 namespace {
 thread_local std::string g_last_error;
 }  // namespace
+
+// Device scratch of emrs_plan_compare_static, the entry point that allocates
+// nothing: its accumulators, group ids, segment table and pointer table.  Each
+// device holds its own copy for the life of the process; host code reaches it
+// only through the address hipGetSymbolAddress returns on that device.
+static __device__ __align__(256) unsigned char scratch[EMRS_STATIC_SCRATCH_BYTES];
 
 namespace emrs_internal {
 int fail(int code, const std::string &msg) {
@@ -1161,6 +1168,127 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
   if (open) flush_block(m, x, cur_g, cur_ga, cur_aux, acc, lds_d, lds_u, lds_f);
 }
 
+// Zero n 32-bit words (accumulators are cleared by a kernel rather than a memset).
+__global__ void clear_words_kernel(uint32_t *p, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// What both comparison entry points prepare on the host: checked bases, the
+// groups of every device segment, and the element counts per group.
+struct CompareJob {
+  ResolvedBases rb;
+  std::vector<uint32_t> g_host;  // per device segment: its group, then its aux group
+  int cus = 0;
+  int resident = 0;              // compare_plan_kernel workgroups per CU
+};
+
+int compare_setup(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
+                  const uint32_t *aux_groups, uint32_t n_groups, emrs_compare_stats *stats, CompareJob *job) {
+  if (!plan || !stats) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (n_groups == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, "n_groups must be >= 1");
+  const uint64_t n_in = plan->stats.n_segments;
+  for (uint64_t i = 0; i < n_in; ++i)
+    if ((groups && groups[i] >= n_groups) || (aux_groups && aux_groups[i] >= n_groups))
+      return fail(EMRS_ERR_INVALID_ARGUMENT, "group id >= n_groups");
+  int rc = resolve_bases(plan, src_bases, dst_bases, &job->rb);
+  if (rc) return rc;
+  const size_t nd = plan->segs.size();
+  job->g_host.resize(2 * nd);
+  std::vector<uint64_t> elements(n_groups, 0);
+  for (size_t k = 0; k < nd; ++k) {
+    const DevSeg &d = plan->segs[k];
+    const uint32_t o = plan->origin[k];
+    const uint32_t g = groups ? groups[o] : 0, ga = aux_groups ? aux_groups[o] : g;
+    job->g_host[k] = g;
+    job->g_host[nd + k] = ga;
+    const uint64_t units = (uint64_t)d.len * d.rows;
+    elements[g] += units << (d.unit_log2() - d.elem_log2());
+    if (d.ops() & 1) elements[ga] += units << (d.unit_log2() - 2);
+    if (d.ops() & 4) elements[ga] += units << (d.unit_log2() - d.elem_log2());
+  }
+  for (uint32_t g = 0; g < n_groups; ++g) {
+    stats[g] = emrs_compare_stats{};
+    stats[g].elements = elements[g];
+  }
+  return EMRS_OK;
+}
+
+// The current device, its CU count and the compare kernel's residency.
+int compare_device(CompareJob *job, int *dev) {
+  int resident_nt = 0, resident_t = 0;
+  int rc = current_device(dev, &job->cus, &resident_nt, &resident_t);
+  if (rc) return rc;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&job->resident, compare_plan_kernel<false>, kThreads, 0) !=
+          hipSuccess ||
+      job->resident <= 0) {
+    (void)hipGetLastError();
+    job->resident = 4;
+  }
+  return EMRS_OK;
+}
+
+// A persistent grid of resident workgroups, a multiple of 8 (one eighth of
+// the plan per XCD), in runs of up to 32 steps: at most a quarter of each
+// workgroup's share, so that small plans still spread out.
+hipError_t compare_launch(const emrs_plan *plan, const CompareJob &job, const DevSeg *table, const uint32_t *grp,
+                          const uint64_t *tab, GroupAcc *acc, hipStream_t st) {
+  const size_t nd = plan->segs.size();
+  uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)job.cus * (uint32_t)job.resident);
+  blocks = std::max<uint64_t>(8, blocks / 8 * 8);
+  const uint32_t run =
+      (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32 * kUnroll, plan->n_chunks / (blocks * 4)));
+  const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
+  if (job.rb.table)
+    hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
+                       grp + nd, (uint32_t)nd, plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
+  else
+    hipLaunchKernelGGL(compare_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
+                       grp + nd, (uint32_t)nd, plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
+  return hipGetLastError();
+}
+
+void compare_finish(const std::vector<GroupAcc> &host, emrs_compare_stats *stats) {
+  for (size_t g = 0; g < host.size(); ++g) {
+    stats[g].mismatches = host[g].mismatches;
+    stats[g].nonfinite = host[g].nonfinite;
+    stats[g].sum_sq_diff = host[g].sum_sq_diff;
+    stats[g].sum_sq_expected = host[g].sum_sq_expected;
+    uint32_t ma = host[g].max_abs_bits, mr = host[g].max_rel_bits;
+    memcpy(&stats[g].max_abs_diff, &ma, 4);
+    memcpy(&stats[g].max_rel_diff, &mr, 4);
+  }
+}
+
+// Per device: the address of `scratch` (the array's host-side name is not a
+// device address), looked up once with that device current, and the mutex
+// that serialises the calls sharing it.
+std::mutex g_scratch_mu;
+std::vector<unsigned char *> g_scratch_ptr;
+std::vector<std::unique_ptr<std::mutex>> g_scratch_call_mu;
+
+int scratch_of(int dev, unsigned char **out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(EMRS_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = static_cast<unsigned char *>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return EMRS_OK;
+}
+
+std::mutex *scratch_call_mutex(int dev) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  while ((int)g_scratch_call_mu.size() <= dev) g_scratch_call_mu.emplace_back(new std::mutex);
+  return g_scratch_call_mu[dev].get();
+}
+
 }  // namespace
 
 extern "C" {
@@ -1443,39 +1571,11 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
 int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
                       const uint32_t *aux_groups, uint32_t n_groups, emrs_compare_stats *stats, void *stream) {
   g_last_error.clear();
-  if (!plan || !stats) return fail(EMRS_ERR_INVALID_ARGUMENT, "NULL argument");
-  if (n_groups == 0) return fail(EMRS_ERR_INVALID_ARGUMENT, "n_groups must be >= 1");
-  const uint64_t n_in = plan->stats.n_segments;
-  for (uint64_t i = 0; i < n_in; ++i)
-    if ((groups && groups[i] >= n_groups) || (aux_groups && aux_groups[i] >= n_groups))
-      return fail(EMRS_ERR_INVALID_ARGUMENT, "group id >= n_groups");
-  ResolvedBases rb;
-  int rc = resolve_bases(plan, src_bases, dst_bases, &rb);
-  if (rc) return rc;
-
-  // Per device segment: its groups, and the element counts on the host.
-  const size_t nd = plan->segs.size();
-  std::vector<uint32_t> g_host(2 * nd);
-  std::vector<uint64_t> elements(n_groups, 0);
-  for (size_t k = 0; k < nd; ++k) {
-    const DevSeg &d = plan->segs[k];
-    const uint32_t o = plan->origin[k];
-    const uint32_t g = groups ? groups[o] : 0, ga = aux_groups ? aux_groups[o] : g;
-    g_host[k] = g;
-    g_host[nd + k] = ga;
-    const uint64_t units = (uint64_t)d.len * d.rows;
-    elements[g] += units << (d.unit_log2() - d.elem_log2());
-    if (d.ops() & 1) elements[ga] += units << (d.unit_log2() - 2);
-    if (d.ops() & 4) elements[ga] += units << (d.unit_log2() - d.elem_log2());
-  }
-  for (uint32_t g = 0; g < n_groups; ++g) {
-    stats[g] = emrs_compare_stats{};
-    stats[g].elements = elements[g];
-  }
-  if (plan->n_chunks == 0) return EMRS_OK;
-
-  int dev = 0, cus = 0, resident_nt = 0, resident_t = 0;
-  rc = current_device(&dev, &cus, &resident_nt, &resident_t);
+  CompareJob job;
+  int rc = compare_setup(plan, src_bases, dst_bases, groups, aux_groups, n_groups, stats, &job);
+  if (rc || plan->n_chunks == 0) return rc;
+  int dev = 0;
+  rc = compare_device(&job, &dev);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   // The comparison allocates its accumulators and waits for the stream.
@@ -1484,16 +1584,9 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   DevSeg *table = nullptr;
   rc = device_table(plan, dev, st, &table);
   if (rc) return rc;
-  int resident_cmp = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident_cmp, compare_plan_kernel<false>, kThreads, 0) !=
-          hipSuccess ||
-      resident_cmp <= 0) {
-    (void)hipGetLastError();
-    resident_cmp = 4;
-  }
 
   const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
-  const size_t grp_bytes = g_host.size() * sizeof(uint32_t);
+  const size_t grp_bytes = job.g_host.size() * sizeof(uint32_t);
   char *buf = nullptr;
   hipError_t e = hipMalloc(&buf, acc_bytes + grp_bytes);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(compare buffers)");
@@ -1501,43 +1594,80 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   uint32_t *grp = reinterpret_cast<uint32_t *>(buf + acc_bytes);
   std::vector<GroupAcc> host(n_groups);
   e = hipMemsetAsync(acc, 0, acc_bytes, st);
-  if (e == hipSuccess) e = hipMemcpyAsync(grp, g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(grp, job.g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
   uint64_t *tab = nullptr;
   bool tab_owned = false;
   int table_rc = EMRS_OK;  // a pointer-table failure keeps its own message
-  if (e == hipSuccess) table_rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
-  if (e == hipSuccess && table_rc == EMRS_OK) {
-    // A persistent grid of resident workgroups, a multiple of 8 (one eighth
-    // of the plan per XCD), in runs of up to 32 chunks: at most a quarter of
-    // each workgroup's share, so that small plans still spread out.
-    uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)cus * (uint32_t)resident_cmp);
-    blocks = std::max<uint64_t>(8, blocks / 8 * 8);
-    const uint32_t run =
-        (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32 * kUnroll, plan->n_chunks / (blocks * 4)));
-    const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
-    if (rb.table)
-      hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                         grp + nd, (uint32_t)nd, plan->n_chunks, run, rb.src, rb.dst, tab, dtab, acc);
-    else
-      hipLaunchKernelGGL(compare_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                         grp + nd, (uint32_t)nd, plan->n_chunks, run, rb.src, rb.dst, tab, dtab, acc);
-    e = hipGetLastError();
-  }
+  if (e == hipSuccess) table_rc = pointer_table(plan, dev, job.rb, st, &tab, &tab_owned);
+  if (e == hipSuccess && table_rc == EMRS_OK) e = compare_launch(plan, job, table, grp, tab, acc, st);
   if (tab_owned) (void)hipFreeAsync(tab, st);
   if (e == hipSuccess && table_rc == EMRS_OK) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   (void)hipFree(buf);
   if (table_rc != EMRS_OK) return table_rc;
   if (e != hipSuccess) return hip_fail(e, "compare_plan_kernel");
-  for (uint32_t g = 0; g < n_groups; ++g) {
-    stats[g].mismatches = host[g].mismatches;
-    stats[g].nonfinite = host[g].nonfinite;
-    stats[g].sum_sq_diff = host[g].sum_sq_diff;
-    stats[g].sum_sq_expected = host[g].sum_sq_expected;
-    uint32_t ma = host[g].max_abs_bits, mr = host[g].max_rel_bits;
-    memcpy(&stats[g].max_abs_diff, &ma, 4);
-    memcpy(&stats[g].max_rel_diff, &mr, 4);
+  compare_finish(host, stats);
+  return EMRS_OK;
+}
+
+int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
+                             const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,
+                             emrs_compare_stats *stats, void *stream) {
+  g_last_error.clear();
+  CompareJob job;
+  int rc = compare_setup(plan, src_bases, dst_bases, groups, aux_groups, n_groups, stats, &job);
+  if (rc || plan->n_chunks == 0) return rc;
+  // Everything the kernel reads or writes beyond the caller's buffers lives in `scratch`, in
+  // 256-byte aligned regions: accumulators, group ids, the segment table, the pointer table.
+  const size_t nd = plan->segs.size();
+  const size_t acc_bytes = align256((size_t)n_groups * sizeof(GroupAcc));
+  const size_t grp_bytes = align256(job.g_host.size() * sizeof(uint32_t));
+  const size_t seg_bytes = align256(nd * sizeof(DevSeg));
+  const size_t ptr_bytes = job.rb.table ? align256(job.rb.ptrs.size() * sizeof(uint64_t)) : 0;
+  const size_t need = acc_bytes + grp_bytes + seg_bytes + ptr_bytes;
+  if (need > EMRS_STATIC_SCRATCH_BYTES) {
+    char msg[200];
+    snprintf(msg, sizeof msg,
+             "the comparison needs %zu bytes of scratch (%zu segments, %u groups); the allocation-free "
+             "entry point holds at most %u: use emrs_plan_compare",
+             need, nd, n_groups, (unsigned)EMRS_STATIC_SCRATCH_BYTES);
+    return fail(EMRS_ERR_TOO_LARGE, msg);
   }
+  int dev = 0;
+  rc = compare_device(&job, &dev);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = refuse_capture(st, "emrs_plan_compare_static");  // it waits for the stream
+  if (rc) return rc;
+  unsigned char *base = nullptr;
+  rc = scratch_of(dev, &base);
+  if (rc) return rc;
+
+  // One call at a time per device: the array is shared by every call on it.
+  std::lock_guard<std::mutex> lk(*scratch_call_mutex(dev));
+  GroupAcc *acc = reinterpret_cast<GroupAcc *>(base);
+  uint32_t *grp = reinterpret_cast<uint32_t *>(base + acc_bytes);
+  DevSeg *table = reinterpret_cast<DevSeg *>(base + acc_bytes + grp_bytes);
+  uint64_t *tab = job.rb.table ? reinterpret_cast<uint64_t *>(base + acc_bytes + grp_bytes + seg_bytes) : nullptr;
+  // The previous call's accumulators are still there: clear them with a kernel (no memset node).
+  const uint64_t acc_words = (uint64_t)n_groups * sizeof(GroupAcc) / sizeof(uint32_t);
+  hipLaunchKernelGGL(clear_words_kernel, dim3((uint32_t)std::min<uint64_t>(1024, (acc_words + 255) / 256)),
+                     dim3(256), 0, st, reinterpret_cast<uint32_t *>(acc), acc_words);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(grp, job.g_host.data(), job.g_host.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(table, plan->segs.data(), nd * sizeof(DevSeg), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess && tab)
+    e = hipMemcpyAsync(tab, job.rb.ptrs.data(), job.rb.ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = compare_launch(plan, job, table, grp, tab, acc, st);
+  std::vector<GroupAcc> host(n_groups);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(host.data(), acc, (size_t)n_groups * sizeof(GroupAcc), hipMemcpyDeviceToHost, st);
+  // The host copies above read job's and plan's vectors: wait before they can go.
+  const hipError_t se = hipStreamSynchronize(st);
+  if (e == hipSuccess) e = se;
+  if (e != hipSuccess) return hip_fail(e, "compare_plan_kernel (static scratch)");
+  compare_finish(host, stats);
   return EMRS_OK;
 }
 

@@ -58,6 +58,7 @@ extern "C" {
 #define EMRS_ERR_TOO_MANY_BUFFERS (-7)
 #define EMRS_ERR_ALIAS (-8)
 #define EMRS_ERR_CAPTURE (-9) /* the call would allocate or upload while its stream captures a graph */
+#define EMRS_ERR_TOO_LARGE (-10) /* the call needs more than the static scratch of emrs_plan_compare_static */
 
 /* Maximum number of source (and, separately, destination) buffers.  Up to
  * 128 per side travel in kernel arguments; a plan with more on either side
@@ -214,6 +215,28 @@ typedef struct emrs_compare_stats {
 int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
                       const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,
                       emrs_compare_stats *stats, void *stream);
+
+/*
+ * emrs_plan_compare without any allocation.  No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device
+ * memory (tight verification loops of an elastic controller, harnesses that
+ * forbid hipMalloc).  Same arguments, checks and results as
+ * emrs_plan_compare, but it calls no hipMalloc, hipFree or allocating
+ * library routine: its accumulators, group ids, the plan's segment table and
+ * (beyond 128 buffers a side) its pointer table are staged in a static device
+ * array of EMRS_STATIC_SCRATCH_BYTES that every device holds until the
+ * process ends.  A comparison that needs more (about 50,000 device segments
+ * with few groups) returns EMRS_ERR_TOO_LARGE and does nothing.  The array is
+ * shared by every call on a device and keeps the last call's contents; the
+ * accumulators are cleared at the start of each call.  The library serialises
+ * the calls of one process on one device, and each call waits for `stream`
+ * before it returns, so calls never overlap in their use of the array.  Not
+ * for capture into a graph (EMRS_ERR_CAPTURE).
+ */
+#define EMRS_STATIC_SCRATCH_BYTES (4u << 20)
+int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
+                             const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,
+                             emrs_compare_stats *stats, void *stream);
 
 /*
  * Launch-shape knobs of emrs_plan_execute, process-wide.  Results never
