@@ -81,7 +81,9 @@ def parse():
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
-                    help="one workgroup per chunk of 256 units: lanes per workgroup (0: the default, 64)")
+                    help="one workgroup per piece of a chunk of 256 units: lanes per workgroup (0: the default, 64)")
+    ap.add_argument("--units", type=int, default=0, choices=(0, 1, 2, 4),
+                    help="16-byte units per lane (0: a whole chunk per workgroup, 256 / lanes)")
     ap.add_argument("--persistent", type=int, default=0,
                     help="0: one workgroup per chunk of 256 units; 1: persistent grid (the next three flags)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
@@ -97,44 +99,62 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(spec_fn, src, dst, backup, target_s=10.0, max_reps=25, full_payload=0):
-    """Oracle-1 (the reference's three-pass executor restated on CPU torch tensors) on layer 0."""
+def cpu_baseline(spec, ls, src, dst, backup, a):
+    """Oracle-1 (the reference's three-pass executor restated on CPU torch tensors) on every
+    parameter of the switch, one parameter at a time, on all of the host's cores.
+
+    Each parameter's source pieces are copied from the device state ``a`` (the seeded values;
+    outside the timed region, as the reference's Timer scopes only the executor), then the
+    oracle's passes for that parameter are timed.  The parameters' times add up to the whole
+    switch, as the reference's loop over parameters does (transfer.py:291-341)."""
     import torch
 
     from oracle import model
     from oracle import transfer as oracle1
-    from oracle.plan import Strat
+    from oracle.plan import Strat, dp_distributions, local_shape, tp_size
 
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
-    spec = spec_fn()
     inv = model.inventory(spec)
-    params = {p["id"] for p in inv if p["layer"] == 0}
     S, D = Strat.of(src), Strat.of(dst)
-    world0 = oracle1.build_src_world(inv, spec, S, SEED, params)
-    total_t, total_b, reps = 0.0, 0, 0
-    while reps < max_reps and (total_t < target_s or reps == 0):
-        world = {pid: {g: oracle1.OptInfo([t.clone() for t in i.tensors], i.rng, i.model_shape)
-                       for g, i in infos.items()} for pid, infos in world0.items()}
+    sd, dd = dp_distributions(inv, S, spec), dp_distributions(inv, D, spec)
+    space = ls.space
+    total_t = total_b = copy_t = 0.0
+    l0_t = l0_b = 0.0
+    n_params = n_elems = 0
+    for p in inv:
+        pid = p["id"]
+        if pid not in sd:
+            continue
+        vp = space.all_virtual_params[pid]
+        shape = local_shape(p, tp_size(S, p))
         t0 = time.perf_counter()
+        world = {pid: {h.rank: oracle1.OptInfo([t[h.offset:h.offset + h.hi - h.lo].cpu()
+                                                for t in (a.main, a.exp_avg, a.exp_avg_sq)], (h.lo, h.hi), shape)
+                       for h in ls.fp32_holders(vp)}}
+        t1 = time.perf_counter()
         if backup is None:
-            dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
+            dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, {pid}, dists=(sd, dd))
         else:
-            dw, dbf = oracle1.redundant_backup(inv, spec, S, D, world, backup), {}
-        total_t += time.perf_counter() - t0
-        total_b += sum((i.rng[1] - i.rng[0]) * 12 for infos in dw.values() for i in infos.values())
-        total_b += sum(a.size * 2 for a in dbf.values())
-        reps += 1
-    n = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
-    rate = total_b / total_t
-    out = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-           "sample": f"transformer layer 0 ({len(params)} params, {n} elements) of the same switch, "
-                     f"executed {reps}x: {total_b / 1e9:.1f} GB payload in {total_t:.1f} s; "
-                     f"torch CPU threads={cores}",
-           "ms_per_rep": round(total_t / reps * 1e3, 2), "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
-    if full_payload:
-        out["full_switch_ms_at_this_rate"] = round(full_payload / rate * 1e3, 1)
-    return out
+            dw, dbf = oracle1.redundant_backup(inv, spec, S, D, world, backup, {pid}, dist=dd), {}
+        t2 = time.perf_counter()
+        nb = sum((i.rng[1] - i.rng[0]) * 12 for infos in dw.values() for i in infos.values())
+        nb += sum(x.size * 2 for x in dbf.values())
+        copy_t += t1 - t0
+        total_t += t2 - t1
+        total_b += nb
+        if p["layer"] == 0:
+            l0_t += t2 - t1
+            l0_b += nb
+        n_params += 1
+        n_elems += model.numel(p["shape"])
+        del world, dw, dbf
+    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"the whole switch: all {n_params} parameters ({n_elems} elements), one parameter at a "
+                      f"time, {total_b / 1e9:.1f} GB payload in {total_t:.1f} s; torch CPU threads={cores}",
+            "full_switch_ms": round(total_t * 1e3, 1), "input_copy_s": round(copy_t, 1),
+            "layer0_gbps": round(l0_b / l0_t / 1e9, 3) if l0_t else None,
+            "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
 
 
 def _cpu_model() -> str:
@@ -171,7 +191,7 @@ def main():
     torch.cuda.set_device(dev)
     _native.load()
     _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run,
-                       bool(args.persistent), args.lanes)
+                       bool(args.persistent), args.lanes, args.units)
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:
@@ -310,12 +330,13 @@ def main():
         out["config"]["copy_ceiling"] = copy_ceiling(a, b, stream, traffic_gbps, plan.read_bytes, payload)
     views.clear()
     del b
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline: Oracle-1 over every parameter", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(spec, ls, src, dst, backup, a)
     if not args.no_e2e:
         a, out["config"]["reshard_e2e"] = reshard_end_to_end(a, spec, src, dst, repad, tm, args.no_verify)
     del a
     torch.cuda.empty_cache()
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(spec_fn, src, dst, backup, full_payload=payload)
     print(json.dumps(out), flush=True)
     return 0
 

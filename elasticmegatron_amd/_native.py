@@ -68,7 +68,7 @@ class PlanStats(ctypes.Structure):
 class Tuning(ctypes.Structure):
     _fields_ = [("blocks_per_cu", ctypes.c_uint32), ("nontemporal", ctypes.c_uint32),
                 ("xcd_remap", ctypes.c_uint32), ("run", ctypes.c_uint32), ("persistent", ctypes.c_uint32),
-                ("lanes", ctypes.c_uint32)]
+                ("lanes", ctypes.c_uint32), ("units", ctypes.c_uint32), ("buffer_ops", ctypes.c_uint32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -147,11 +147,13 @@ def get_tuning() -> Tuning:
 
 
 def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True, run: int = 4,
-               persistent: bool = False, lanes: int = 0) -> None:
+               persistent: bool = False, lanes: int = 0, units: int = 0, buffer_ops: bool = False) -> None:
     """Launch shape of every later execution.  The default runs one workgroup of ``lanes`` lanes
-    (0: 64) per chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu``,
-    ``xcd_remap`` and ``run`` shape."""
-    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run, 1 if persistent else 0, lanes)
+    (0: 64) with ``units`` 16-byte units each (0: a whole chunk of 256 units per workgroup) per piece
+    of a chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu``, ``xcd_remap``
+    and ``run`` shape."""
+    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run, 1 if persistent else 0, lanes,
+               units, 1 if buffer_ops else 0)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 
 

@@ -88,8 +88,12 @@ constexpr int kUnroll = EMRS_COPY_UNROLL;
 constexpr uint32_t kChunkUnits = kThreads;  // units per work chunk: one per lane
 constexpr uint32_t kStepUnits = kThreads * kUnroll;  // units per step of a persistent workgroup
 constexpr uint64_t kMaxGridY = 65535;                     // rows of a one-workgroup-per-chunk grid
-constexpr uint64_t kMaxGridX = 0xffffffffull / kThreads;  // a grid dimension holds fewer than 2^32 lanes
 constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 bits
+// Row pitches of multi-row segments stay below this many bytes, so that a piece
+// of at most 256 rows spans less than 2^31 bytes from its first row: the
+// buffer-instruction path addresses it with 32-bit offsets.  Segments with
+// longer pitches are emitted one row at a time.
+constexpr uint64_t kMaxPitchBytes = 1ull << 23;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -173,7 +177,9 @@ struct Tuning {
   std::atomic<uint32_t> xcd_remap{1};      // persistent grid
   std::atomic<uint32_t> run{4};            // persistent grid: round-robin runs of 4 x kUnroll chunks
   std::atomic<uint32_t> persistent{0};     // 0: one workgroup per chunk
-  std::atomic<uint32_t> lanes{64};         // lanes per workgroup of one chunk: 64, 128 or 256
+  std::atomic<uint32_t> lanes{64};         // lanes per workgroup of one piece: 64, 128 or 256
+  std::atomic<uint32_t> units{4};          // 16-byte units per lane: lanes * units is 64, 128 or 256
+  std::atomic<uint32_t> buffer_ops{0};     // 1: 16-byte units through buffer instructions
 };
 Tuning g_tuning;
 
@@ -395,15 +401,14 @@ __global__ __launch_bounds__(kThreads) void copy_plan_persistent_kernel(
                               dst_tab);
 }
 
-// Chunk [u0, u0 + kChunkUnits) of segment s (clipped to its `total` units) by
-// a workgroup of L lanes, kChunkUnits / L units per lane: every load is issued
-// before the first store.
-template <typename T, bool kNT, bool kCast, bool kZero, bool kDup, int L>
+// Units [u0, u0 + L * U) of segment s (clipped to its `total` units) by a
+// workgroup of L lanes, U units per lane: every load is issued before the
+// first store.
+template <typename T, bool kNT, bool kCast, bool kZero, bool kDup, int L, int U>
 __device__ __forceinline__ void copy_units(const DevSeg &s, const char *sbase, char *dbase, char *abase, uint32_t u0,
                                            uint32_t total) {
   typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
   typedef typename C::type A;
-  constexpr int U = kChunkUnits / L;
   const T *src = reinterpret_cast<const T *>(sbase);
   T *dst = reinterpret_cast<T *>(dbase);
   A *aux = reinterpret_cast<A *>(abase);
@@ -442,33 +447,166 @@ __device__ __forceinline__ void copy_units(const DevSeg &s, const char *sbase, c
   }
 }
 
-template <bool kNT, bool kZero, bool kDup, int L>
-__device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, const char *sb, char *db, char *ab,
-                                               uint32_t u0, uint32_t total) {
-  switch (ul) {
-    case 4: copy_units<u32x4, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
-    case 3: copy_units<uint64_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
-    case 2: copy_units<uint32_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
-    case 1: copy_units<uint16_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
-    default: copy_units<uint8_t, kNT, false, kZero, kDup, L>(s, sb, db, ab, u0, total); break;
+// A buffer resource for raw (unstructured) accesses at 32-bit byte offsets from
+// `base`, over the whole 4 GiB range (word 3: the gfx9-family raw-buffer
+// configuration).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const char *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), 0, -1, 0x00020000);
+}
+
+// Cache policy of buffer instructions: bit 1 is the non-temporal hint on gfx94x/gfx950.
+template <bool kNT>
+struct BufPolicy {
+  static constexpr int value = kNT ? 2 : 0;
+};
+
+// One unit of T through a buffer instruction at a 32-bit byte offset.
+template <typename T, int kPolicy>
+__device__ __forceinline__ T buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 16) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kPolicy);
+  } else if constexpr (sizeof(T) == 8) {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kPolicy);
+    return (uint64_t)w[0] | ((uint64_t)w[1] << 32);
+  } else if constexpr (sizeof(T) == 4) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kPolicy);
+  } else if constexpr (sizeof(T) == 2) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kPolicy);
+  } else {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, kPolicy);
   }
 }
 
-// One workgroup of L lanes per chunk (the default schedule).  The grid is
-// two-dimensional (chunk = blockIdx.y * gridDim.x + blockIdx.x) because one
-// dimension holds fewer than 2^32 lanes; workgroups past the last chunk exit
-// at once.  The segment search depends on the chunk alone, so it runs on the
-// scalar unit, once per wave, and the upper levels of the search stay in the
-// scalar cache for every workgroup in flight.  With L = 64 (the default) a
-// chunk is one wave: one search per 4 KB, four loads in flight per lane.
-// With 256 lanes four waves repeat the same search for one 16-byte load each,
-// and the launch runs about 20% slower.
-template <bool kNT, bool kTable, int L>
+template <typename T, int kPolicy>
+__device__ __forceinline__ void buf_store(T v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 16) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kPolicy);
+  } else if constexpr (sizeof(T) == 8) {
+    typedef unsigned int v2u __attribute__((__vector_size__(8)));
+    uint64_t x;
+    memcpy(&x, &v, 8);
+    const v2u w = {(unsigned)x, (unsigned)(x >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, kPolicy);
+  } else if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kPolicy);
+  } else if constexpr (sizeof(T) == 2) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kPolicy);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, kPolicy);
+  }
+}
+
+// copy_units with buffer instructions: each stream (source, destination,
+// second destination) is one scalar base, the start of the piece's first row,
+// plus a 32-bit per-lane byte offset, so a lane needs one VGPR per address
+// instead of two.  In a one-row segment the offsets of a lane's units differ
+// by constants, which the instructions' immediate offsets hold.  Row pitches
+// are below 2^23 bytes (the plan emits longer ones row by row) and a piece
+// spans at most 256 rows, so offsets stay below 2^31.  Loads and stores are
+// masked exactly as in copy_units.
+template <typename T, bool kNT, bool kCast, bool kZero, bool kDup, int L, int U>
+__device__ __forceinline__ void copy_units_buf(const DevSeg &s, const char *sbase, char *dbase, char *abase,
+                                               uint32_t u0, uint32_t total) {
+  typedef typename std::conditional<kCast, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
+  constexpr int cp = BufPolicy<kNT>::value;
+  constexpr uint32_t B = sizeof(T);                          // bytes per unit
+  constexpr uint32_t AB = kCast ? sizeof(A) : sizeof(T);     // second-destination bytes per unit
+  const uint32_t tid = threadIdx.x;
+  T v[U];
+  if (s.rows == 1) {
+    const __amdgpu_buffer_rsrc_t rs = raw_rsrc(sbase + (s.src_off + u0) * B);
+    const __amdgpu_buffer_rsrc_t rd = raw_rsrc(dbase + (s.dst_off + u0) * B);
+    const __amdgpu_buffer_rsrc_t ra = raw_rsrc(abase + (s.aux_off + u0) * AB);
+    const uint32_t n = total - u0;  // units left in the segment from u0
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      v[j] = T{};
+      if constexpr (!kZero)
+        if (j * L + tid < n) v[j] = buf_load<T, cp>(rs, (j * L + tid) * B);
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+      if (j * L + tid < n) {
+        buf_store<T, cp>(v[j], rd, (j * L + tid) * B);
+        if constexpr (kCast) buf_store<A, cp>(C::cast(v[j]), ra, (j * L + tid) * AB);
+        if constexpr (kDup) buf_store<T, cp>(v[j], ra, (j * L + tid) * AB);
+      }
+    return;
+  }
+  const uint32_t row0 = magic_div(u0, s.magic, s.sh1(), s.sh2());
+  const __amdgpu_buffer_rsrc_t rs = raw_rsrc(sbase + (s.src_off + (uint64_t)row0 * s.src_stride) * B);
+  const __amdgpu_buffer_rsrc_t rd = raw_rsrc(dbase + (s.dst_off + (uint64_t)row0 * s.dst_stride) * B);
+  const __amdgpu_buffer_rsrc_t ra = raw_rsrc(abase + (s.aux_off + (uint64_t)row0 * s.aux_stride) * AB);
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * L + tid;
+    v[j] = T{};
+    if constexpr (!kZero)
+      if (u < total) {
+        const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2());
+        const uint32_t col = u - row * s.len;
+        v[j] = buf_load<T, cp>(rs, ((row - row0) * s.src_stride + col) * B);
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * L + tid;
+    if (u < total) {
+      const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2()), dr = row - row0;
+      const uint32_t col = u - row * s.len;
+      buf_store<T, cp>(v[j], rd, (dr * s.dst_stride + col) * B);
+      if constexpr (kCast) buf_store<A, cp>(C::cast(v[j]), ra, (dr * s.aux_stride + col) * AB);
+      if constexpr (kDup) buf_store<T, cp>(v[j], ra, (dr * s.aux_stride + col) * AB);
+    }
+  }
+}
+
+template <bool kNT, bool kZero, bool kDup, int L, int U>
+__device__ __forceinline__ void dispatch_chunk_buf(uint32_t ul, const DevSeg &s, const char *sb, char *db,
+                                                   char *ab, uint32_t u0, uint32_t total) {
+  switch (ul) {
+    case 4: copy_units_buf<u32x4, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 3: copy_units_buf<uint64_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 2: copy_units_buf<uint32_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 1: copy_units_buf<uint16_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    default: copy_units_buf<uint8_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+  }
+}
+
+template <bool kNT, bool kZero, bool kDup, int L, int U>
+__device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, const char *sb, char *db, char *ab,
+                                               uint32_t u0, uint32_t total) {
+  switch (ul) {
+    case 4: copy_units<u32x4, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 3: copy_units<uint64_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 2: copy_units<uint32_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    case 1: copy_units<uint16_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+    default: copy_units<uint8_t, kNT, false, kZero, kDup, L, U>(s, sb, db, ab, u0, total); break;
+  }
+}
+
+// One workgroup of L lanes per piece of L * U units of a chunk (the default
+// schedule: L = 64, U = 4, one workgroup per chunk).  A chunk of 256 units
+// holds 256 / (L * U) pieces; workgroup w takes piece w % that of chunk
+// w / that, and a piece past the end of its segment's last chunk does
+// nothing.  The grid is two-dimensional (w = blockIdx.y * gridDim.x +
+// blockIdx.x) because one dimension holds fewer than 2^32 lanes; workgroups
+// past the last piece exit at once.  The segment search depends on the chunk
+// alone, so it runs on the scalar unit, once per wave, and the upper levels
+// of the search stay in the scalar cache for every workgroup in flight.  With
+// L = 64 and U = 4 a chunk is one wave: one search per 4 KB, four loads in
+// flight per lane.  With 256 lanes four waves repeat the same search for one
+// 16-byte load each, and the launch runs about 20% slower.
+template <bool kNT, bool kTable, int L, int U, bool kBuf>
 __global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint64_t n_chunks,
                                                       SegHint hint, Bases src, Bases dst,
                                                       const uint64_t *__restrict__ src_tab,
                                                       const uint64_t *__restrict__ dst_tab) {
-  const uint64_t c = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  constexpr uint32_t kPieces = kChunkUnits / (L * U);  // pieces per chunk: 1, 2 or 4
+  static_assert(kPieces * L * U == kChunkUnits, "a piece divides a chunk");
+  const uint64_t w = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const uint64_t c = w / kPieces;
   if (c >= n_chunks) return;
   const uint32_t b = (uint32_t)(c >> hint.shift);
   uint32_t lo = hint.first[b], hi = hint.first[b + 1];
@@ -478,26 +616,47 @@ __global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__
     else hi = mid - 1;
   }
   const DevSeg s = segs[lo];
-  const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits, total = s.len * s.rows;
+  const uint32_t total = s.len * s.rows;
+  const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits + (uint32_t)(w % kPieces) * (L * U);
+  if (kPieces > 1 && u0 >= total) return;
   const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
   char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
   char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
   const uint32_t ops = s.ops(), ul = s.unit_log2();
+  if constexpr (kBuf) {  // every unit width through buffer instructions
+    if (ops & 4) {
+      if (ops & 2) dispatch_chunk_buf<kNT, true, true, L, U>(ul, s, sb, db, ab, u0, total);
+      else dispatch_chunk_buf<kNT, false, true, L, U>(ul, s, sb, db, ab, u0, total);
+    } else if (ops & 1) {  // with the bf16 image (fp32 only: 16- or 4-byte units)
+      if (ops & 2) {
+        if (ul == 4) copy_units_buf<u32x4, kNT, true, true, false, L, U>(s, sb, db, ab, u0, total);
+        else copy_units_buf<uint32_t, kNT, true, true, false, L, U>(s, sb, db, ab, u0, total);
+      } else {
+        if (ul == 4) copy_units_buf<u32x4, kNT, true, false, false, L, U>(s, sb, db, ab, u0, total);
+        else copy_units_buf<uint32_t, kNT, true, false, false, L, U>(s, sb, db, ab, u0, total);
+      }
+    } else if (ops & 2) {
+      dispatch_chunk_buf<kNT, true, false, L, U>(ul, s, sb, db, ab, u0, total);
+    } else {
+      dispatch_chunk_buf<kNT, false, false, L, U>(ul, s, sb, db, ab, u0, total);
+    }
+    return;
+  }
   if (ops & 4) {  // duplicate to aux, with or without zero fill
-    if (ops & 2) dispatch_chunk<kNT, true, true, L>(ul, s, sb, db, ab, u0, total);
-    else dispatch_chunk<kNT, false, true, L>(ul, s, sb, db, ab, u0, total);
+    if (ops & 2) dispatch_chunk<kNT, true, true, L, U>(ul, s, sb, db, ab, u0, total);
+    else dispatch_chunk<kNT, false, true, L, U>(ul, s, sb, db, ab, u0, total);
   } else if (ops & 1) {  // with the bf16 image (fp32 only: 16- or 4-byte units), with or without zero fill
     if (ops & 2) {
-      if (ul == 4) copy_units<u32x4, kNT, true, true, false, L>(s, sb, db, ab, u0, total);
-      else copy_units<uint32_t, kNT, true, true, false, L>(s, sb, db, ab, u0, total);
+      if (ul == 4) copy_units<u32x4, kNT, true, true, false, L, U>(s, sb, db, ab, u0, total);
+      else copy_units<uint32_t, kNT, true, true, false, L, U>(s, sb, db, ab, u0, total);
     } else {
-      if (ul == 4) copy_units<u32x4, kNT, true, false, false, L>(s, sb, db, ab, u0, total);
-      else copy_units<uint32_t, kNT, true, false, false, L>(s, sb, db, ab, u0, total);
+      if (ul == 4) copy_units<u32x4, kNT, true, false, false, L, U>(s, sb, db, ab, u0, total);
+      else copy_units<uint32_t, kNT, true, false, false, L, U>(s, sb, db, ab, u0, total);
     }
   } else if (ops & 2) {
-    dispatch_chunk<kNT, true, false, L>(ul, s, sb, db, ab, u0, total);
+    dispatch_chunk<kNT, true, false, L, U>(ul, s, sb, db, ab, u0, total);
   } else {
-    dispatch_chunk<kNT, false, false, L>(ul, s, sb, db, ab, u0, total);
+    dispatch_chunk<kNT, false, false, L, U>(ul, s, sb, db, ab, u0, total);
   }
 }
 
@@ -615,7 +774,10 @@ struct Builder {
       }
       return;
     }
-    if (len >= kMaxUnitsPerSeg || ss > 0xffffffffull || ds > 0xffffffffull || ax.stride > 0xffffffffull) {
+    // Bytes per second-destination unit: half a unit for a bf16 image, a whole one for a duplicate.
+    const uint64_t aub = ax.on ? (ax.cast ? (1ull << ul) / 2 : (1ull << ul)) : 0;
+    if (len >= kMaxUnitsPerSeg || (ss << ul) >= kMaxPitchBytes || (ds << ul) >= kMaxPitchBytes ||
+        ax.stride * aub >= kMaxPitchBytes) {
       for (uint64_t r = 0; r < rows; ++r)
         for (uint64_t off = 0; off < len; off += kMaxUnitsPerSeg) {
           const uint64_t n = std::min<uint64_t>(kMaxUnitsPerSeg, len - off);
@@ -1441,22 +1603,37 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
 }  // extern "C"
 
 namespace {
-template <int L>
+template <int L, int U, bool kBuf>
 void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table,
                    uint64_t n_chunks, const SegHint &hint, const uint64_t *stab, const uint64_t *dtab) {
   const dim3 block(L);
   if (nt && rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<true, true, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
-                       stab, dtab);
+    hipLaunchKernelGGL((copy_plan_kernel<true, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
+                       rb.src, rb.dst, stab, dtab);
   else if (nt)
-    hipLaunchKernelGGL((copy_plan_kernel<true, false, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
-                       stab, dtab);
+    hipLaunchKernelGGL((copy_plan_kernel<true, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
+                       rb.src, rb.dst, stab, dtab);
   else if (rb.table)
-    hipLaunchKernelGGL((copy_plan_kernel<false, true, L>), grid, block, 0, st, table, n_chunks, hint, rb.src, rb.dst,
-                       stab, dtab);
+    hipLaunchKernelGGL((copy_plan_kernel<false, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
+                       rb.src, rb.dst, stab, dtab);
   else
-    hipLaunchKernelGGL((copy_plan_kernel<false, false, L>), grid, block, 0, st, table, n_chunks, hint, rb.src,
-                       rb.dst, stab, dtab);
+    hipLaunchKernelGGL((copy_plan_kernel<false, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
+                       rb.src, rb.dst, stab, dtab);
+}
+
+// The one-workgroup-per-piece launch for `lanes` lanes of `units` units each.
+template <bool kBuf>
+void launch_pieces(uint32_t lanes, uint32_t units, bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st,
+                   const DevSeg *table, uint64_t n_chunks, const SegHint &hint, const uint64_t *stab,
+                   const uint64_t *dtab) {
+  switch (lanes * 8 + units) {
+    case 64 * 8 + 1: launch_chunks<64, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    case 64 * 8 + 2: launch_chunks<64, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    case 128 * 8 + 1: launch_chunks<128, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    case 128 * 8 + 2: launch_chunks<128, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    case 256 * 8 + 1: launch_chunks<256, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    default: launch_chunks<64, 4, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+  }
 }
 }  // namespace
 
@@ -1489,11 +1666,12 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   const uint32_t nseg = (uint32_t)plan->segs.size();
   const dim3 block(kThreads);
   if (!g_tuning.persistent.load()) {
-    // One workgroup per chunk, on a grid of at most 65535 rows.
-    const uint64_t gx = std::min<uint64_t>(
-        plan->n_chunks, std::max<uint64_t>(1ull << 16, (plan->n_chunks + kMaxGridY - 1) / kMaxGridY));
-    if (gx > kMaxGridX) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan has too many chunks for one launch");
-    const dim3 grid((uint32_t)gx, (uint32_t)((plan->n_chunks + gx - 1) / gx));
+    // One workgroup per piece of lanes * units units, on a grid of at most 65535 rows.
+    const uint32_t lanes = g_tuning.lanes.load(), units = g_tuning.units.load();
+    const uint64_t n_wg = plan->n_chunks * (kChunkUnits / (lanes * units));
+    const uint64_t gx = std::min<uint64_t>(n_wg, std::max<uint64_t>(1ull << 16, (n_wg + kMaxGridY - 1) / kMaxGridY));
+    if (gx > 0xffffffffull / lanes) return fail(EMRS_ERR_INVALID_ARGUMENT, "plan has too many chunks for one launch");
+    const dim3 grid((uint32_t)gx, (uint32_t)((n_wg + gx - 1) / gx));
     uint64_t *tab = nullptr;
     bool tab_owned = false;
     rc = pointer_table(plan, dev, rb, st, &tab, &tab_owned);
@@ -1515,13 +1693,10 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
         stab = dtab = nullptr;
       }
     }
-    const uint32_t lanes = g_tuning.lanes.load();
-    if (lanes == 256)
-      launch_chunks<256>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
-    else if (lanes == 128)
-      launch_chunks<128>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
+    if (g_tuning.buffer_ops.load())
+      launch_pieces<true>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
     else
-      launch_chunks<64>(nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
+      launch_pieces<false>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
     hipError_t le = hipGetLastError();
     if (tab_owned) (void)hipFreeAsync(tab, st);
     if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
@@ -1702,6 +1877,8 @@ int emrs_get_tuning(emrs_tuning *out) {
   out->run = g_tuning.run.load();
   out->persistent = g_tuning.persistent.load();
   out->lanes = g_tuning.lanes.load();
+  out->units = g_tuning.units.load();
+  out->buffer_ops = g_tuning.buffer_ops.load();
   return EMRS_OK;
 }
 
@@ -1711,12 +1888,19 @@ int emrs_set_tuning(const emrs_tuning *t) {
   if (t->run > (1u << 20)) return fail(EMRS_ERR_INVALID_ARGUMENT, "run must be in [0, 2^20]");
   if (t->lanes != 0 && t->lanes != 64 && t->lanes != 128 && t->lanes != 256)
     return fail(EMRS_ERR_INVALID_ARGUMENT, "lanes must be 0, 64, 128 or 256");
+  const uint32_t lanes = t->lanes ? t->lanes : 64;
+  // 0 keeps the pre-existing meaning: one chunk of 256 units per workgroup.
+  const uint32_t units = t->units ? t->units : kChunkUnits / lanes;
+  if (units != 1 && units != 2 && units != 4) return fail(EMRS_ERR_INVALID_ARGUMENT, "units must be 0, 1, 2 or 4");
+  if (kChunkUnits % (lanes * units)) return fail(EMRS_ERR_INVALID_ARGUMENT, "lanes * units must divide 256");
   g_tuning.blocks_per_cu.store(t->blocks_per_cu);
   g_tuning.nontemporal.store(t->nontemporal ? 1 : 0);
   g_tuning.xcd_remap.store(t->xcd_remap ? 1 : 0);
   g_tuning.run.store(t->run);
   g_tuning.persistent.store(t->persistent ? 1 : 0);
-  g_tuning.lanes.store(t->lanes ? t->lanes : 64);
+  g_tuning.lanes.store(lanes);
+  g_tuning.units.store(units);
+  g_tuning.buffer_ops.store(t->buffer_ops ? 1 : 0);
   return EMRS_OK;
 }
 

@@ -254,8 +254,14 @@ typedef struct emrs_tuning {
                              chunks; N in [1, 2^20]: chunks are dealt out round-robin in runs of
                              8N, capped at a quarter of a workgroup's share (default 4) */
   uint32_t persistent;    /* 0 (default): one workgroup per chunk; 1: persistent grid */
-  uint32_t lanes;         /* one workgroup per chunk: lanes per workgroup, 64, 128 or 256
-                             (0: the default, 64, four 16-byte units per lane) */
+  uint32_t lanes;         /* one workgroup per piece of a chunk: lanes per workgroup, 64, 128 or 256
+                             (0: the default, 64) */
+  uint32_t units;         /* 16-byte units per lane, 1, 2 or 4, with lanes * units dividing 256: a
+                             chunk of 256 units is split into 256 / (lanes * units) pieces, one
+                             workgroup each (0: 256 / lanes, one workgroup per chunk) */
+  uint32_t buffer_ops;    /* one workgroup per piece, 1: 16-byte units are moved with buffer
+                             instructions (32-bit offsets from a per-piece base); 0: with 64-bit
+                             global addresses */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);

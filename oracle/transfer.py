@@ -141,9 +141,12 @@ def build_src_world(inv, hp, src, seed, params=None):
     return world
 
 
-def transfer(inv, hp, src, dst, src_world, params=None):
-    """Run transfer.py:291-341 over the simulated world; returns (dst fp32 world, dst bf16, mailbox)."""
-    sd, dd = dp_distributions(inv, src, hp), dp_distributions(inv, dst, hp)
+def transfer(inv, hp, src, dst, src_world, params=None, dists=None):
+    """Run transfer.py:291-341 over the simulated world; returns (dst fp32 world, dst bf16, mailbox).
+
+    ``dists``: the (source, destination) DP distributions of every parameter, when the caller has
+    them already (the reference computes them when it plans, outside its timed executor)."""
+    sd, dd = dists if dists is not None else (dp_distributions(inv, src, hp), dp_distributions(inv, dst, hp))
     mb = Mailbox()
     plans, dst_world = {}, {}
     for p in inv:
@@ -278,11 +281,12 @@ def rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst):
     return out
 
 
-def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None):
+def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None, dist=None):
     """Group-ZeRO switch (transfer.py:343-388): migrate on the master, broadcast to the instances.
 
-    ``params``: the parameter ids to move (default: all); ``src_world`` must hold them."""
-    dist = dp_distributions(inv, dst, hp)
+    ``params``: the parameter ids to move (default: all); ``src_world`` must hold them.
+    ``dist``: the destination's DP distributions, when the caller has them already."""
+    dist = dist if dist is not None else dp_distributions(inv, dst, hp)
     out = {}
     for p in inv:
         pid = p["id"]

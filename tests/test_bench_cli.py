@@ -76,3 +76,31 @@ def test_committed_traffic_describes_the_current_plan(traffic_file):
         rec["hbm_bytes_per_launch"]
     assert abs(rec["hbm_bytes_per_launch"] / plan.traffic_bytes - 1) < 1e-3   # within 0.1% of the algorithmic bytes
     assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes + 1) is None
+
+
+@pytest.mark.parametrize("src,dst", [(ParallelStrategy(8, 2, 1), ParallelStrategy(8, 1, 1)),
+                                     (ParallelStrategy(4, 1, 1),
+                                      ParallelStrategy(8, 1, 1, num_distributed_optimizer_instances=2))])
+def test_cpu_baseline_covers_every_parameter(src, dst):
+    """The CPU leg runs Oracle-1 over every parameter of the switch and sums their times."""
+    import numpy as np
+    import torch
+
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.resharding.model_spec import tiny_llama2
+    from tests.helpers import SEED, new_arenas, piece_fill_numpy
+
+    spec = tiny_llama2()
+    ls = build_virtual_model(spec).layout(src)
+    host = new_arenas(ls, fill=0)
+    piece_fill_numpy(ls.pieces(), host, SEED)
+    a = TrainingState(ls, *[torch.from_numpy(x.view(np.float32)) for x in host[:3]],
+                      torch.from_numpy(host[3].view(np.int16)).view(torch.bfloat16))
+    out = bench.cpu_baseline(spec, ls, src, dst, ParallelStrategy.is_redundant_backup(src, dst), a)
+    assert out["kind"] == "port" and out["cores"] == os.cpu_count()
+    assert f"all {len(ls.place)} parameters ({spec.num_params()} elements)" in out["sample"]
+    assert out["value"] > 0 and out["full_switch_ms"] > 0
+    payload = TransferManager().compile(ls, ls.space.layout(dst),
+                                        "transfer" if dst.num_distributed_optimizer_instances == 1
+                                        else "backup_up").payload_bytes
+    assert f"{payload / 1e9:.1f} GB payload" in out["sample"]

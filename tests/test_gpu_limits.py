@@ -130,8 +130,8 @@ def _expected(t, srcs_h, n, size):
     return out
 
 
-@pytest.mark.parametrize("lanes", [64, 256])
-def test_table_bases_every_segment_kind(gpu_device, lanes):
+@pytest.mark.parametrize("lanes,buffer_ops", [(64, False), (256, False), (64, True)])
+def test_table_bases_every_segment_kind(gpu_device, lanes, buffer_ops):
     """A plan over 200 source and 400 destination buffers, with every kind of segment, run on the
     bases of its first call (the segment table resolved against them, no base lookup in the
     kernel), on other bases (the pointer table), and on the first bases again."""
@@ -145,9 +145,10 @@ def test_table_bases_every_segment_kind(gpu_device, lanes):
     want = _expected(t, srcs_h, n, size)
     sp = [s.data_ptr() for s in srcs]
     try:
-        _native.set_tuning(lanes=lanes)
+        _native.set_tuning(lanes=lanes, buffer_ops=buffer_ops)
         for k, which in enumerate([0, 0, 1, 0, 1]):
-            print(f"case table bases lanes {lanes} call {k}: destination set {which}", flush=True)
+            print(f"case table bases lanes {lanes} buffer {buffer_ops} call {k}: destination set {which}",
+                  flush=True)
             for d in sets[which]:
                 d.zero_()
             plan.execute(sp, [d.data_ptr() for d in sets[which]], torch.cuda.current_stream().cuda_stream)
@@ -187,3 +188,31 @@ def test_segments_beyond_two_to_the_thirty_units(gpu_device):
     want = src2.view(rows, 1001)[:, :ln]
     assert torch.equal(got, want)
     assert int(dst2[5:5 + rows * 1003].view(rows, 1003)[:, ln:].sum()) == 0
+
+
+@pytest.mark.parametrize("buffer_ops", [False, True])
+def test_long_row_pitches_are_emitted_row_by_row(gpu_device, buffer_ops):
+    """Row pitches of 2^23 bytes and more (here 8 MiB and 12 MiB) are emitted one row at a time, so
+    the buffer-instruction path's 32-bit offsets cover every piece; the copy is unchanged."""
+    rows, n = 5, 1000
+    ps, pd = (1 << 21), (3 << 20)          # fp32 elements: 8 MiB and 12 MiB pitches
+    src = torch.randint(0, 1 << 30, (rows * ps,), dtype=torch.int32, device=gpu_device)
+    dst = torch.zeros(rows * pd, dtype=torch.int32, device=gpu_device)
+    t = np.zeros(2, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 8, 4, n, rows, ps, pd, 0, 0, 0, 0)          # long pitches: split by rows
+    t[1] = (0, 0, 4, 0, 8 + n, 4 + n, 16, 4, 64, 64, 0, 0, 0, 0)    # short pitches: one device segment
+    plan = _native.Plan(t, [rows * ps * 4], [rows * pd * 4], check_disjoint=True)
+    assert plan.stats().n_device_segments >= rows + 1
+    try:
+        _native.set_tuning(buffer_ops=buffer_ops)
+        print(f"case long pitches buffer {buffer_ops}", flush=True)
+        plan.execute([src.data_ptr()], [dst.data_ptr()], torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning()
+    want = torch.zeros_like(dst)
+    for r in range(rows):
+        want[4 + r * pd:4 + r * pd + n] = src[8 + r * ps:8 + r * ps + n]
+    for r in range(4):
+        want[4 + n + r * 64:4 + n + r * 64 + 16] = src[8 + n + r * 64:8 + n + r * 64 + 16]
+    assert torch.equal(dst, want)

@@ -130,7 +130,12 @@ def test_manager_repad_round_trip(gpu_device):
 
 
 @pytest.mark.parametrize("tuning", [dict(nontemporal=False), dict(lanes=128), dict(lanes=256),
-                                    dict(lanes=256, nontemporal=False), dict(persistent=True),
+                                    dict(lanes=256, nontemporal=False), dict(units=1), dict(units=2),
+                                    dict(lanes=128, units=1), dict(units=1, nontemporal=False),
+                                    dict(buffer_ops=True), dict(buffer_ops=True, nontemporal=False),
+                                    dict(buffer_ops=True, units=1), dict(buffer_ops=True, lanes=256),
+                                    dict(buffer_ops=True, lanes=128, units=2),
+                                    dict(persistent=True),
                                     dict(persistent=True, run=0), dict(persistent=True, run=0, xcd_remap=False),
                                     dict(persistent=True, run=1), dict(persistent=True, run=64),
                                     dict(persistent=True, blocks_per_cu=1),
@@ -208,7 +213,11 @@ def _random_table(rng, n_segs, sizes):
 
 
 @pytest.mark.parametrize("seed,tuning", [(0, {}), (1, {}), (2, {}), (3, dict(lanes=128)), (4, dict(lanes=256)),
-                                         (5, dict(persistent=True)), (6, dict(lanes=256, nontemporal=False))])
+                                         (5, dict(persistent=True)), (6, dict(lanes=256, nontemporal=False)),
+                                         (7, dict(units=1)), (8, dict(units=2)), (9, dict(lanes=128, units=1)),
+                                         (10, dict(buffer_ops=True)), (11, dict(buffer_ops=True, nontemporal=False)),
+                                         (12, dict(buffer_ops=True, units=1)),
+                                         (13, dict(buffer_ops=True, lanes=256))])
 def test_random_segments_match_numpy(gpu_device, seed, tuning):
     """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills,
     bf16 images and duplicates, under each launch shape.

@@ -232,14 +232,19 @@ def test_xor_checksum_rejects_bad_arguments_before_touching_a_device():
 def test_tuning_defaults_and_rejections():
     """emrs_tuning: the default launch shape reads back, settings round-trip, and values outside the
     documented ranges are refused without changing the current setting (no device needed)."""
-    assert ctypes.sizeof(_native.Tuning) == 24  # six uint32 fields, as in emrs.h
+    assert ctypes.sizeof(_native.Tuning) == 32  # eight uint32 fields, as in emrs.h
     t = _native.get_tuning()
-    assert (t.persistent, t.lanes, t.nontemporal, t.run) == (0, 64, 1, 4)
+    assert (t.persistent, t.lanes, t.units, t.nontemporal, t.run) == (0, 64, 4, 1, 4)
     try:
         _native.set_tuning(lanes=128, persistent=True, run=7, blocks_per_cu=3)
         t = _native.get_tuning()
         assert (t.persistent, t.lanes, t.run, t.blocks_per_cu) == (1, 128, 7, 3)
-        for kw in (dict(lanes=96), dict(lanes=512), dict(run=(1 << 20) + 1), dict(blocks_per_cu=65)):
+        assert _native.get_tuning().units == 2   # 0: one chunk of 256 units per workgroup
+        _native.set_tuning(lanes=64, units=1, buffer_ops=True)
+        assert (_native.get_tuning().lanes, _native.get_tuning().units, _native.get_tuning().buffer_ops) == (64, 1, 1)
+        _native.set_tuning(lanes=128, persistent=True, run=7, blocks_per_cu=3)
+        for kw in (dict(lanes=96), dict(lanes=512), dict(run=(1 << 20) + 1), dict(blocks_per_cu=65),
+                   dict(units=3), dict(units=8), dict(lanes=128, units=4), dict(lanes=256, units=2)):
             with pytest.raises(_native.EmrsError) as e:
                 _native.set_tuning(**kw)
             assert e.value.code == -1
@@ -249,4 +254,4 @@ def test_tuning_defaults_and_rejections():
     finally:
         _native.set_tuning()
     t = _native.get_tuning()
-    assert (t.persistent, t.lanes, t.run, t.blocks_per_cu) == (0, 64, 4, 0)
+    assert (t.persistent, t.lanes, t.units, t.run, t.blocks_per_cu) == (0, 64, 4, 4, 0)
