@@ -8,16 +8,13 @@ source exactly (round trip = identity).  The destination starts filled with a
 canary pattern, and every element the layout does not store (padding) must
 still hold it afterwards.
 
-The CPU oracle cannot run a whole model at these sizes, but it runs the
-parameters where placement is hardest: the word embedding and the output
-layer (the largest tensors, whose DP shards cross bucket boundaries), the
-final norm, and the last transformer layer.  For the transfer switches
 Oracle-1 (the reference's three-pass executor, transfer.py:36-341, restated
-on CPU tensors) runs them; for the Group-ZeRO switch Oracle-1's redundant
-backup (transfer.py:343-388) does, after every source rank's shard has been
-made distinct so that the instance -> rank mapping shows.  The GPU's pieces
-of those parameters must equal the oracle bit for bit.  Peak memory is two
-layouts' worth of state.
+on CPU tensors; for the Group-ZeRO switch its redundant backup,
+transfer.py:343-388) then runs the whole switch on the host, one parameter at
+a time, and the GPU's pieces of every parameter must equal it bit for bit.
+For the Group-ZeRO switch every source rank's shard is made distinct first, so
+that the instance -> rank mapping shows.  Peak memory is two layouts' worth of
+state on the device and one parameter's on the host.
 """
 
 import gc
@@ -54,26 +51,6 @@ def _release():
     torch.cuda.empty_cache()
 
 
-ORACLE_NAMES = ("embedding.word_embeddings.weight", "decoder.final_layernorm.weight", "output_layer.weight")
-
-
-def _oracle_params(spec, budget=250_000_000):
-    """Ids of the word embedding, final norm and output layer, and of the last transformer layer's
-    parameters in order up to ``budget`` elements (Mixtral's experts exceed it)."""
-    from oracle import model
-
-    inv = model.inventory(spec)
-    last = spec.num_layers - 1
-    params, total = {p["id"] for p in inv if p["name"] in ORACLE_NAMES}, 0
-    layer = False
-    for p in inv:
-        if p["layer"] == last and (not layer or total + model.numel(p["shape"]) <= budget):
-            params.add(p["id"])
-            total += model.numel(p["shape"])
-            layer = True
-    return inv, params
-
-
 def _device_pieces(layout, state, params, bf16=True):
     got32, gotbf = {}, {}
     space = layout.space
@@ -90,52 +67,6 @@ def _device_pieces(layout, state, params, bf16=True):
                 gotbf[(layout.shard_keys[h.rank], pid)] = \
                     state.param[h.offset:h.offset + n].view(torch.int16).cpu().numpy().view(np.uint16)
     return got32, gotbf
-
-
-def _check_against_oracle1(spec, src, dst, layout, state):
-    """Oracle-1's transfer of the word embedding, final norm, output layer and last layer, against
-    the same pieces of the device state, bit for bit."""
-    from oracle import model
-    from oracle import transfer as oracle1
-    from oracle.plan import Strat
-    from tests.helpers import compare
-
-    inv, params = _oracle_params(spec)
-    S, D = Strat.of(src), Strat.of(dst)
-    world = oracle1.build_src_world(inv, spec, S, SEED, params)
-    dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, params)
-    want32 = oracle1.flatten(dw)
-    del world, dw
-    got32, gotbf = _device_pieces(layout, state, params)
-    total = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
-    print(f"oracle-1: {len(params)} params, {total} elements", flush=True)
-    assert got32 and gotbf
-    assert compare(got32, gotbf, want32, dbf) == []
-
-
-def _check_backup_against_oracle1(spec, src, dst, a, b, tm, plan, scale_up):
-    """Oracle-1's redundant backup from a source whose ranks hold distinct shards, against the
-    device.  The source and destination are restored afterwards."""
-    from oracle import model
-    from oracle import transfer as oracle1
-    from oracle.plan import Strat
-    from tests.helpers import compare
-
-    perturb_per_rank(a)
-    tm.execute(plan, a, b)
-    inv, params = _oracle_params(spec)
-    S, D = Strat.of(src), Strat.of(dst)
-    world = oracle1.build_src_world(inv, spec, S, SEED, params)
-    perturb_per_rank(world)
-    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, world, scale_up, params))
-    del world
-    got, _ = _device_pieces(b.layout, b, params, bf16=False)
-    total = sum(model.numel(p["shape"]) for p in inv if p["id"] in params)
-    print(f"oracle-1 redundant backup: {len(params)} params, {total} elements", flush=True)
-    assert got
-    assert compare(got, {}, want, {}) == []
-    perturb_per_rank(a)  # XOR again: the seeded values are back
-    tm.execute(plan, a, b)
 
 
 @pytest.mark.parametrize("factory,src,dst,repad", [p if len(p.values) == 4 else
@@ -173,11 +104,6 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
         assert padding_damage(b, bf16=backup is None) == 0, "padding was written"
         report = tm.verify(a, b, kind)  # the plan's own check, against the source state
         assert report.bit_exact, report.lines()[:5]
-        if kind == "transfer" and not repad:  # the reference keeps the padded vocabulary fixed
-            _check_against_oracle1(spec, src, dst, ld, b)
-        elif backup is not None:
-            _check_backup_against_oracle1(spec, src, dst, a, b, tm, fwd, backup)
-            assert b.verify_synthetic(SEED)[0] == 0
         # Round trip into fresh storage: must reproduce every source element.
         param = a.param
         del a
@@ -192,4 +118,76 @@ def test_full_size_switch_and_round_trip(gpu_device, factory, src, dst, repad):
         assert bad == 0, first
     finally:
         a = b = a2 = param = None  # noqa: F841
+        _release()
+
+
+# Every switch the reference itself can make (it keeps the padded vocabulary fixed).
+WHOLE_CASES = [p for p in CASES if "repad" not in p.id]
+
+
+@pytest.mark.parametrize("factory,src,dst", WHOLE_CASES)
+def test_every_parameter_against_oracle1(gpu_device, factory, src, dst):
+    """Oracle-1 on every parameter of a full-size switch, one parameter at a time.
+
+    Each parameter's source pieces are copied from the device (they hold the
+    seeded values, which the device check against the generator confirms; for
+    the Group-ZeRO switch every rank's shard is made distinct first), Oracle-1
+    moves them on the CPU (transfer.py:36-341, or the redundant backup,
+    transfer.py:343-388), and the device's destination pieces of that
+    parameter must equal the oracle's bit for bit.  Every stored element of
+    the destination is compared.
+    """
+    import time
+
+    from oracle import model
+    from oracle import transfer as oracle1
+    from oracle.plan import Strat, dp_distributions, local_shape, tp_size
+    from tests.helpers import compare
+
+    spec = factory()
+    backup = PS.is_redundant_backup(src, dst)
+    kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+    print(f"case every parameter {spec.name}: {src} -> {dst}", flush=True)
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    plan = tm.compile(ls, ld, kind)
+    try:
+        a = TrainingState.allocate(ls, gpu_device)
+        b = TrainingState.allocate(ld, gpu_device, param=a.param if backup is not None else None)
+        a.fill_synthetic(SEED)
+        assert a.verify_synthetic(SEED)[0] == 0
+        if backup is not None:
+            perturb_per_rank(a)
+        tm.execute(plan, a, b)
+        torch.cuda.synchronize()
+        inv = model.inventory(spec)
+        S, D = Strat.of(src), Strat.of(dst)
+        sd, dd = dp_distributions(inv, S, spec), dp_distributions(inv, D, spec)
+        t0, n_params, n_elems = time.perf_counter(), 0, 0
+        for p in inv:
+            pid = p["id"]
+            if pid not in sd:
+                continue
+            vp = space.all_virtual_params[pid]
+            shape = local_shape(p, tp_size(S, p))
+            world = {pid: {h.rank: oracle1.OptInfo([t[h.offset:h.offset + h.hi - h.lo].cpu()
+                                                    for t in (a.main, a.exp_avg, a.exp_avg_sq)], (h.lo, h.hi), shape)
+                           for h in ls.fp32_holders(vp)}}
+            if backup is None:
+                dw, dbf, _ = oracle1.transfer(inv, spec, S, D, world, {pid}, dists=(sd, dd))
+            else:
+                dw, dbf = oracle1.redundant_backup(inv, spec, S, D, world, backup, {pid}, dist=dd), {}
+            got32, gotbf = _device_pieces(ld, b, {pid}, bf16=backup is None)
+            errs = compare(got32, gotbf, oracle1.flatten(dw), dbf)
+            assert not errs, (p["name"], errs[:3])
+            n_params += 1
+            n_elems += model.numel(p["shape"])
+            if n_params % 40 == 0:
+                print(f"  {n_params} parameters compared, {time.perf_counter() - t0:.0f} s", flush=True)
+        assert n_params == len(ld.place)
+        print(f"oracle-1 on every parameter: {n_params} params, {n_elems} elements, "
+              f"{time.perf_counter() - t0:.0f} s", flush=True)
+    finally:
+        a = b = None  # noqa: F841
         _release()
