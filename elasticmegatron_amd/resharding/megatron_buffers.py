@@ -30,6 +30,8 @@ from __future__ import annotations
 
 from typing import Dict, List, Tuple
 
+import numpy as np
+
 from .layout import ARENA_PARAM, FP32_KINDS, StrategyLayout
 from .tensors import TensorBuffers
 
@@ -93,6 +95,22 @@ class MegatronBuffers:
             key, local = self.locate(a, off, n)
             out.append(buffers[key][local:local + n])
         return out
+
+    def remap_pieces(self, pieces: np.ndarray) -> np.ndarray:
+        """The layout's ``emrs_piece`` records (arena ids and offsets, from ``layout.pieces()``)
+        re-expressed over these buffers: buffer ids in ``specs`` order, offsets inside each buffer.
+        A piece is one holder's run of a parameter, so it lies in one buffer."""
+        index = {key: i for i, (key, _, _) in enumerate(self.specs)}
+        out = pieces.copy()
+        for r in out:
+            key, local = self.locate(int(r["buf"]), int(r["buf_off"]), int(r["len"]))
+            r["buf"] = index[key]
+            r["buf_off"] = local
+        return out
+
+    def byte_sizes(self) -> List[int]:
+        """Bytes of every buffer, in ``specs`` order."""
+        return [n * (2 if d == "bf16" else 4) for _, d, n in self.specs]
 
 
 def _last_at_or_below(starts: List[int], x: int) -> int:

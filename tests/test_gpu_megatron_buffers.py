@@ -94,3 +94,54 @@ def test_switch_on_megatron_flat_buffers(gpu_device, factory, src, dst):
     world = oracle1.build_src_world(inv, spec, strat(src), SEED)
     dw, dbf, _ = oracle1.transfer(inv, spec, strat(src), strat(dst), world)
     assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []
+
+
+def _gap_damage(buffers, views, keys_of_views):
+    """Padding elements (outside every view) that lost their canary, read gap by gap."""
+    runs = {}
+    for v, k in zip(views, keys_of_views):
+        off = v.storage_offset() - buffers[k].storage_offset()
+        runs.setdefault(k, []).append((off, off + v.numel()))
+    bad = 0
+    for k, t in buffers.items():
+        bits = t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+        canary = CANARY16 if t.dtype == torch.bfloat16 else CANARY32
+        at = 0
+        for a, b in sorted(runs.get(k, [])) + [(t.numel(), t.numel())]:
+            if a > at:
+                bad += int(torch.count_nonzero(bits[at:a] != canary))
+            at = max(at, b)
+    return bad
+
+
+@pytest.mark.parametrize("src,dst", [pytest.param(PS(8, 1, 1), PS(8, 4, 1), id="llama2-7b-tp1dp8-tp4dp2"),
+                                     pytest.param(PS(8, 1, 1), PS(6, 1, 1), id="llama2-7b-dp8-dp6")])
+def test_full_size_switch_on_megatron_buffers(gpu_device, src, dst):
+    """Llama-2-7B switched directly on Megatron-shaped buffers: each buffer its own allocation, the
+    source filled with the seeded values through the remapped pieces, every stored destination
+    element checked against the generator on the device, every padding element's canary kept."""
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.resharding import model_spec as ms
+
+    print(f"case megatron buffers full size {src} -> {dst}", flush=True)
+    space = build_virtual_model(ms.llama2_7b())
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    plan = tm.compile_tensors(ls, ld)
+    ms_, md = MegatronBuffers(ls), MegatronBuffers(ld)
+    try:
+        sbuf, dbuf = ms_.allocate(gpu_device), md.allocate(gpu_device)
+        _canary(dbuf)
+        st = torch.cuda.current_stream().cuda_stream
+        _native.synth_fill(ms_.remap_pieces(ls.pieces()), [sbuf[k].data_ptr() for k in ms_.keys()],
+                           ms_.byte_sizes(), SEED, st)
+        src_views, dst_views = ms_.tensor_views(plan.src, sbuf), md.tensor_views(plan.dst, dbuf)
+        tm.execute_tensors(plan, src_views, dst_views)
+        bad, first = _native.synth_verify(md.remap_pieces(ld.pieces()), [dbuf[k].data_ptr() for k in md.keys()],
+                                          md.byte_sizes(), SEED, st)
+        assert bad == 0, first
+        dkeys = [md.locate(ar, o, n)[0] for ar, o, n in zip(plan.dst.arena, plan.dst.offset, plan.dst.numel)]
+        assert _gap_damage(dbuf, dst_views, dkeys) == 0
+    finally:
+        sbuf = dbuf = src_views = dst_views = None  # noqa: F841
+        torch.cuda.empty_cache()

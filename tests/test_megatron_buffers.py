@@ -86,3 +86,26 @@ def test_views_sit_where_megatron_keeps_them(factory, ps):
     # Uncovered elements are exactly the padding: buffer sizes minus stored elements.
     stored = sum(int(t.sum()) for t in bufs.values())
     assert stored == sum(tb.numel)
+
+
+@pytest.mark.parametrize("factory,ps", CASES, ids=lambda x: getattr(x, "__name__", str(x))[:40])
+def test_remapped_pieces_fill_the_same_values(factory, ps):
+    """The generator's pieces re-expressed over the flat buffers write, into every view, what the
+    arena pieces write into the same tensor of the arena layout."""
+    import numpy as np
+
+    from tests.helpers import SEED, new_arenas, piece_fill_numpy
+
+    lay = build_virtual_model(factory()).layout(ps)
+    mb, tb = MegatronBuffers(lay), TensorBuffers(lay)
+    arenas = new_arenas(lay, fill=0)
+    piece_fill_numpy(lay.pieces(), arenas, SEED)
+    flat = [np.zeros(n, dtype=np.uint16 if d == "bf16" else np.uint32) for _, d, n in mb.specs]
+    piece_fill_numpy(mb.remap_pieces(lay.pieces()), flat, SEED)
+    bufs = {k: torch.from_numpy(x.view(np.int16) if x.dtype == np.uint16 else x.view(np.int32))
+            for k, x in zip(mb.keys(), flat)}
+    views = mb.tensor_views(tb, bufs)
+    for a, off, n, v in zip(tb.arena, tb.offset, tb.numel, views):
+        want = arenas[a][off:off + n]
+        assert np.array_equal(v.numpy().view(want.dtype), want)
+    assert mb.byte_sizes() == [x.nbytes for x in flat]
