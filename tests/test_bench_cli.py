@@ -29,8 +29,11 @@ def test_more_than_one_gpu_is_refused_with_a_reason():
 def test_launch_shape_flags_are_checked_before_any_device_work():
     r = _run("--lanes", "96")
     assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""
+    r = _run("--units", "3")
+    assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""
     r = _run("--help")
-    assert r.returncode == 0 and "--lanes" in r.stdout and "--persistent" in r.stdout
+    assert r.returncode == 0 and all(f in r.stdout for f in ("--lanes", "--units", "--persistent", "--megatron-buffers",
+                                                              "--low-memory", "--tensors"))
 
 
 @pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="checks the behaviour without a GPU")
