@@ -27,7 +27,11 @@ Contents
 Parity status
   megatron_buffer: parity unpinned.  Megatron-core (core_r0.11.0) is not
   vendored with the reference and cannot be imported here; its layout rules
-  are restated from its published algorithm and checked only by invariants.
+  are restated from its published algorithm and checked by invariants and by
+  known answers derived by hand from that algorithm for every branch
+  (reverse order, start and end padding, the >= bucket close, shared
+  embeddings, expert buffers; tests/test_ddp_layout.py), never against
+  Megatron itself.
   canonical.world(vocab_rows=...): the vocabulary re-padding extension has
   no counterpart in the reference (virtual_param.py:480-481 keeps the padded
   vocabulary fixed); it is an invariant (kept rows keep their values, new

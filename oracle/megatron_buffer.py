@@ -4,7 +4,8 @@ Restates the published layout algorithm of megatron/core/distributed/
 param_and_grad_buffer.py (core_r0.11.0), which the reference obtains by
 instantiating ``_ParamAndGradBuffer`` under mocks
 (elastic_megatron/resharding/resharding_dp.py:155-315).  Megatron-core is not
-available here, so this restatement is checked by invariants only.
+available here, so this restatement is checked by invariants and by known
+answers derived by hand from the published algorithm (parity unpinned).
 """
 
 import math
