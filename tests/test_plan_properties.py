@@ -108,3 +108,42 @@ def test_switch_to_the_same_strategy_reproduces_the_state(sw):
     got32, gotbf = extract(la, out)
     want32, wantbf = extract(la, arena)
     assert compare(got32, gotbf, want32, wantbf) == []
+
+
+@settings(max_examples=15, deadline=None, suppress_health_check=[HealthCheck.filter_too_much, HealthCheck.too_slow])
+@given(switches())
+def test_megatron_buffer_views_tile_the_stored_elements(sw):
+    """Over drawn layouts, the views MegatronBuffers hands out are disjoint, lie inside their
+    buffers, cover exactly the layout's stored elements, and the remapped generator pieces land
+    in the same views as the arena pieces."""
+    import numpy as np
+    import torch
+
+    from elasticmegatron_amd.resharding.megatron_buffers import MegatronBuffers
+    from elasticmegatron_amd.resharding.tensors import TensorBuffers
+
+    spec, a, _ = sw
+    space = build_virtual_model(spec)
+    try:
+        lay = space.layout(a)
+    except (AssertionError, RuntimeError, ValueError):
+        assume(False)
+    mb, tb = MegatronBuffers(lay), TensorBuffers(lay)
+    flat = [np.zeros(n, dtype=np.uint16 if d == "bf16" else np.uint32) for _, d, n in mb.specs]
+    piece_fill_numpy(mb.remap_pieces(lay.pieces()), flat, SEED)
+    hits = [np.zeros(x.size, dtype=np.int32) for x in flat]
+    bufs = {k: torch.from_numpy(x.view(np.int16) if x.dtype == np.uint16 else x.view(np.int32))
+            for k, x in zip(mb.keys(), flat)}
+    index = {k: i for i, k in enumerate(mb.keys())}
+    arenas = new_arenas(lay, fill=0)
+    piece_fill_numpy(lay.pieces(), arenas, SEED)
+    for ar, off, n, v in zip(tb.arena, tb.offset, tb.numel, mb.tensor_views(tb, bufs)):
+        key, local = mb.locate(ar, off, n)
+        hits[index[key]][local:local + n] += 1
+        assert np.array_equal(v.numpy().view(arenas[ar].dtype), arenas[ar][off:off + n])
+    assert all(int(h.max(initial=0)) <= 1 for h in hits)
+    covered = sum(int(h.sum()) for h in hits)
+    assert covered == sum(tb.numel)
+    fp32 = sum(n for ar, n in zip(tb.arena, tb.numel) if ar != 3)   # three kinds
+    bf16 = sum(n for ar, n in zip(tb.arena, tb.numel) if ar == 3)
+    assert 4 * fp32 + 2 * bf16 == _stored_bytes(lay)
