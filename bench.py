@@ -88,7 +88,7 @@ def parse():
                     help="0: one workgroup per chunk of 256 units; 1: persistent grid (the next three flags)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
     ap.add_argument("--nontemporal", type=int, default=1)
-    ap.add_argument("--xcd-remap", type=int, default=1, help="persistent grid")
+    ap.add_argument("--xcd-remap", type=int, default=1, help="1: each XCD takes one contiguous eighth of the chunks (either grid)")
     ap.add_argument("--run", type=int, default=4,
                     help="persistent grid; 0: contiguous chunk run per workgroup; N: round-robin runs of 8N chunks")
     ap.add_argument("--megatron-buffers", action="store_true",

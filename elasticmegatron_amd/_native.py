@@ -150,8 +150,8 @@ def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool
                persistent: bool = False, lanes: int = 0, units: int = 0, buffer_ops: bool = False) -> None:
     """Launch shape of every later execution.  The default runs one workgroup of ``lanes`` lanes
     (0: 64) with ``units`` 16-byte units each (0: a whole chunk of 256 units per workgroup) per piece
-    of a chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu``, ``xcd_remap``
-    and ``run`` shape."""
+    of a chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu`` and ``run``
+    shape.  ``xcd_remap`` (either grid) gives each of the 8 XCDs one contiguous eighth of the chunks."""
     t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run, 1 if persistent else 0, lanes,
                units, 1 if buffer_ops else 0)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")

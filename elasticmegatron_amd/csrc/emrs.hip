@@ -134,20 +134,32 @@ struct DevSeg {
   uint32_t dst_stride;
   uint32_t aux_stride;
   uint32_t magic;        // row = (t + ((u - t) >> sh1)) >> sh2, t = umulhi(magic, u)
-  uint16_t src_buf;
-  uint16_t dst_buf;
-  uint16_t aux_buf;
-  uint8_t sh;            // bits 0-4: sh2; bit 5: sh1
-  uint8_t bits;          // bits 0-2: unit_log2; bits 3-4: elem_log2; bits 5-7: ops
+  // Whole 32-bit words only, so that a workgroup reads its descriptor with
+  // scalar loads alone (the compiler reads 8- and 16-bit fields with vector
+  // loads, which put a vector-memory round trip ahead of the workgroup's data).
+  uint32_t bufs;         // bits 0-15: source buffer; bits 16-31: destination buffer
+  uint32_t meta;         // bits 0-15: second destination (aux) buffer; 16-23: shifts; 24-31: kind
 
-  // ops bit 0: also write bf16 to aux; bit 1: write zeros, read nothing;
-  // bit 2: also write the values unchanged to aux.  elem_log2: element size of
-  // the input segment (read by the compare kernel and for duplicates).
-  __host__ __device__ uint32_t sh1() const { return (sh >> 5) & 1u; }
-  __host__ __device__ uint32_t sh2() const { return sh & 31u; }
-  __host__ __device__ uint32_t unit_log2() const { return bits & 7u; }
-  __host__ __device__ uint32_t elem_log2() const { return (bits >> 3) & 3u; }
-  __host__ __device__ uint32_t ops() const { return (bits >> 5) & 7u; }
+  // shifts: bits 0-4 sh2, bit 5 sh1.  kind: bits 0-2 unit_log2, bits 3-4
+  // elem_log2, bits 5-7 ops.  ops bit 0: also write bf16 to aux; bit 1: write
+  // zeros, read nothing; bit 2: also write the values unchanged to aux.
+  // elem_log2: element size of the input segment (read by the compare kernel
+  // and for duplicates).
+  __host__ __device__ uint32_t src_buf() const { return bufs & 0xffffu; }
+  __host__ __device__ uint32_t dst_buf() const { return bufs >> 16; }
+  __host__ __device__ uint32_t aux_buf() const { return meta & 0xffffu; }
+  __host__ __device__ uint32_t sh1() const { return (meta >> 21) & 1u; }
+  __host__ __device__ uint32_t sh2() const { return (meta >> 16) & 31u; }
+  __host__ __device__ uint32_t unit_log2() const { return (meta >> 24) & 7u; }
+  __host__ __device__ uint32_t elem_log2() const { return (meta >> 27) & 3u; }
+  __host__ __device__ uint32_t ops() const { return meta >> 29; }
+  void set_bufs(uint32_t src, uint32_t dst, uint32_t aux) {
+    bufs = (src & 0xffffu) | (dst << 16);
+    meta = (meta & 0xffff0000u) | (aux & 0xffffu);
+  }
+  void set_kind(uint32_t sh2_, uint32_t sh1_, uint32_t unit_log2_, uint32_t elem_log2_, uint32_t ops_) {
+    meta = (meta & 0xffffu) | ((sh2_ | (sh1_ << 5)) << 16) | ((unit_log2_ | (elem_log2_ << 3) | (ops_ << 5)) << 24);
+  }
 };
 static_assert(sizeof(DevSeg) == 64, "DevSeg layout");
 
@@ -341,9 +353,9 @@ __device__ __forceinline__ void copy_chunk_run(const DevSeg *__restrict__ segs, 
     const uint32_t total = s.len * s.rows;
     const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits;
     const uint32_t u_end = min(u0 + (uint32_t)nq * kChunkUnits, total);
-    const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
-    char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
-    char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+    const char *sb = base_of<kTable>(src, src_tab, s.src_buf());
+    char *db = base_of<kTable>(dst, dst_tab, s.dst_buf());
+    char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf());
     const uint32_t ops = s.ops(), ul = s.unit_log2();
     if (ops & 4) {  // duplicate to aux, with or without zero fill
       if (ops & 2) dispatch_units<kNT, false, true, true>(ul, s, sb, db, ab, u0, u_end);
@@ -598,14 +610,24 @@ __device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, con
 // L = 64 and U = 4 a chunk is one wave: one search per 4 KB, four loads in
 // flight per lane.  With 256 lanes four waves repeat the same search for one
 // 16-byte load each, and the launch runs about 20% slower.
+//
+// xcd_share != 0: the first 8 * xcd_share workgroups are renumbered so that
+// each XCD (the hardware deals workgroups out to the 8 XCDs round-robin, so
+// workgroup w runs on XCD w % 8) works through one contiguous share of them,
+// in order: workgroup w takes piece (w % 8) * xcd_share + w / 8.  The
+// workgroups resident on one XCD then touch a window of the plan one eighth
+// as wide as when all eight XCDs share one window, so that XCD's L2 and
+// address-translation caches hold fewer pages at a time.  The rest (fewer
+// than 8) keep their own numbers.
 template <bool kNT, bool kTable, int L, int U, bool kBuf>
 __global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint64_t n_chunks,
                                                       SegHint hint, Bases src, Bases dst,
                                                       const uint64_t *__restrict__ src_tab,
-                                                      const uint64_t *__restrict__ dst_tab) {
+                                                      const uint64_t *__restrict__ dst_tab, uint64_t xcd_share) {
   constexpr uint32_t kPieces = kChunkUnits / (L * U);  // pieces per chunk: 1, 2 or 4
   static_assert(kPieces * L * U == kChunkUnits, "a piece divides a chunk");
-  const uint64_t w = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  uint64_t w = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  if (w < xcd_share * 8) w = (w & 7) * xcd_share + (w >> 3);
   const uint64_t c = w / kPieces;
   if (c >= n_chunks) return;
   const uint32_t b = (uint32_t)(c >> hint.shift);
@@ -619,9 +641,9 @@ __global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__
   const uint32_t total = s.len * s.rows;
   const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits + (uint32_t)(w % kPieces) * (L * U);
   if (kPieces > 1 && u0 >= total) return;
-  const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
-  char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
-  char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+  const char *sb = base_of<kTable>(src, src_tab, s.src_buf());
+  char *db = base_of<kTable>(dst, dst_tab, s.dst_buf());
+  char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf());
   const uint32_t ops = s.ops(), ul = s.unit_log2();
   if constexpr (kBuf) {  // every unit width through buffer instructions
     if (ops & 4) {
@@ -806,12 +828,9 @@ struct Builder {
     d.dst_stride = rows > 1 ? ds : 0;
     uint32_t sh1 = 0, sh2 = 0;
     make_magic(len, &d.magic, &sh1, &sh2);
-    d.sh = (uint8_t)(sh2 | (sh1 << 5));
     const uint32_t ops = (ax.cast ? 1u : 0u) | (ax.zero ? 2u : 0u) | (ax.dup ? 4u : 0u);
-    d.bits = (uint8_t)(ul | ((uint32_t)cur_elem_log2 << 3) | (ops << 5));
-    d.src_buf = (uint16_t)sbuf;
-    d.dst_buf = (uint16_t)dbuf;
-    d.aux_buf = (uint16_t)(ax.on ? ax.buf : dbuf);
+    d.set_kind(sh2, sh1, ul, cur_elem_log2, ops);
+    d.set_bufs(sbuf, dbuf, ax.on ? ax.buf : dbuf);
     d.aux_off = ax.on ? aoff : 0;
     d.aux_stride = ax.on && rows > 1 ? astride : 0;
     const uint64_t units = (uint64_t)len * rows;
@@ -1038,10 +1057,10 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_
     for (DevSeg &d : segs) {
       const uint32_t ul = d.unit_log2(), ops = d.ops();
       const uint32_t aux_log2 = (ops & 1) ? ul - 1 : ul;  // a bf16 image unit is half a unit
-      d.src_off = (ops & 2) ? 0 : d.src_off + units_from_lo(rb.ptrs[d.src_buf], ul);
-      d.dst_off += units_from_lo(rb.ptrs[ns + d.dst_buf], ul);
-      d.aux_off += units_from_lo(rb.ptrs[ns + d.aux_buf], aux_log2);
-      d.src_buf = d.dst_buf = d.aux_buf = 0;
+      d.src_off = (ops & 2) ? 0 : d.src_off + units_from_lo(rb.ptrs[d.src_buf()], ul);
+      d.dst_off += units_from_lo(rb.ptrs[ns + d.dst_buf()], ul);
+      d.aux_off += units_from_lo(rb.ptrs[ns + d.aux_buf()], aux_log2);
+      d.set_bufs(0, 0, 0);
     }
     const size_t bytes = segs.size() * sizeof(DevSeg);
     DevSeg *t = nullptr;
@@ -1315,9 +1334,9 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
       const uint32_t total = s.len * s.rows;
       const uint32_t u0 = (uint32_t)(q - s.chunk_begin) * kChunkUnits;
       const uint32_t u_end = min(u0 + (uint32_t)nq * kChunkUnits, total);
-      const char *sb = base_of<kTable>(src, src_tab, s.src_buf);
-      const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf);
-      const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf);
+      const char *sb = base_of<kTable>(src, src_tab, s.src_buf());
+      const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf());
+      const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf());
       switch (s.unit_log2()) {
         case 4: compare_chunk<u32x4>(s, sb, db, ab, u0, u_end, m, x); break;
         case 3: compare_chunk<uint64_t>(s, sb, db, ab, u0, u_end, m, x); break;
@@ -1607,18 +1626,19 @@ template <int L, int U, bool kBuf>
 void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table,
                    uint64_t n_chunks, const SegHint &hint, const uint64_t *stab, const uint64_t *dtab) {
   const dim3 block(L);
+  const uint64_t xcd_share = g_tuning.xcd_remap.load() ? n_chunks * (kChunkUnits / (L * U)) / 8 : 0;
   if (nt && rb.table)
     hipLaunchKernelGGL((copy_plan_kernel<true, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab);
+                       rb.src, rb.dst, stab, dtab, xcd_share);
   else if (nt)
     hipLaunchKernelGGL((copy_plan_kernel<true, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab);
+                       rb.src, rb.dst, stab, dtab, xcd_share);
   else if (rb.table)
     hipLaunchKernelGGL((copy_plan_kernel<false, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab);
+                       rb.src, rb.dst, stab, dtab, xcd_share);
   else
     hipLaunchKernelGGL((copy_plan_kernel<false, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab);
+                       rb.src, rb.dst, stab, dtab, xcd_share);
 }
 
 // The one-workgroup-per-piece launch for `lanes` lanes of `units` units each.
