@@ -85,10 +85,12 @@ def parse():
     ap.add_argument("--units", type=int, default=0, choices=(0, 1, 2, 4),
                     help="16-byte units per lane (0: a whole chunk per workgroup, 256 / lanes)")
     ap.add_argument("--persistent", type=int, default=0,
-                    help="0: one workgroup per chunk of 256 units; 1: persistent grid (the next three flags)")
+                    help="0: one workgroup per chunk of 256 units; 1: persistent grid (--blocks-per-cu, --run)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
     ap.add_argument("--nontemporal", type=int, default=1)
-    ap.add_argument("--xcd-remap", type=int, default=1, help="1: each XCD takes one contiguous eighth of the chunks (either grid)")
+    ap.add_argument("--xcd-remap", type=int, default=1, choices=(0, 1, 2),
+                    help="each XCD takes one contiguous eighth of the chunks: 1 in the persistent grid and for "
+                         "plans of at least 2^19 chunks, 2 always, 0 never")
     ap.add_argument("--run", type=int, default=4,
                     help="persistent grid; 0: contiguous chunk run per workgroup; N: round-robin runs of 8N chunks")
     ap.add_argument("--megatron-buffers", action="store_true",
@@ -193,7 +195,7 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _native.load()
-    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), bool(args.xcd_remap), args.run,
+    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), args.xcd_remap, args.run,
                        bool(args.persistent), args.lanes, args.units)
     stream = torch.cuda.current_stream(dev)
 

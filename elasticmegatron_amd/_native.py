@@ -146,13 +146,14 @@ def get_tuning() -> Tuning:
     return t
 
 
-def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: bool = True, run: int = 4,
+def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: int = 1, run: int = 4,
                persistent: bool = False, lanes: int = 0, units: int = 0, buffer_ops: bool = False) -> None:
     """Launch shape of every later execution.  The default runs one workgroup of ``lanes`` lanes
     (0: 64) with ``units`` 16-byte units each (0: a whole chunk of 256 units per workgroup) per piece
     of a chunk; ``persistent=True`` selects a persistent grid, which ``blocks_per_cu`` and ``run``
-    shape.  ``xcd_remap`` (either grid) gives each of the 8 XCDs one contiguous eighth of the chunks."""
-    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, 1 if xcd_remap else 0, run, 1 if persistent else 0, lanes,
+    shape.  ``xcd_remap`` gives each of the 8 XCDs one contiguous eighth of the chunks: 1 (or True) in
+    the persistent grid and for plans of at least 2^19 chunks, 2 always, 0 (or False) never."""
+    t = Tuning(blocks_per_cu, 1 if nontemporal else 0, int(xcd_remap), run, 1 if persistent else 0, lanes,
                units, 1 if buffer_ops else 0)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 

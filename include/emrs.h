@@ -248,9 +248,11 @@ typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
                              0 (default): as many as can be resident at once */
   uint32_t nontemporal;   /* 1: streaming (non-temporal) loads and stores (default 1) */
-  uint32_t xcd_remap;     /* 1 (default): each XCD works through one contiguous eighth of the
-                             chunks (workgroup b runs on XCD b % 8), in either grid; 0: workgroup b
-                             takes piece b (one workgroup per piece) or the b-th run (persistent) */
+  uint32_t xcd_remap;     /* 0, 1 (default) or 2.  Nonzero: each XCD works through one contiguous
+                             eighth of the chunks (workgroup b runs on XCD b % 8); the persistent
+                             grid does so for 1 and 2, one workgroup per piece for 2 and, with 1,
+                             for plans of at least 2^19 chunks.  0: workgroup b takes piece b (one
+                             workgroup per piece) or the b-th run (persistent) */
   uint32_t run;           /* persistent grid, 0: each workgroup copies one contiguous run of
                              chunks; N in [1, 2^20]: chunks are dealt out round-robin in runs of
                              8N, capped at a quarter of a workgroup's share (default 4) */

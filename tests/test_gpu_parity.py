@@ -135,9 +135,9 @@ def test_manager_repad_round_trip(gpu_device):
                                     dict(buffer_ops=True), dict(buffer_ops=True, nontemporal=False),
                                     dict(buffer_ops=True, units=1), dict(buffer_ops=True, lanes=256),
                                     dict(buffer_ops=True, lanes=128, units=2),
-                                    dict(xcd_remap=False), dict(units=1, xcd_remap=False),
-                                    dict(lanes=256, units=1, xcd_remap=False),
-                                    dict(buffer_ops=True, xcd_remap=False),
+                                    dict(xcd_remap=False), dict(xcd_remap=2), dict(units=1, xcd_remap=2),
+                                    dict(lanes=256, units=1, xcd_remap=2), dict(lanes=128, units=2, xcd_remap=2),
+                                    dict(buffer_ops=True, xcd_remap=2), dict(nontemporal=False, xcd_remap=2),
                                     dict(persistent=True),
                                     dict(persistent=True, run=0), dict(persistent=True, run=0, xcd_remap=False),
                                     dict(persistent=True, run=1), dict(persistent=True, run=64),

@@ -242,9 +242,13 @@ def test_tuning_defaults_and_rejections():
         assert _native.get_tuning().units == 2   # 0: one chunk of 256 units per workgroup
         _native.set_tuning(lanes=64, units=1, buffer_ops=True)
         assert (_native.get_tuning().lanes, _native.get_tuning().units, _native.get_tuning().buffer_ops) == (64, 1, 1)
+        for x in (0, 2, 1):
+            _native.set_tuning(xcd_remap=x)
+            assert _native.get_tuning().xcd_remap == x
         _native.set_tuning(lanes=128, persistent=True, run=7, blocks_per_cu=3)
         for kw in (dict(lanes=96), dict(lanes=512), dict(run=(1 << 20) + 1), dict(blocks_per_cu=65),
-                   dict(units=3), dict(units=8), dict(lanes=128, units=4), dict(lanes=256, units=2)):
+                   dict(units=3), dict(units=8), dict(lanes=128, units=4), dict(lanes=256, units=2),
+                   dict(xcd_remap=3)):
             with pytest.raises(_native.EmrsError) as e:
                 _native.set_tuning(**kw)
             assert e.value.code == -1
@@ -254,4 +258,4 @@ def test_tuning_defaults_and_rejections():
     finally:
         _native.set_tuning()
     t = _native.get_tuning()
-    assert (t.persistent, t.lanes, t.units, t.run, t.blocks_per_cu) == (0, 64, 4, 4, 0)
+    assert (t.persistent, t.lanes, t.units, t.run, t.blocks_per_cu, t.xcd_remap) == (0, 64, 4, 4, 0, 1)
