@@ -178,7 +178,7 @@ def main():
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
         print("bench.py measures one GPU: the reshard is simulated for every rank on a single device; "
-              "run it with --gpus 1 (multi-GPU runs are not part of this build).", file=sys.stderr)
+              "run it with --gpus 1 (the benchmark has no multi-GPU mode).", file=sys.stderr)
         return 2
 
     import torch

@@ -1,4 +1,4 @@
-// Synthetic optimizer-state generator and checker for the reshard repack.
+// Synthetic optimizer-state generator and on-device verifier for the reshard repack.
 //
 // Each value is a pure function of (seed, parameter id, kind, full flat
 // index), so any shard of any layout can be produced or checked on its own.

@@ -175,7 +175,7 @@ class ElasticMegatronManager:
         return t.elapsed
 
     def log_communication_info(self, transfer_time: float, logger: Optional[logging.Logger] = None) -> str:
-        """The reference's perf line (elastic_manager.py:158-178) plus this build's HBM payload.
+        """The reference's perf line (elastic_manager.py:158-178) plus the payload written on the device.
 
         ``communication bytes`` keeps the reference's definition (GiB a rank
         would exchange with other ranks, max over ranks); ``payload`` is the
