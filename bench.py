@@ -244,17 +244,22 @@ def main():
     print(f"[bench] {args.workload}: plan {plan.segments.shape[0]} segments, payload {plan.payload_bytes / 1e9:.2f} GB,"
           f" planning {t_plan:.2f}s", file=sys.stderr, flush=True)
 
+    def check_destination():
+        """Every destination element against the generator; None when --no-verify."""
+        if args.no_verify:
+            return None
+        vocab_rows = ls.space.spec.padded_vocab_size if repad else None
+        bad, first = b.verify_synthetic(SEED, bf16=backup is None, vocab_rows=vocab_rows)
+        if bad:
+            print(f"[bench] verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+        return bad == 0
+
     for _ in range(args.warmup):
         step(a, b)
     torch.cuda.synchronize()
-    verified = None
-    if not args.no_verify:
-        vocab_rows = ls.space.spec.padded_vocab_size if repad else None
-        bad, first = b.verify_synthetic(SEED, bf16=backup is None, vocab_rows=vocab_rows)
-        verified = bad == 0
-        if bad:
-            print(f"[bench] verification FAILED: {bad} elements, first {first}", file=sys.stderr)
-            return 3
+    verified = check_destination() if args.warmup else None  # without a warm-up, after the timed steps
+    if verified is False:
+        return 3
 
     events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
@@ -265,6 +270,10 @@ def main():
         events[i + 1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1e3
+    if not args.warmup:
+        verified = check_destination()
+        if verified is False:
+            return 3
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = sum(step_ms) / len(step_ms)
     payload = plan.payload_bytes
@@ -467,17 +476,22 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
     print(f"[bench] {args.workload} on Megatron buffers: {len(ms_.specs)} source and {len(md.specs)} destination "
           f"buffers, {len(plan.src)} / {len(plan.dst)} tensors, {plan.segments.shape[0]} segments",
           file=sys.stderr, flush=True)
+    def check_destination():
+        """Every destination element against the generator; None when --no-verify."""
+        if args.no_verify:
+            return None
+        bad, _ = _native.synth_verify(md.remap_pieces(ld.pieces(include_bf16=backup is None)), d_ptrs,
+                                      md.byte_sizes(), SEED, stream.cuda_stream)
+        if bad:
+            print(f"[bench] verification FAILED: {bad} elements", file=sys.stderr)
+        return bad == 0
+
     for _ in range(args.warmup):
         tm.execute_tensors(plan, src_views, dst_views, stream)
     torch.cuda.synchronize()
-    verified = None
-    if not args.no_verify:
-        bad, _ = _native.synth_verify(md.remap_pieces(ld.pieces(include_bf16=backup is None)), d_ptrs,
-                                      md.byte_sizes(), SEED, stream.cuda_stream)
-        verified = bad == 0
-        if bad:
-            print(f"[bench] verification FAILED: {bad} elements", file=sys.stderr)
-            return 3
+    verified = check_destination() if args.warmup else None  # without a warm-up, after the timed steps
+    if verified is False:
+        return 3
     events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     events[0].record(stream)
@@ -485,6 +499,10 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
         tm.execute_tensors(plan, src_views, dst_views, stream)
         events[i + 1].record(stream)
     torch.cuda.synchronize()
+    if not args.warmup:
+        verified = check_destination()
+        if verified is False:
+            return 3
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = sum(step_ms) / len(step_ms)
     traffic_gbps = arena_plan.traffic_bytes / (ms / 1e3) / 1e9
