@@ -82,10 +82,12 @@ def parse():
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
                     help="one workgroup per piece of a chunk of 256 units: lanes per workgroup (0: the default, 64)")
-    ap.add_argument("--units", type=int, default=0, choices=(0, 1, 2, 4),
-                    help="16-byte units per lane (0: a whole chunk per workgroup, 256 / lanes)")
+    ap.add_argument("--units", type=int, default=1, choices=(0, 1, 2, 4),
+                    help="16-byte units per lane (default 1; 0: a whole chunk per workgroup, 256 / lanes)")
+    ap.add_argument("--chunk-index", type=int, default=1, choices=(0, 1),
+                    help="1: each workgroup reads its segment from the plan's chunk table; 0: binary search")
     ap.add_argument("--persistent", type=int, default=0,
-                    help="0: one workgroup per chunk of 256 units; 1: persistent grid (--blocks-per-cu, --run)")
+                    help="0: one workgroup per piece of a chunk; 1: persistent grid (--blocks-per-cu, --run)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
     ap.add_argument("--nontemporal", type=int, default=1)
     ap.add_argument("--xcd-remap", type=int, default=1, choices=(0, 1, 2),
@@ -196,7 +198,7 @@ def main():
     torch.cuda.set_device(dev)
     _native.load()
     _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), args.xcd_remap, args.run,
-                       bool(args.persistent), args.lanes, args.units)
+                       bool(args.persistent), args.lanes, args.units, chunk_index=bool(args.chunk_index))
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:

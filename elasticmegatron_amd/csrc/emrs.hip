@@ -191,12 +191,13 @@ __host__ __device__ __forceinline__ uint32_t magic_div(uint32_t n, uint32_t m, u
 struct Tuning {
   std::atomic<uint32_t> blocks_per_cu{0};  // persistent grid: 0 = as many as can be resident
   std::atomic<uint32_t> nontemporal{1};
-  std::atomic<uint32_t> xcd_remap{1};      // persistent grid
+  std::atomic<uint32_t> xcd_remap{1};      // 0, 1 (by plan size) or 2
   std::atomic<uint32_t> run{4};            // persistent grid: round-robin runs of 4 x kUnroll chunks
   std::atomic<uint32_t> persistent{0};     // 0: one workgroup per chunk
   std::atomic<uint32_t> lanes{64};         // lanes per workgroup of one piece: 64, 128 or 256
-  std::atomic<uint32_t> units{4};          // 16-byte units per lane: lanes * units is 64, 128 or 256
+  std::atomic<uint32_t> units{1};          // 16-byte units per lane: lanes * units is 64, 128 or 256
   std::atomic<uint32_t> buffer_ops{0};     // 1: 16-byte units through buffer instructions
+  std::atomic<uint32_t> chunk_index{1};    // 1: each chunk's segment from the plan's chunk table
 };
 Tuning g_tuning;
 
@@ -628,19 +629,26 @@ template <bool kNT, bool kTable, int L, int U, bool kBuf>
 __global__ __launch_bounds__(L) void copy_plan_kernel(const DevSeg *__restrict__ segs, uint64_t n_chunks,
                                                       SegHint hint, Bases src, Bases dst,
                                                       const uint64_t *__restrict__ src_tab,
-                                                      const uint64_t *__restrict__ dst_tab, uint64_t xcd_share) {
+                                                      const uint64_t *__restrict__ dst_tab, uint64_t xcd_share,
+                                                      const uint32_t *__restrict__ chunk_seg) {
   constexpr uint32_t kPieces = kChunkUnits / (L * U);  // pieces per chunk: 1, 2 or 4
   static_assert(kPieces * L * U == kChunkUnits, "a piece divides a chunk");
   uint64_t w = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
   if (w < xcd_share * 8) w = (w & 7) * xcd_share + (w >> 3);
   const uint64_t c = w / kPieces;
   if (c >= n_chunks) return;
-  const uint32_t b = (uint32_t)(c >> hint.shift);
-  uint32_t lo = hint.first[b], hi = hint.first[b + 1];
-  while (lo < hi) {
-    const uint32_t mid = (lo + hi + 1) >> 1;
-    if (segs[mid].chunk_begin <= c) lo = mid;
-    else hi = mid - 1;
+  uint32_t lo;
+  if (chunk_seg) {  // the segment of every chunk, looked up
+    lo = chunk_seg[c];
+  } else {  // found by a binary search bounded by the hint
+    const uint32_t b = (uint32_t)(c >> hint.shift);
+    lo = hint.first[b];
+    uint32_t hi = hint.first[b + 1];
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (segs[mid].chunk_begin <= c) lo = mid;
+      else hi = mid - 1;
+    }
   }
   const DevSeg s = segs[lo];
   const uint32_t total = s.len * s.rows;
@@ -752,6 +760,9 @@ struct emrs_plan {
   emrs_plan_stats stats{};
   std::mutex mu;
   std::vector<DevSeg *> dev_tables;  // per device, uploaded on first use
+  // Per device, uploaded on first use when emrs_tuning.chunk_index is set:
+  // the device segment of every chunk (4 bytes per 4 KB chunk).
+  std::vector<uint32_t *> chunk_tables;
   // Plans with more than kArgBuffers buffers on a side: per device, the
   // pointer table of the first execution and the base pointers it holds.
   std::vector<uint64_t *> ptr_tables;
@@ -1081,6 +1092,34 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_
   }
   *out = plan->abs_tables[dev];
   *common = reinterpret_cast<char *>(plan->abs_base[dev]);
+  return EMRS_OK;
+}
+
+// The device segment of every chunk on device `dev`, built and uploaded on
+// first use and never written again.
+int chunk_table(emrs_plan *plan, int dev, hipStream_t st, uint32_t **out) {
+  std::lock_guard<std::mutex> lk(plan->mu);
+  if ((int)plan->chunk_tables.size() <= dev) plan->chunk_tables.resize(dev + 1, nullptr);
+  if (!plan->chunk_tables[dev]) {
+    if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
+    if (plan->segs.size() > 0xffffffffull) return fail(EMRS_ERR_INVALID_ARGUMENT, "too many device segments");
+    std::vector<uint32_t> seg_of(plan->n_chunks);
+    for (size_t k = 0; k < plan->segs.size(); ++k) {
+      const uint64_t c1 = k + 1 < plan->segs.size() ? plan->segs[k + 1].chunk_begin : plan->n_chunks;
+      std::fill(seg_of.begin() + plan->segs[k].chunk_begin, seg_of.begin() + c1, (uint32_t)k);
+    }
+    const size_t bytes = seg_of.size() * sizeof(uint32_t);
+    uint32_t *t = nullptr;
+    hipError_t e = hipMalloc(&t, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(chunk table)");
+    e = hipMemcpy(t, seg_of.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(t);
+      return hip_fail(e, "hipMemcpy(chunk table)");
+    }
+    plan->chunk_tables[dev] = t;
+  }
+  *out = plan->chunk_tables[dev];
   return EMRS_OK;
 }
 
@@ -1629,37 +1668,38 @@ int emrs_plan_create(const emrs_segment *segs, uint64_t n_segs, const uint64_t *
 namespace {
 template <int L, int U, bool kBuf>
 void launch_chunks(bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st, const DevSeg *table,
-                   uint64_t n_chunks, const SegHint &hint, const uint64_t *stab, const uint64_t *dtab) {
+                   uint64_t n_chunks, const SegHint &hint, const uint64_t *stab, const uint64_t *dtab,
+                   const uint32_t *cseg) {
   const dim3 block(L);
   const uint32_t remap = g_tuning.xcd_remap.load();
   const bool by_xcd = remap == 2 || (remap == 1 && n_chunks >= kXcdRemapMinChunks);
   const uint64_t xcd_share = by_xcd ? n_chunks * (kChunkUnits / (L * U)) / 8 : 0;
   if (nt && rb.table)
     hipLaunchKernelGGL((copy_plan_kernel<true, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab, xcd_share);
+                       rb.src, rb.dst, stab, dtab, xcd_share, cseg);
   else if (nt)
     hipLaunchKernelGGL((copy_plan_kernel<true, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab, xcd_share);
+                       rb.src, rb.dst, stab, dtab, xcd_share, cseg);
   else if (rb.table)
     hipLaunchKernelGGL((copy_plan_kernel<false, true, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab, xcd_share);
+                       rb.src, rb.dst, stab, dtab, xcd_share, cseg);
   else
     hipLaunchKernelGGL((copy_plan_kernel<false, false, L, U, kBuf>), grid, block, 0, st, table, n_chunks, hint,
-                       rb.src, rb.dst, stab, dtab, xcd_share);
+                       rb.src, rb.dst, stab, dtab, xcd_share, cseg);
 }
 
 // The one-workgroup-per-piece launch for `lanes` lanes of `units` units each.
 template <bool kBuf>
 void launch_pieces(uint32_t lanes, uint32_t units, bool nt, const ResolvedBases &rb, dim3 grid, hipStream_t st,
                    const DevSeg *table, uint64_t n_chunks, const SegHint &hint, const uint64_t *stab,
-                   const uint64_t *dtab) {
+                   const uint64_t *dtab, const uint32_t *cseg) {
   switch (lanes * 8 + units) {
-    case 64 * 8 + 1: launch_chunks<64, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
-    case 64 * 8 + 2: launch_chunks<64, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
-    case 128 * 8 + 1: launch_chunks<128, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
-    case 128 * 8 + 2: launch_chunks<128, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
-    case 256 * 8 + 1: launch_chunks<256, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
-    default: launch_chunks<64, 4, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab); break;
+    case 64 * 8 + 1: launch_chunks<64, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
+    case 64 * 8 + 2: launch_chunks<64, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
+    case 128 * 8 + 1: launch_chunks<128, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
+    case 128 * 8 + 2: launch_chunks<128, 2, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
+    case 256 * 8 + 1: launch_chunks<256, 1, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
+    default: launch_chunks<64, 4, kBuf>(nt, rb, grid, st, table, n_chunks, hint, stab, dtab, cseg); break;
   }
 }
 }  // namespace
@@ -1720,10 +1760,18 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
         stab = dtab = nullptr;
       }
     }
+    uint32_t *cseg = nullptr;
+    if (g_tuning.chunk_index.load()) {
+      rc = chunk_table(plan, dev, st, &cseg);
+      if (rc) {
+        if (tab_owned) (void)hipFreeAsync(tab, st);
+        return rc;
+      }
+    }
     if (g_tuning.buffer_ops.load())
-      launch_pieces<true>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
+      launch_pieces<true>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab, cseg);
     else
-      launch_pieces<false>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab);
+      launch_pieces<false>(lanes, units, nt, *lb, grid, st, table, plan->n_chunks, plan->hint, stab, dtab, cseg);
     hipError_t le = hipGetLastError();
     if (tab_owned) (void)hipFreeAsync(tab, st);
     if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
@@ -1877,18 +1925,21 @@ int emrs_plan_destroy(emrs_plan *plan) {
   if (!plan) return EMRS_OK;
   int prev = 0;
   (void)hipGetDevice(&prev);
-  const size_t n_dev = std::max({plan->dev_tables.size(), plan->ptr_tables.size(), plan->abs_tables.size()});
+  const size_t n_dev = std::max({plan->dev_tables.size(), plan->ptr_tables.size(), plan->abs_tables.size(),
+                                  plan->chunk_tables.size()});
   for (size_t d = 0; d < n_dev; ++d) {
     DevSeg *segs = d < plan->dev_tables.size() ? plan->dev_tables[d] : nullptr;
     uint64_t *ptrs = d < plan->ptr_tables.size() ? plan->ptr_tables[d] : nullptr;
     DevSeg *abs = d < plan->abs_tables.size() ? plan->abs_tables[d] : nullptr;
-    if (segs || ptrs || abs) {
+    uint32_t *chunks = d < plan->chunk_tables.size() ? plan->chunk_tables[d] : nullptr;
+    if (segs || ptrs || abs || chunks) {
       (void)hipSetDevice((int)d);
       // Launches enqueued on any stream may still read the tables.
       (void)hipDeviceSynchronize();
       if (segs) (void)hipFree(segs);
       if (ptrs) (void)hipFree(ptrs);
       if (abs) (void)hipFree(abs);
+      if (chunks) (void)hipFree(chunks);
     }
   }
   (void)hipSetDevice(prev);
@@ -1906,6 +1957,7 @@ int emrs_get_tuning(emrs_tuning *out) {
   out->lanes = g_tuning.lanes.load();
   out->units = g_tuning.units.load();
   out->buffer_ops = g_tuning.buffer_ops.load();
+  out->chunk_index = g_tuning.chunk_index.load();
   return EMRS_OK;
 }
 
@@ -1929,6 +1981,7 @@ int emrs_set_tuning(const emrs_tuning *t) {
   g_tuning.lanes.store(lanes);
   g_tuning.units.store(units);
   g_tuning.buffer_ops.store(t->buffer_ops ? 1 : 0);
+  g_tuning.chunk_index.store(t->chunk_index ? 1 : 0);
   return EMRS_OK;
 }
 

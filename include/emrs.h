@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 5
+#define EMRS_ABI_VERSION 6
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -259,12 +259,16 @@ typedef struct emrs_tuning {
   uint32_t persistent;    /* 0 (default): one workgroup per chunk; 1: persistent grid */
   uint32_t lanes;         /* one workgroup per piece of a chunk: lanes per workgroup, 64, 128 or 256
                              (0: the default, 64) */
-  uint32_t units;         /* 16-byte units per lane, 1, 2 or 4, with lanes * units dividing 256: a
-                             chunk of 256 units is split into 256 / (lanes * units) pieces, one
-                             workgroup each (0: 256 / lanes, one workgroup per chunk) */
+  uint32_t units;         /* 16-byte units per lane, 1 (default), 2 or 4, with lanes * units
+                             dividing 256: a chunk of 256 units is split into 256 / (lanes * units)
+                             pieces, one workgroup each (0: 256 / lanes, one workgroup per chunk) */
   uint32_t buffer_ops;    /* one workgroup per piece, 1: 16-byte units are moved with buffer
                              instructions (32-bit offsets from a per-piece base); 0: with 64-bit
                              global addresses */
+  uint32_t chunk_index;   /* one workgroup per piece, 1 (default): each workgroup reads its
+                             segment from the plan's chunk table (4 bytes per 4 KB chunk, device
+                             memory made on the plan's first such call on a device, freed with the
+                             plan); 0: a binary search bounded by a hint in the kernel arguments */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);

@@ -130,7 +130,7 @@ def _expected(t, srcs_h, n, size):
     return out
 
 
-@pytest.mark.parametrize("lanes,buffer_ops", [(64, False), (256, False), (64, True)])
+@pytest.mark.parametrize("lanes,buffer_ops", [(64, False), (256, False), (64, True), (128, False)])
 def test_table_bases_every_segment_kind(gpu_device, lanes, buffer_ops):
     """A plan over 200 source and 400 destination buffers, with every kind of segment, run on the
     bases of its first call (the segment table resolved against them, no base lookup in the

@@ -129,7 +129,11 @@ def test_manager_repad_round_trip(gpu_device):
     assert st.verify_synthetic(SEED)[0] == 0
 
 
-@pytest.mark.parametrize("tuning", [dict(nontemporal=False), dict(lanes=128), dict(lanes=256),
+@pytest.mark.parametrize("tuning", [dict(chunk_index=False), dict(units=4, chunk_index=False), dict(units=0),
+                                    dict(units=2, chunk_index=False), dict(lanes=256, units=1, chunk_index=False),
+                                    dict(buffer_ops=True, chunk_index=False), dict(xcd_remap=2, chunk_index=False),
+                                    dict(units=4), dict(units=4, xcd_remap=2),
+                                    dict(nontemporal=False), dict(lanes=128), dict(lanes=256),
                                     dict(lanes=256, nontemporal=False), dict(units=1), dict(units=2),
                                     dict(lanes=128, units=1), dict(units=1, nontemporal=False),
                                     dict(buffer_ops=True), dict(buffer_ops=True, nontemporal=False),
@@ -219,7 +223,8 @@ def _random_table(rng, n_segs, sizes):
                                          (5, dict(persistent=True)), (6, dict(lanes=256, nontemporal=False)),
                                          (7, dict(units=1)), (8, dict(units=2)), (9, dict(lanes=128, units=1)),
                                          (10, dict(buffer_ops=True)), (11, dict(buffer_ops=True, nontemporal=False)),
-                                         (12, dict(buffer_ops=True, units=1)),
+                                         (12, dict(buffer_ops=True, units=1)), (13, dict(chunk_index=False)),
+                                         (14, dict(units=4, chunk_index=False)), (15, dict(units=0)),
                                          (13, dict(buffer_ops=True, lanes=256))])
 def test_random_segments_match_numpy(gpu_device, seed, tuning):
     """Arbitrary element sizes, offsets and strides (scalar, split and vector paths), zero fills,
@@ -300,7 +305,7 @@ def test_bf16_cast_rounding_special_values(gpu_device):
     assert (want[~np.concatenate([finite[:n // 2], [True], finite[n // 2:n - 1]])] == 0x7FC0).all()
 
 
-@pytest.mark.parametrize("tuning", [{}, dict(persistent=True)])
+@pytest.mark.parametrize("tuning", [{}, dict(chunk_index=False), dict(units=4), dict(persistent=True)])
 def test_large_multichunk_plan(gpu_device, tuning):
     """More chunks than one grid row holds, 2-D segments with > 2^16 rows, segments split at 2^30
     units, and (persistent grid) many chunks per workgroup."""
