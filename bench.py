@@ -9,7 +9,7 @@ A step is one execution of the switch's copy plan (one kernel launch) with
 every source shard already resident in HBM.  Inputs are synthetic: seeded
 values ~N(0, 0.02) for bf16 params, main = their exact upcast, exp_avg
 ~N(0, 1e-3), exp_avg_sq = |N(0, 1e-6)|.  The destination is checked
-bit-exact against the generator after warm-up.
+bit-exact against the generator after the timed steps.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
@@ -259,9 +259,6 @@ def main():
     for _ in range(args.warmup):
         step(a, b)
     torch.cuda.synchronize()
-    verified = check_destination() if args.warmup else None  # without a warm-up, after the timed steps
-    if verified is False:
-        return 3
 
     events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
@@ -272,10 +269,12 @@ def main():
         events[i + 1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1e3
-    if not args.warmup:
-        verified = check_destination()
-        if verified is False:
-            return 3
+    # Every step rewrites the whole destination with the same values, so the check after the last
+    # timed step covers them all; run between the warm-up and the timed steps, its own pass over
+    # the destination would leave the first timed launch cold.
+    verified = check_destination()
+    if verified is False:
+        return 3
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = sum(step_ms) / len(step_ms)
     payload = plan.payload_bytes
@@ -491,9 +490,6 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
     for _ in range(args.warmup):
         tm.execute_tensors(plan, src_views, dst_views, stream)
     torch.cuda.synchronize()
-    verified = check_destination() if args.warmup else None  # without a warm-up, after the timed steps
-    if verified is False:
-        return 3
     events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     events[0].record(stream)
@@ -501,10 +497,9 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
         tm.execute_tensors(plan, src_views, dst_views, stream)
         events[i + 1].record(stream)
     torch.cuda.synchronize()
-    if not args.warmup:
-        verified = check_destination()
-        if verified is False:
-            return 3
+    verified = check_destination()  # after the timed steps, as in the arena benchmark
+    if verified is False:
+        return 3
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = sum(step_ms) / len(step_ms)
     traffic_gbps = arena_plan.traffic_bytes / (ms / 1e3) / 1e9
@@ -531,7 +526,9 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
     together), with the same 16-byte non-temporal accesses:
 
     - a plain contiguous copy of the source main arena into the destination one, by copy_plan_kernel;
-    - write-only: the same kernel zero-filling the destination main arena (no reads);
+    - write-only: the same kernel zero-filling the destination main arena (no reads), with one
+      workgroup per 4 KB chunk whatever the launch shape: a workgroup that only stores 1 KB is so
+      short that the rate of launching workgroups, not the memory, would bound the figure;
     - read-only: emrs_xor_checksum over the source main arena (no writes);
     - the workload's own read and write bytes moved one direction after the other at those two
       rates, a figure a kernel that overlaps reads with writes can beat.
@@ -561,7 +558,15 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
     ms = timed(lambda: copy.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
     t[0]["flags"] = SEG_ZERO_FILL
     fill = _native.Plan(t, [n * 4], [n * 4])
-    w_ms = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
+    tu = _native.get_tuning()
+    shape = dict(blocks_per_cu=tu.blocks_per_cu, nontemporal=bool(tu.nontemporal), xcd_remap=tu.xcd_remap,
+                 run=tu.run, persistent=bool(tu.persistent), lanes=tu.lanes, buffer_ops=bool(tu.buffer_ops),
+                 chunk_index=bool(tu.chunk_index))
+    _native.set_tuning(**shape, units=0)  # one workgroup per chunk
+    try:
+        w_ms = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
+    finally:
+        _native.set_tuning(**shape, units=tu.units)
     word = torch.zeros(1, dtype=torch.int32, device=a.main.device)
     r_ms = timed(lambda: _native.xor_checksum(a.main.data_ptr(), n * 4, word.data_ptr(), stream.cuda_stream))
     gbps = 2 * n * 4 / (ms / 1e3) / 1e9
@@ -613,13 +618,19 @@ def reshard_end_to_end(a, spec, src, dst, repad, tm, no_verify, reps=3):
 
 
 def copy_calibration(args, dev, stream):
-    """One contiguous segment of known size: the reference point for HBM counters."""
+    """One contiguous segment of known size: the reference point for HBM counters.
+
+    The launch shape is the one the flags select, except that the workgroups find their segment by
+    search rather than in the plan's chunk table, so that the kernel reads exactly the copied bytes.
+    """
     import numpy as np
     import torch
 
     from elasticmegatron_amd import _native
     from elasticmegatron_amd.resharding.layout import SEGMENT_DTYPE
 
+    _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), args.xcd_remap, args.run,
+                       bool(args.persistent), args.lanes, args.units, chunk_index=False)
     n = int(args.copy_calibration_gib * (1 << 30)) // 16 * 4
     a = torch.ones(n, dtype=torch.float32, device=dev)
     b = torch.empty(n, dtype=torch.float32, device=dev)

@@ -77,7 +77,9 @@ def test_committed_traffic_describes_the_current_plan(traffic_file):
         rec = json.load(f)
     assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes) == \
         rec["hbm_bytes_per_launch"]
-    assert abs(rec["hbm_bytes_per_launch"] / plan.traffic_bytes - 1) < 1e-3   # within 0.1% of the algorithmic bytes
+    # Within 0.2% of the algorithmic bytes: the measured traffic also holds the plan's chunk table
+    # (4 bytes per 4 KB chunk, about 0.05%) and the segment descriptors.
+    assert abs(rec["hbm_bytes_per_launch"] / plan.traffic_bytes - 1) < 2e-3
     assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes + 1) is None
 
 
