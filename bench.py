@@ -305,7 +305,8 @@ def main():
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4),
                    "median_ms": round(sorted(step_ms)[len(step_ms) // 2], 4),
                    "first_third_ms": round(sum(step_ms[:max(1, len(step_ms) // 3)]) / max(1, len(step_ms) // 3), 4),
-                   "last_third_ms": round(sum(step_ms[-max(1, len(step_ms) // 3):]) / max(1, len(step_ms) // 3), 4)},
+                   "last_third_ms": round(sum(step_ms[-max(1, len(step_ms) // 3):]) / max(1, len(step_ms) // 3), 4),
+                   "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
     }
@@ -513,12 +514,25 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
                    "buffers": f"{len(ms_.specs)} source, {len(md.specs)} destination flat buffers; "
                               f"{len(plan.src)} / {len(plan.dst)} tensor views",
                    "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
-                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4)},
+                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def launch_shape():
+    """The launch shape in effect (emrs_get_tuning), as the JSON line reports it."""
+    from elasticmegatron_amd import _native
+
+    t = _native.get_tuning()
+    if t.persistent:
+        return {"grid": "persistent", "blocks_per_cu": t.blocks_per_cu, "run": t.run, "xcd_remap": t.xcd_remap,
+                "nontemporal": t.nontemporal}
+    return {"grid": "one workgroup per piece", "lanes": t.lanes, "units_per_lane": t.units,
+            "piece_bytes": 16 * t.lanes * t.units, "chunk_index": t.chunk_index, "xcd_remap": t.xcd_remap,
+            "buffer_ops": t.buffer_ops, "nontemporal": t.nontemporal}
 
 
 def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
