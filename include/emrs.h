@@ -266,9 +266,10 @@ typedef struct emrs_tuning {
                              instructions (32-bit offsets from a per-piece base); 0: with 64-bit
                              global addresses */
   uint32_t chunk_index;   /* one workgroup per piece, 1 (default): each workgroup reads its
-                             segment from the plan's chunk table (4 bytes per 4 KB chunk, device
-                             memory made on the plan's first such call on a device, freed with the
-                             plan); 0: a binary search bounded by a hint in the kernel arguments */
+                             segment from the plan's chunk table (4 * emrs_plan_stats.n_chunks
+                             bytes of device memory, made on the plan's first such call on a
+                             device and freed with the plan); 0: a binary search bounded by a
+                             hint in the kernel arguments */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);
