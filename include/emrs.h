@@ -27,8 +27,9 @@
  *   - All offsets, lengths and strides are in elements of the segment's
  *     elem_bytes (1, 2, 4 or 8).  Mixed element sizes may share one plan.
  *   - Buffers are caller-owned device allocations; the library never
- *     allocates or frees caller memory.  A plan owns only its own segment
- *     table in device memory.
+ *     allocates or frees caller memory.  A plan owns only its own tables in
+ *     device memory: the segment table, the chunk table (emrs_tuning.chunk_index)
+ *     and, beyond 128 buffers a side, its pointer tables.
  *   - Every function returns EMRS_OK (0) or a negative EMRS_ERR_* code and
  *     never throws across the ABI; emrs_last_error() returns a description
  *     of the last failure on the calling thread.
@@ -152,8 +153,8 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
  * buffer of the other side or another referenced destination buffer
  * (EMRS_ERR_ALIAS): the copy is out of place.  Unreferenced buffers are not
  * checked and may be NULL.  The first call on a device uploads the plan's
- * table (and, beyond 128 buffers a side, its pointer table for these bases)
- * synchronously; later calls with the same bases enqueue one kernel launch
+ * tables (segment table, chunk table and, beyond 128 buffers a side, its
+ * pointer table for these bases) synchronously; later calls with the same bases enqueue one kernel launch
  * and nothing else, so they may be captured into a HIP graph.  Calls with
  * other bases than the first beyond 128 buffers allocate a stream-ordered
  * pointer table.  Neither the first call nor such a call may be captured:
