@@ -64,6 +64,35 @@ def workloads():
     }
 
 
+SHAPE_KEYS = ("lanes", "units", "chunk_index", "xcd_remap", "buffer_ops", "nontemporal", "persistent",
+              "blocks_per_cu", "run")
+
+
+def parse_shapes(text):
+    """``--shape-sweep`` value: launch shapes separated by ``;``, each ``default`` or comma-separated
+    ``key=int`` settings of emrs_tuning (unset keys keep their defaults)."""
+    shapes = []
+    for part in text.split(";"):
+        part = part.strip()
+        shape = {}
+        if part and part != "default":
+            for kv in part.split(","):
+                key, sep, val = kv.partition("=")
+                key = key.strip().replace("-", "_")
+                if not sep or key not in SHAPE_KEYS:
+                    raise argparse.ArgumentTypeError(f"bad launch-shape setting {kv!r}; keys: {', '.join(SHAPE_KEYS)}")
+                try:
+                    shape[key] = int(val)
+                except ValueError:
+                    raise argparse.ArgumentTypeError(f"launch-shape setting {kv!r} is not an integer") from None
+        lanes, units = shape.get("lanes", 0) or 64, shape.get("units", 1)
+        if lanes not in (64, 128, 256) or units not in (0, 1, 2, 4) or (units and 256 % (lanes * units)):
+            raise argparse.ArgumentTypeError(f"launch shape {part!r}: lanes 64/128/256, units 0/1/2/4, "
+                                             "lanes * units dividing 256")
+        shapes.append(shape)
+    return shapes
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,6 +107,10 @@ def parse():
                     help="run the per-tensor plan (one buffer per stored tensor, as views into the arenas)")
     ap.add_argument("--placement-trials", type=int, default=0,
                     help="re-allocate the destination state this many times and time 5 launches each")
+    ap.add_argument("--shape-sweep", type=parse_shapes, default=None,
+                    help="time several launch shapes on the same allocations, in --rounds rounds, e.g. "
+                         "'default;units=4,chunk_index=0;units=2'; prints one JSON line per workload")
+    ap.add_argument("--rounds", type=int, default=3, help="rounds of --shape-sweep")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
@@ -230,6 +263,9 @@ def main():
     b = TrainingState.allocate(ld, dev, param=a.param if backup is not None else None)
     a.fill_synthetic(SEED, bf16=True)
     torch.cuda.synchronize()
+    if args.shape_sweep is not None:
+        return shape_sweep(args, desc, tm, plan, a, b, backup, ls.space.spec.padded_vocab_size if repad else None,
+                           stream)
     views = {}
 
     def step(a, b):
@@ -519,6 +555,57 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
+    return 0
+
+
+def shape_sweep(args, desc, tm, plan, a, b, backup, vocab_rows, stream):
+    """Each launch shape of --shape-sweep, timed on the same allocations in one process: round after
+    round, every shape runs --warmup untimed and --steps timed launches.  Each shape's output is
+    checked bit-exact once.  Physical placement moves all shapes together, so the shapes compare to
+    within the spread between rounds."""
+    import torch
+
+    from elasticmegatron_amd import _native
+
+    rows = [{"shape": shp or "default", "ms": []} for shp in args.shape_sweep]
+    try:
+        for r in range(args.rounds):
+            for shp, row in zip(args.shape_sweep, rows):
+                try:
+                    _native.set_tuning(**shp)
+                except _native.EmrsError as e:
+                    print(f"[bench] launch shape {shp}: {e}", file=sys.stderr)
+                    return 2
+                if r == 0:
+                    row["launch"] = launch_shape()
+                    for x in (b.main, b.exp_avg, b.exp_avg_sq):
+                        x.fill_(float("nan"))
+                    if backup is None:
+                        b.param.zero_()
+                    tm.execute(plan, a, b, stream)
+                    torch.cuda.synchronize()
+                    bad, first = b.verify_synthetic(SEED, bf16=backup is None, vocab_rows=vocab_rows)
+                    if bad:
+                        print(f"[bench] launch shape {shp}: verification FAILED: {bad} elements, first {first}",
+                              file=sys.stderr)
+                        return 3
+                for _ in range(args.warmup):
+                    tm.execute(plan, a, b, stream)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(args.steps):
+                    tm.execute(plan, a, b, stream)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                row["ms"].append(round(e0.elapsed_time(e1) / args.steps, 4))
+    finally:
+        _native.set_tuning()
+    for row in rows:
+        row["best_ms"] = min(row["ms"])
+        row["traffic_tbps_at_best"] = round(plan.traffic_bytes / (row["best_ms"] / 1e3) / 1e12, 3)
+    print(json.dumps({"workload": desc, "what": "launch shapes on the same allocations in one process",
+                      "steps": args.steps, "warmup": args.warmup, "rounds": args.rounds,
+                      "traffic_bytes": plan.traffic_bytes, "verified_bit_exact": True, "shapes": rows}), flush=True)
     return 0
 
 

@@ -26,6 +26,14 @@ def test_more_than_one_gpu_is_refused_with_a_reason():
     assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
 
 
+def test_shape_sweep_settings_are_checked_before_any_device_work():
+    assert bench.parse_shapes("default;units=4,chunk_index=0; lanes=256") == [{}, {"units": 4, "chunk_index": 0},
+                                                                              {"lanes": 256}]
+    for bad in ("lanes=96", "units=3", "lanes=128,units=4", "foo=1", "units", "units=x"):
+        r = _run("--shape-sweep", bad)
+        assert r.returncode == 2 and "--shape-sweep" in r.stderr and r.stdout == "", bad
+
+
 def test_launch_shape_flags_are_checked_before_any_device_work():
     r = _run("--lanes", "96")
     assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""

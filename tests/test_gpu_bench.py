@@ -24,8 +24,19 @@ def _bench(*args):
 @pytest.mark.parametrize("extra", [(), ("--megatron-buffers",), ("--tensors",)])
 @pytest.mark.parametrize("warmup", [0, 1])
 def test_bench_line_checks_the_destination(gpu_device, warmup, extra):
-    """Without a warm-up the destination is checked after the timed steps, not before any launch."""
+    """The destination is checked after the timed steps, with a warm-up or without one."""
     d = _bench("--warmup", str(warmup), "--steps", "2", *extra)
     assert d["warmup"] == warmup and d["steps"] == 2 and d["n_gpus"] == 1
     assert d["config"]["verified_bit_exact"] is True
     assert d["ms_per_step"] > 0 and d["value"] > 0
+
+
+@pytest.mark.gpu
+def test_shape_sweep_times_every_shape_on_the_same_allocations(gpu_device):
+    d = _bench("--shape-sweep", "default;units=4,chunk_index=0;units=2", "--steps", "2", "--warmup", "1",
+               "--rounds", "2")
+    assert d["verified_bit_exact"] is True and d["rounds"] == 2
+    assert [r["shape"] for r in d["shapes"]] == ["default", {"units": 4, "chunk_index": 0}, {"units": 2}]
+    assert [(r["launch"]["units_per_lane"], r["launch"]["chunk_index"]) for r in d["shapes"]] == \
+        [(1, 1), (4, 0), (2, 1)]
+    assert all(len(r["ms"]) == 2 and r["best_ms"] > 0 for r in d["shapes"])
