@@ -55,6 +55,8 @@ def workloads():
                                ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4),
                                PS(8, 1, 1, expert_model_parallel_size=8)),
         "llama2-7b-dp8-dp6": ("Llama-2-7B world 8 DP8 -> world 6 DP6", ms.llama2_7b, PS(8, 1, 1), PS(6, 1, 1)),
+        "llama2-7b-cp2tp2dp2-tp4dp2": ("Llama-2-7B CP2TP2DP2 -> TP4DP2, world 8, 40M buckets", ms.llama2_7b,
+                                       PS(8, 2, 1, context_parallel_size=2), PS(8, 4, 1)),
         "llama2-7b-groupzero-1-2": ("Llama-2-7B Group ZeRO instances 1 -> 2 (world 6 -> 12), fp32 only",
                                     ms.llama2_7b, PS(6, 1, 1),
                                     PS(12, 1, 1, num_distributed_optimizer_instances=2)),

@@ -40,6 +40,8 @@ CASES = [
     pytest.param(ms.mixtral_8x7b_slice, PS(8, 1, 1, expert_model_parallel_size=4),
                  PS(8, 1, 1, expert_model_parallel_size=8), id="mixtral-4l-ep4-ep8"),
     pytest.param(ms.llama2_7b, PS(8, 1, 1), PS(6, 1, 1), id="llama2-7b-dp8-dp6"),
+    # Context parallelism: the optimizer shards over DP x CP ranks on the source side.
+    pytest.param(ms.llama2_7b, PS(8, 2, 1, context_parallel_size=2), PS(8, 4, 1), id="llama2-7b-cp2tp2dp2-tp4dp2"),
     pytest.param(ms.llama2_7b, PS(6, 1, 1), PS(12, 1, 1, num_distributed_optimizer_instances=2),
                  id="llama2-7b-groupzero-1-2"),
 ]
