@@ -1103,15 +1103,22 @@ int chunk_table(emrs_plan *plan, int dev, hipStream_t st, uint32_t **out) {
   if (!plan->chunk_tables[dev]) {
     if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
     if (plan->segs.size() > 0xffffffffull) return fail(EMRS_ERR_INVALID_ARGUMENT, "too many device segments");
+    const size_t bytes = plan->n_chunks * sizeof(uint32_t);
+    uint32_t *t = nullptr;
+    hipError_t e = hipMalloc(&t, bytes);
+    if (e == hipErrorOutOfMemory) {
+      // The table only spares each workgroup its search: with no room for it,
+      // this launch searches instead, and the next call tries again.
+      (void)hipGetLastError();
+      *out = nullptr;
+      return EMRS_OK;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(chunk table)");
     std::vector<uint32_t> seg_of(plan->n_chunks);
     for (size_t k = 0; k < plan->segs.size(); ++k) {
       const uint64_t c1 = k + 1 < plan->segs.size() ? plan->segs[k + 1].chunk_begin : plan->n_chunks;
       std::fill(seg_of.begin() + plan->segs[k].chunk_begin, seg_of.begin() + c1, (uint32_t)k);
     }
-    const size_t bytes = seg_of.size() * sizeof(uint32_t);
-    uint32_t *t = nullptr;
-    hipError_t e = hipMalloc(&t, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(chunk table)");
     e = hipMemcpy(t, seg_of.data(), bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       (void)hipFree(t);

@@ -269,8 +269,9 @@ typedef struct emrs_tuning {
   uint32_t chunk_index;   /* one workgroup per piece, 1 (default): each workgroup reads its
                              segment from the plan's chunk table (4 * emrs_plan_stats.n_chunks
                              bytes of device memory, made on the plan's first such call on a
-                             device and freed with the plan); 0: a binary search bounded by a
-                             hint in the kernel arguments */
+                             device and freed with the plan; when that allocation runs out of
+                             memory, the launch searches instead); 0: a binary search bounded by
+                             a hint in the kernel arguments */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);
