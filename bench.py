@@ -344,7 +344,13 @@ def main():
                    "median_ms": round(sorted(step_ms)[len(step_ms) // 2], 4),
                    "first_third_ms": round(sum(step_ms[:max(1, len(step_ms) // 3)]) / max(1, len(step_ms) // 3), 4),
                    "last_third_ms": round(sum(step_ms[-max(1, len(step_ms) // 3):]) / max(1, len(step_ms) // 3), 4),
-                   "launch": launch_shape()},
+                   "launch": launch_shape(),
+                   "reference_perf_line": {
+                       "what": "the figures of the reference's perf log line (elastic_manager.py:158-178): GiB "
+                               "of fp32 state the busiest rank would exchange with other ranks, per second of "
+                               "this launch; a different quantity from value and roofline",
+                       "communication_gib": round(plan.reference_comm_bytes / 2 ** 30, 3),
+                       "gib_per_s": round(plan.reference_comm_bytes / 2 ** 30 / (ms / 1e3), 1)}},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
     }
