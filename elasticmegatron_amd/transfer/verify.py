@@ -20,16 +20,18 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, List, NamedTuple, Optional, Tuple
 
 import numpy as np
 
 KIND_NAMES = ("param", "main", "exp_avg", "exp_avg_sq")
 
 
-@dataclass(frozen=True)
-class TensorDiff:
-    """One (parameter, kind)'s comparison, with compare_ckpt.py's figures (compare_ckpt.py:52-66)."""
+class TensorDiff(NamedTuple):
+    """One (parameter, kind)'s comparison, with compare_ckpt.py's figures (compare_ckpt.py:52-66).
+
+    An immutable tuple: a report holds one per (parameter, kind), hundreds per switch, and a tuple
+    is built about three times faster than a frozen dataclass."""
 
     elements: int
     mismatches: int
@@ -100,11 +102,12 @@ def merge_stats(a: Optional[np.ndarray], b: np.ndarray) -> np.ndarray:
 
 def report_from_stats(stats: np.ndarray, names: List[str]) -> VerifyReport:
     """Build the report from emrs_plan_compare records indexed by ``4 * parameter index + kind``."""
+    # Whole columns to Python numbers at once: reading the fields record by record costs
+    # milliseconds per report on a few hundred parameters.
+    cols = [stats[f].tolist() for f in ("elements", "mismatches", "nonfinite", "sum_sq_diff", "sum_sq_expected",
+                                        "max_abs_diff", "max_rel_diff")]
     tensors = {}
-    for g, rec in enumerate(stats):
-        if not rec["elements"]:
-            continue
-        tensors[(names[g // 4], KIND_NAMES[g % 4])] = TensorDiff(
-            int(rec["elements"]), int(rec["mismatches"]), int(rec["nonfinite"]), float(rec["sum_sq_diff"]),
-            float(rec["sum_sq_expected"]), float(rec["max_abs_diff"]), float(rec["max_rel_diff"]))
+    for g, rec in enumerate(zip(*cols)):
+        if rec[0]:
+            tensors[(names[g // 4], KIND_NAMES[g % 4])] = TensorDiff(*rec)
     return VerifyReport(tensors)
