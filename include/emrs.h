@@ -242,8 +242,9 @@ int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *cons
 /*
  * Launch-shape knobs of emrs_plan_execute, process-wide.  Results never
  * depend on them; only speed does.  By default every chunk of 256 units is
- * a workgroup of its own; persistent = 1 selects a persistent grid, which
- * the other three fields shape.
+ * split into four pieces of 64 units (1 KB), one 64-lane workgroup each,
+ * which finds its segment in the plan's chunk table; persistent = 1 selects
+ * a persistent grid, which blocks_per_cu, run and xcd_remap shape.
  */
 typedef struct emrs_tuning {
   uint32_t blocks_per_cu; /* workgroups per CU in the persistent grid (0..64);
@@ -257,7 +258,7 @@ typedef struct emrs_tuning {
   uint32_t run;           /* persistent grid, 0: each workgroup copies one contiguous run of
                              chunks; N in [1, 2^20]: chunks are dealt out round-robin in runs of
                              8N, capped at a quarter of a workgroup's share (default 4) */
-  uint32_t persistent;    /* 0 (default): one workgroup per chunk; 1: persistent grid */
+  uint32_t persistent;    /* 0 (default): one workgroup per piece of a chunk; 1: persistent grid */
   uint32_t lanes;         /* one workgroup per piece of a chunk: lanes per workgroup, 64, 128 or 256
                              (0: the default, 64) */
   uint32_t units;         /* 16-byte units per lane, 1 (default), 2 or 4, with lanes * units
