@@ -605,17 +605,18 @@ __device__ __forceinline__ void dispatch_chunk(uint32_t ul, const DevSeg &s, con
 }
 
 // One workgroup of L lanes per piece of L * U units of a chunk (the default
-// schedule: L = 64, U = 4, one workgroup per chunk).  A chunk of 256 units
+// schedule: L = 64, U = 1, four 1 KB pieces per chunk).  A chunk of 256 units
 // holds 256 / (L * U) pieces; workgroup w takes piece w % that of chunk
 // w / that, and a piece past the end of its segment's last chunk does
 // nothing.  The grid is two-dimensional (w = blockIdx.y * gridDim.x +
 // blockIdx.x) because one dimension holds fewer than 2^32 lanes; workgroups
-// past the last piece exit at once.  The segment search depends on the chunk
-// alone, so it runs on the scalar unit, once per wave, and the upper levels
-// of the search stay in the scalar cache for every workgroup in flight.  With
-// L = 64 and U = 4 a chunk is one wave: one search per 4 KB, four loads in
-// flight per lane.  With 256 lanes four waves repeat the same search for one
-// 16-byte load each, and the launch runs about 20% slower.
+// past the last piece exit at once.  The segment depends on the chunk alone,
+// so finding it runs on the scalar unit, once per wave: one load from the
+// plan's chunk table (chunk_seg, by default), or a binary search whose upper
+// levels stay in the scalar cache for every workgroup in flight.  With the
+// search, small pieces repeat it for little data (256 lanes of one unit ran
+// about 20% slower than 64 lanes of four); with the table, 1 KB pieces are
+// the fastest shape.
 //
 // xcd_share != 0: the first 8 * xcd_share workgroups are renumbered so that
 // each XCD (the hardware deals workgroups out to the 8 XCDs round-robin, so
