@@ -445,9 +445,9 @@ __device__ __forceinline__ void copy_units(const DevSeg &s, const char *sbase, c
       if (u < total) v[j] = ld<T, kNT>(src + so);
     }
   }
-  // Destination offsets are recomputed rather than kept from the loads: that
-  // holds the kernel at 66 VGPRs instead of 74, so seven waves fit on each
-  // SIMD instead of six.
+  // Destination offsets are recomputed rather than kept from the loads: with
+  // four units per lane that holds the kernel at 66 VGPRs instead of 74, so
+  // seven waves fit on each SIMD instead of six.
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     const uint32_t u = u0 + j * L + threadIdx.x;
