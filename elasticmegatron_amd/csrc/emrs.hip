@@ -193,7 +193,7 @@ struct Tuning {
   std::atomic<uint32_t> nontemporal{1};
   std::atomic<uint32_t> xcd_remap{1};      // 0, 1 (by plan size) or 2
   std::atomic<uint32_t> run{4};            // persistent grid: round-robin runs of 4 x kUnroll chunks
-  std::atomic<uint32_t> persistent{0};     // 0: one workgroup per chunk
+  std::atomic<uint32_t> persistent{0};     // 0: one workgroup per piece of a chunk
   std::atomic<uint32_t> lanes{64};         // lanes per workgroup of one piece: 64, 128 or 256
   std::atomic<uint32_t> units{1};          // 16-byte units per lane: lanes * units is 64, 128 or 256
   std::atomic<uint32_t> buffer_ops{0};     // 1: 16-byte units through buffer instructions
