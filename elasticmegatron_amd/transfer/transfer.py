@@ -298,18 +298,25 @@ class TransferManager:
                                  st.cuda_stream)
         return stats, names
 
-    def transfer_optimizer_tensors(self, virtual_param_space, src: Optional[TrainingState] = None,
-                                   dst: Optional[TrainingState] = None, include_bf16: bool = True,
-                                   stream=None) -> CompiledPlan:
+    def transfer_optimizer_tensors(self, virtual_param_space, use_block_and_print: bool = False, *,
+                                   src: Optional[TrainingState] = None, dst: Optional[TrainingState] = None,
+                                   include_bf16: bool = True, stream=None) -> CompiledPlan:
         """Move fp32 optimizer state from ``src`` to ``dst`` and rebuild the bf16 params (transfer.py:291-341).
 
         By default the destination bf16 params are the bf16 rounding of the
         destination main weights, written in the same pass (the reference's
         cast plus DP all-gather, training_state.py:176-197); with
         ``bf16_source="copy"`` they are copied from the source bf16 shards.
+
+        ``use_block_and_print`` keeps the reference's debugging switch
+        (transfer.py:271-289): every parameter's global send and receive
+        ranges are printed before the switch runs.  There is nothing to block
+        on: the whole switch is one launch.
         """
         src = src if src is not None else virtual_param_space.src_state
         dst = dst if dst is not None else virtual_param_space.dst_state
+        if use_block_and_print and virtual_param_space is not None:
+            print(plan_dump(virtual_param_space), flush=True)
         plan = self.compile(src.layout, dst.layout, "transfer", include_bf16)
         self.execute(plan, src, dst, stream)
         return plan
@@ -336,3 +343,22 @@ class TransferManager:
         b = self._payload_bytes
         self._payload_bytes = 0
         return b
+
+
+def plan_dump(virtual_param_space) -> str:
+    """Every parameter's registered switch as global (rank, range) pairs: who sends what to whom
+    and who receives what from whom, in the order the reference walks the parameters."""
+    lines = []
+    for vp in virtual_param_space.all_virtual_params:
+        rp = vp.reshard_plan
+        lines.append(f"[reshard plan] {vp.param_position_attr}")
+        if rp is None:
+            lines.append("  (no switch registered)")
+            continue
+        for s_rank, per_dst in sorted(rp.global_send_info.items()):
+            for d_rank, rng in sorted(per_dst.items()):
+                lines.append(f"  send  {s_rank:>4} -> {d_rank:<4} {rng}")
+        for d_rank, per_src in sorted(rp.global_recv_info.items()):
+            for s_rank, rng in sorted(per_src.items()):
+                lines.append(f"  recv  {d_rank:>4} <- {s_rank:<4} {rng}")
+    return "\n".join(lines)

@@ -232,3 +232,26 @@ def test_dict_strategies_share_the_cached_plan():
     state = TrainingState.allocate(mgr.virtual_param_space.layout(ParallelStrategy(8, 2, 1)), "cpu")
     ElasticMegatronManager([dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1,
                                  sequence_parallel=False)], tiny_llama2(), training_state=state)
+
+
+def test_block_and_print_keeps_the_reference_signature():
+    """transfer_optimizer_tensors(space, use_block_and_print) as the reference declares it
+    (transfer.py:291-293); the dump lists every registered parameter's global send and receive
+    ranges, one line per (source rank, destination rank) pair of its plan."""
+    import inspect
+
+    from elasticmegatron_amd.resharding.model_spec import tiny_llama2
+    from elasticmegatron_amd.transfer.transfer import TransferManager, plan_dump
+
+    params = list(inspect.signature(TransferManager.transfer_optimizer_tensors).parameters)
+    assert params[:3] == ["self", "virtual_param_space", "use_block_and_print"]
+    space = build_virtual_model(tiny_llama2())
+    src, dst = ParallelStrategy(8, 2, 1), ParallelStrategy(8, 4, 1)
+    space.register_reshard(src, dst)
+    text = plan_dump(space).splitlines()
+    heads = [l for l in text if l.startswith("[reshard plan]")]
+    assert len(heads) == len(space.all_virtual_params)
+    sends = sum(len(d) for vp in space.all_virtual_params for d in vp.reshard_plan.global_send_info.values())
+    recvs = sum(len(d) for vp in space.all_virtual_params for d in vp.reshard_plan.global_recv_info.values())
+    assert sum(l.startswith("  send") for l in text) == sends > 0
+    assert sum(l.startswith("  recv") for l in text) == recvs > 0

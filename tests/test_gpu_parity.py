@@ -71,7 +71,7 @@ def test_kernel_matches_oracle1(gpu_device, factory, src, dst, bf16_source):
     a.fill_synthetic(SEED)
     fill_canaries(b)  # every stored element must be overwritten, every padding element kept
     tm = TransferManager(check_disjoint=True, bf16_source=bf16_source)
-    tm.transfer_optimizer_tensors(space, a, b)
+    tm.transfer_optimizer_tensors(space, src=a, dst=b)
     got32, gotbf = extract(ld, _host_arenas(b))
     assert padding_damage(b) == 0
 
@@ -101,7 +101,7 @@ def test_repad_kernel_matches_invariant(gpu_device, factory, vocab, src, dst, bf
     a.fill_synthetic(SEED)
     for t in b.arenas():
         t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
-    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, a, b)
+    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, src=a, dst=b)
     got32, gotbf = extract(ld, _host_arenas(b))
     want32, wantbf = canonical.world(model.inventory(sb.spec), sb.spec, strat(dst), SEED,
                                      vocab_rows=sa.spec.padded_vocab_size)
@@ -167,7 +167,7 @@ def test_launch_shape_does_not_change_results(gpu_device, tuning):
             b = TrainingState.allocate(ld, gpu_device)
             for x in b.arenas():
                 x.fill_(0) if x.dtype != torch.float32 else x.fill_(float("nan"))
-            TransferManager(check_disjoint=True).transfer_optimizer_tensors(None, a, b)
+            TransferManager(check_disjoint=True).transfer_optimizer_tensors(None, src=a, dst=b)
             outs.append(_host_arenas(b))
     finally:
         _native.set_tuning()
@@ -420,7 +420,7 @@ def test_random_switch_kernel_matches_oracle1(gpu_device, spec, src, dst, bf16_s
     a.fill_synthetic(SEED)
     for t in b.arenas():
         t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
-    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, a, b)
+    TransferManager(check_disjoint=True, bf16_source=bf16_source).transfer_optimizer_tensors(None, src=a, dst=b)
     got32, gotbf = extract(ld, _host_arenas(b))
     inv = model.inventory(spec)
     S, D = strat(src), strat(dst)

@@ -60,13 +60,13 @@ def test_medium_random_switch(gpu_device, spec, src, dst):
     a.fill_synthetic(SEED)
     for t in b.arenas():
         t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
-    tm.transfer_optimizer_tensors(None, a, b)
+    tm.transfer_optimizer_tensors(None, src=a, dst=b)
     bad, first = b.verify_synthetic(SEED)
     assert bad == 0, first
     assert tm.verify(a, b).bit_exact
     back = TrainingState.allocate(ls, gpu_device)
     for t in back.arenas():
         t.fill_(0) if t.dtype != torch.float32 else t.fill_(float("nan"))
-    tm.transfer_optimizer_tensors(None, b, back)
+    tm.transfer_optimizer_tensors(None, src=b, dst=back)
     bad, first = back.verify_synthetic(SEED)  # the round trip reproduces every source element
     assert bad == 0, first

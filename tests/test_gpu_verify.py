@@ -51,7 +51,7 @@ def test_compare_kernel_matches_numpy(gpu_device, factory, src, dst, bf16_source
     b = TrainingState.allocate(ld, gpu_device)
     a.fill_synthetic(SEED)
     tm = TransferManager(bf16_source=bf16_source)
-    tm.transfer_optimizer_tensors(None, a, b)
+    tm.transfer_optimizer_tensors(None, src=a, dst=b)
     rep = tm.verify(a, b)
     assert rep.bit_exact
     held = [vp for vp in space.all_virtual_params if ld.has_param(vp)]
