@@ -119,8 +119,15 @@ class ElasticMegatronManager:
     def parallel_strategy(self) -> ParallelStrategy:
         return self.training_state.parallel_strategy
 
-    def transfer_params(self, src: TrainingState, dst: TrainingState) -> float:
-        """Plan (cached) and move the state; returns the executor's time in ms."""
+    def transfer_params(self, src: TrainingState, dst: TrainingState, union_world_group=None,
+                        is_meta_device: bool = False) -> float:
+        """Plan (cached) and move the state; returns the executor's time in ms.
+
+        The arguments keep the reference's order (elastic_manager.py:106-122).  One process holds
+        every rank's state, so ``union_world_group`` is accepted and unused; ``is_meta_device``
+        plans and caches without moving data, as the reference's fake transfer does
+        (elastic_manager.py:115-117, 282-285).
+        """
         space = src.layout.space
         if space is dst.layout.space:
             space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
@@ -128,11 +135,15 @@ class ElasticMegatronManager:
         # The states are the space's for the duration of the transfer only: the space outlives the
         # switch, and holding them would keep a released state's memory alive.
         space.src_state, space.dst_state = src, dst
+        fake = self.transfer_manager.fake_transfer
         try:
+            if is_meta_device:
+                self.transfer_manager.set_fake_transfer(True)
             with Timer() as t:
                 self.transfer_manager.transfer_optimizer_tensors(space)
         finally:
             space.src_state = space.dst_state = None
+            self.transfer_manager.set_fake_transfer(fake)
         return t.elapsed
 
     def transfer_staged(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
@@ -168,18 +179,25 @@ class ElasticMegatronManager:
                 src.release_kind(k)
         return elapsed, (stats, names) if verify else None
 
-    def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool) -> float:
+    def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool,
+                         is_meta_device: bool = False) -> float:
+        """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
+        ``is_meta_device`` plans and caches without moving data.  Returns the executor's ms."""
         plan = self.transfer_manager.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
         with Timer() as t:
-            self.transfer_manager.execute(plan, src, dst)
+            if not is_meta_device:
+                self.transfer_manager.execute(plan, src, dst)
         return t.elapsed
 
-    def log_communication_info(self, transfer_time: float, logger: Optional[logging.Logger] = None) -> str:
+    def log_communication_info(self, transfer_time: float, union_world_group=None,
+                               logger: Optional[logging.Logger] = None) -> str:
         """The reference's perf line (elastic_manager.py:158-178) plus the payload written on the device.
 
         ``communication bytes`` keeps the reference's definition (GiB a rank
         would exchange with other ranks, max over ranks); ``payload`` is the
-        decimal GB of state written on the device.
+        decimal GB of state written on the device.  The reference reduces the
+        line's figures over ``union_world_group``; one process already holds
+        every rank's figures, so the group is accepted and unused.
         """
         gib = self.transfer_manager.get_communication_bytes()
         payload = self.transfer_manager.get_payload_bytes()
@@ -266,7 +284,7 @@ class ElasticMegatronManager:
         if self.release_source:
             src_state.release_optimizer()
         self.training_state = dst_state
-        msg = self.log_communication_info(elapsed, logger)
+        msg = self.log_communication_info(elapsed, logger=logger)
         if logger is None and torch.distributed.is_available() and not torch.distributed.is_initialized():
             print(msg)
         return dst_state

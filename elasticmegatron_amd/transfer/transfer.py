@@ -119,9 +119,9 @@ class TransferManager:
         self._payload_bytes = 0
         self._comm_bytes = 0
 
-    def set_fake_transfer(self, fake: bool) -> None:
+    def set_fake_transfer(self, fake_transfer: bool) -> None:
         """Plan without moving data (transfer.py:32-34)."""
-        self.fake_transfer = fake
+        self.fake_transfer = fake_transfer
 
     def evict(self, strategy: Optional[ParallelStrategy] = None) -> int:
         """Drop the cached plans (copy and verification) that switch from or to ``strategy``, or every

@@ -255,3 +255,58 @@ def test_block_and_print_keeps_the_reference_signature():
     recvs = sum(len(d) for vp in space.all_virtual_params for d in vp.reshard_plan.global_recv_info.values())
     assert sum(l.startswith("  send") for l in text) == sends > 0
     assert sum(l.startswith("  recv") for l in text) == recvs > 0
+
+
+def test_fake_transfer_plans_without_moving_data():
+    """set_fake_transfer(fake_transfer) under the reference's argument name (transfer.py:32-34):
+    with it set a transfer plans, caches the plan and returns before touching either state, so it
+    runs on CPU states too; cleared, the same call refuses them."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(tiny_llama2())
+    s, d = ParallelStrategy(8, 1, 1), ParallelStrategy(8, 2, 1)
+    src, dst = TrainingState.allocate(space.layout(s), "cpu"), TrainingState.allocate(space.layout(d), "cpu")
+    src.main.fill_(1.0)
+    dst.main.zero_()
+    tm = TransferManager()
+    tm.set_fake_transfer(fake_transfer=True)
+    plan = tm.transfer_optimizer_tensors(space, src=src, dst=dst)
+    assert plan.payload_bytes > 0 and tm.compile(src.layout, dst.layout) is plan
+    assert int(dst.main.count_nonzero()) == 0
+    tm.set_fake_transfer(False)
+    with pytest.raises(RuntimeError, match="GPU memory"):
+        tm.transfer_optimizer_tensors(space, src=src, dst=dst)
+
+
+def test_manager_transfer_methods_keep_the_reference_argument_order():
+    """transfer_params(src, dst, union_world_group, is_meta_device), redundant_backup(src, dst,
+    is_scale_up, is_meta_device) and log_communication_info(transfer_time, union_world_group,
+    logger) in the reference's order (elastic_manager.py:106-178).  With ``is_meta_device`` both
+    transfers only plan, so CPU states pass through untouched and the fake flag is restored."""
+    import logging
+
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
+    space = mgr.virtual_param_space
+    src = mgr.training_state
+    dst = TrainingState.allocate(space.layout(ParallelStrategy(**SEQ[1])), "cpu")
+    src.main.fill_(1.0)
+    dst.main.zero_()
+    assert mgr.transfer_params(src, dst, None, True) >= 0.0
+    assert int(dst.main.count_nonzero()) == 0 and mgr.transfer_manager.fake_transfer is False
+    with pytest.raises(RuntimeError, match="GPU memory"):
+        mgr.transfer_params(src, dst, None, False)
+    assert mgr.transfer_manager.fake_transfer is False
+    s, d = ParallelStrategy(8, 1, 1, num_distributed_optimizer_instances=2), ParallelStrategy(4, 1, 1)
+    a, b = TrainingState.allocate(space.layout(s), "cpu"), TrainingState.allocate(space.layout(d), "cpu")
+    assert mgr.redundant_backup(a, b, False, True) >= 0.0
+    seen = []
+
+    class Keep(logging.Handler):
+        def emit(self, record):
+            seen.append(record.getMessage())
+
+    log = logging.getLogger("emrs-test-perf-line")
+    log.addHandler(Keep())
+    log.setLevel(logging.INFO)
+    msg = mgr.log_communication_info(12.5, None, log)
+    assert seen == [msg] and msg.startswith("[ElasticMegatron-Perf] : transfer time: 12.50 ms")
