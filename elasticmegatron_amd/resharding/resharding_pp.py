@@ -81,12 +81,10 @@ class ParamPositionAttr:
         return info
 
     def __str__(self):
-        if self.transformer_layer_id == -1:
-            return f"layer_type={self.layer_type}, global_index={self.global_index}, layer_index={self.layer_index}"
-        if self.is_expert:
-            return (f"global_index={self.global_index}, transformer_layer_id={self.transformer_layer_id}, "
-                    f"expert_id={self.expert_id}, expert_param_layer_id={self.expert_param_layer_id}")
-        return (f"global_index={self.global_index}, transformer_layer_id={self.transformer_layer_id}, "
-                f"layer_index={self.layer_index}")
+        where = (f"layer {self.transformer_layer_id}" if self.transformer_layer_id != -1
+                 else self.layer_type.value)
+        slot = (f"expert {self.expert_id} param {self.expert_param_layer_id}" if self.is_expert
+                else f"param {self.layer_index}")
+        return f"#{self.global_index} {where} {slot} {self.module_name}".rstrip()
 
     __repr__ = __str__

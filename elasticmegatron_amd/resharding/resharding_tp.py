@@ -105,12 +105,16 @@ class TensorParallelAttr:
                 send[d * k + i] = {d: chunks[0]}
         return TensorParallelReshardingInfo(send_info=send, recv_info=recv)
 
+    def _key(self):
+        return (self.tensor_model_parallel, self.partition_dim, self.partition_stride,
+                self.model_param_range_in_group)
+
     def __hash__(self):
-        return hash((self.tensor_model_parallel, self.partition_dim, self.partition_stride,
-                     self.model_param_range_in_group))
+        return hash(self._key())
 
     def __eq__(self, other):
-        return isinstance(other, TensorParallelAttr) and hash(self) == hash(other)
+        # Equal attributes, not equal hashes: two attributes whose hashes collide stay distinct.
+        return isinstance(other, TensorParallelAttr) and self._key() == other._key()
 
     def __str__(self):
         split = f"split on dim {self.partition_dim}" if self.tensor_model_parallel else "replicated"
