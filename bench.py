@@ -113,6 +113,9 @@ def parse():
                     help="time several launch shapes on the same allocations, in --rounds rounds, e.g. "
                          "'default;units=4,chunk_index=0;units=2'; prints one JSON line per workload")
     ap.add_argument("--rounds", type=int, default=3, help="rounds of --shape-sweep")
+    ap.add_argument("--rank-shares", action="store_true",
+                    help="time each destination rank's share of the plan on its own (the part one GPU "
+                         "would run with one rank per GPU) beside the whole plan, on the same allocations")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
@@ -268,6 +271,9 @@ def main():
     if args.shape_sweep is not None:
         return shape_sweep(args, desc, tm, plan, a, b, backup, ls.space.spec.padded_vocab_size if repad else None,
                            stream)
+    if args.rank_shares:
+        return rank_shares(args, desc, tm, plan, ls, ld, kind, a, b, backup,
+                           ls.space.spec.padded_vocab_size if repad else None, stream)
     views = {}
 
     def step(a, b):
@@ -614,6 +620,72 @@ def shape_sweep(args, desc, tm, plan, a, b, backup, vocab_rows, stream):
     print(json.dumps({"workload": desc, "what": "launch shapes on the same allocations in one process",
                       "steps": args.steps, "warmup": args.warmup, "rounds": args.rounds,
                       "traffic_bytes": plan.traffic_bytes, "verified_bit_exact": True, "shapes": rows}), flush=True)
+    return 0
+
+
+XGMI_INGRESS_GBPS = 7 * 153.0  # seven peer links per MI355X, each about 153 GB/s one way
+
+
+def rank_shares(args, desc, tm, plan, ls, ld, kind, a, b, backup, vocab_rows, stream):
+    """Each destination rank's share of the plan (``TransferManager.compile_shares``), timed on its
+    own after the whole plan, on the same allocations, with its reads split into the source rank of
+    the same number (local with one rank per GPU) and the others (over xGMI then).  The destination
+    is first overwritten, then written by the shares alone and checked against the generator."""
+    import torch
+
+    from elasticmegatron_amd.resharding.shares import pull_bytes
+
+    per_rank, rest = tm.compile_shares(ls, ld, kind)
+    arenas = [b.main, b.exp_avg, b.exp_avg_sq] + ([b.param] if backup is None else [])
+    for t in arenas:
+        t.view(torch.int16 if t.element_size() == 2 else torch.int32).fill_(-1)
+    for p in list(per_rank) + [rest]:
+        if len(p.segments):
+            tm.execute(p, a, b, stream)
+    torch.cuda.synchronize()
+    bad, first = b.verify_synthetic(SEED, bf16=backup is None, vocab_rows=vocab_rows)
+    if bad:
+        print(f"[bench] shares verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+        return 3
+
+    def timed(p):
+        for _ in range(args.warmup):
+            tm.execute(p, a, b, stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            tm.execute(p, a, b, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    whole_ms = timed(plan)
+    rows = []
+    for g, p in enumerate(per_rank):
+        if not len(p.segments):
+            rows.append({"rank": g, "segments": 0})
+            continue
+        ms = timed(p)
+        fp32, param = pull_bytes(p.segments, ls)
+        local = int(fp32[g]) if g < len(fp32) else 0
+        remote = int(fp32.sum()) - local + param
+        rows.append({"rank": g, "segments": int(len(p.segments)), "payload_bytes": p.payload_bytes,
+                     "read_bytes": p.read_bytes, "ms": round(ms, 4),
+                     "traffic_gbps": round(p.traffic_bytes / (ms / 1e3) / 1e9, 1),
+                     "frac_of_hbm_peak": round(p.traffic_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "read_local_bytes": local, "read_remote_bytes": remote,
+                     "remote_at_xgmi_ingress_ms": round(remote / (XGMI_INGRESS_GBPS * 1e9) * 1e3, 3)})
+    timed_rows = [r for r in rows if r.get("ms")]
+    out = {"what": "each destination rank's share of the copy plan timed alone on one GPU, every source in "
+                   "its HBM; with one rank per GPU, share g is GPU g's part and its remote reads come over xGMI",
+           "workload": desc, "kind": kind, "steps": args.steps, "warmup": args.warmup,
+           "whole_plan_ms": round(whole_ms, 4),
+           "whole_plan_gbps": round(plan.traffic_bytes / (whole_ms / 1e3) / 1e9, 1),
+           "sum_of_shares_ms": round(sum(r["ms"] for r in timed_rows), 4),
+           "max_share_ms": max((r["ms"] for r in timed_rows), default=0.0),
+           "bf16_remainder_segments": int(len(rest.segments)),
+           "verified_bit_exact": True, "launch": launch_shape(), "shares": rows}
+    print(json.dumps(out), flush=True)
     return 0
 
 

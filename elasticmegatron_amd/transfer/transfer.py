@@ -26,6 +26,7 @@ from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, StrategyLayout
+from ..resharding.shares import destination_rank_shares
 from ..resharding.tensors import TensorBuffers, rebase_on_tensors
 from .verify import VerifyReport, report_from_stats
 
@@ -186,6 +187,31 @@ class TransferManager:
         stages = tuple(out)
         self._plans[key] = stages
         return stages
+
+    def compile_shares(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
+                       include_bf16: bool = True) -> Tuple[Tuple[CompiledPlan, ...], CompiledPlan]:
+        """The switch split by destination rank (``resharding.shares``): plan g writes rank g's
+        fp32 shard, with the bf16 image of its ``main`` pieces, and nothing else; the last plan
+        holds the segments whose primary destination is the bf16 param arena (none when the bf16
+        params are cast).  With one rank per GPU, plan g is what GPU g would run, its sources then
+        partly on peers.  Run in any order on the same arenas, they write what :meth:`compile`
+        writes."""
+        key = ("shares", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
+               self.bf16_source)
+        got = self._plans.get(key)
+        if got is not None:
+            return got
+        full = self.compile(src, dst, kind, include_bf16)
+        per_rank, bf16 = destination_rank_shares(full.segments, dst)
+
+        def plan_of(t):
+            return CompiledPlan(t, _native.Plan(t, full.src_buf_bytes, full.dst_buf_bytes, self.check_disjoint),
+                                payload_bytes(t), read_bytes(t), full.src, full.dst, 0, full.src_buf_bytes,
+                                full.dst_buf_bytes, *_arena_refs(t))
+
+        got = (tuple(plan_of(t) for t in per_rank), plan_of(bf16))
+        self._plans[key] = got
+        return got
 
     def compile_tensors(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                         include_bf16: bool = True) -> CompiledTensorPlan:

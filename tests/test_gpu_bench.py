@@ -40,3 +40,14 @@ def test_shape_sweep_times_every_shape_on_the_same_allocations(gpu_device):
     assert [(r["launch"]["units_per_lane"], r["launch"]["chunk_index"]) for r in d["shapes"]] == \
         [(1, 1), (4, 0), (2, 1)]
     assert all(len(r["ms"]) == 2 and r["best_ms"] > 0 for r in d["shapes"])
+
+
+@pytest.mark.gpu
+def test_rank_shares_line(gpu_device):
+    """--rank-shares: every destination rank's share is written alone and checked, then timed."""
+    d = _bench("--rank-shares", "--steps", "2", "--warmup", "1")
+    assert d["verified_bit_exact"] is True and d["bf16_remainder_segments"] == 0
+    assert [r["rank"] for r in d["shares"]] == list(range(8))
+    assert all(r["segments"] > 0 and r["ms"] > 0 for r in d["shares"])
+    assert sum(r["payload_bytes"] for r in d["shares"]) > 0
+    assert d["whole_plan_ms"] > 0 and d["sum_of_shares_ms"] >= d["max_share_ms"] > 0

@@ -1,0 +1,97 @@
+"""Destination-rank shares on the device: the sub-plans one GPU each would run with one rank per GPU.
+
+Every rank's share, launched one after another on canary-filled destination
+arenas, must leave exactly what the whole plan leaves, bit for bit (the whole
+plan is pinned to Oracle-1 by the parity tests), on small switches with both
+bf16 sources, a re-padded vocabulary and Group-ZeRO switches; the padding
+keeps its canary.  Each share alone writes only its own rank's fp32 region.
+"""
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from elasticmegatron_amd.transfer.transfer import TransferManager
+from tests.helpers import (REPAD_CASES, SEED, SMALL_CASES, fill_canaries, padding_damage, perturb_per_rank,
+                           repad_spaces, small_llama2)
+from tests.test_group_zero import CASES as GZ_CASES
+
+pytestmark = pytest.mark.gpu
+
+
+def _host(state, with_param=True):
+    torch.cuda.synchronize()
+    out = [t.cpu().view(torch.int32).numpy().copy() for t in state.arenas()[:3]]
+    if with_param:
+        out.append(state.param.cpu().view(torch.int16).numpy().copy())
+    return out
+
+
+def _run(gpu_device, ls, ld, kind, tm, group_zero=False):
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    if group_zero:
+        perturb_per_rank(a)
+    share_param = a.param if group_zero else None
+    whole = TrainingState.allocate(ld, gpu_device, param=share_param)
+    parts = TrainingState.allocate(ld, gpu_device, param=share_param)
+    for st in (whole, parts):
+        fill_canaries(st)
+    tm.execute(tm.compile(ls, ld, kind), a, whole)
+    want = _host(whole, not group_zero)
+    per_rank, rest = tm.compile_shares(ls, ld, kind)
+    for g, p in enumerate(per_rank):
+        before = _host(parts, False)
+        if len(p.segments):
+            tm.execute(p, a, parts)
+        after = _host(parts, False)
+        lo, hi = ld.rank_fp32_slice(g)
+        for x, y in zip(before, after):  # nothing outside rank g's region changes
+            assert np.array_equal(np.delete(x, np.s_[lo:hi]), np.delete(y, np.s_[lo:hi])), g
+    if len(rest.segments):
+        tm.execute(rest, a, parts)
+    got = _host(parts, not group_zero)
+    for w, x in zip(want, got):
+        assert np.array_equal(w, x)
+    assert padding_damage(parts, bf16=not group_zero) == 0
+
+
+def _switches():
+    for name, factory, seq in SMALL_CASES:
+        for a, b in zip(seq, seq[1:]):
+            yield pytest.param(factory, a, b, id=f"{name}-{a.tensor_model_parallel_size}x"
+                               f"{a.pipeline_model_parallel_size}x{a.world_size}-{b.tensor_model_parallel_size}x"
+                               f"{b.pipeline_model_parallel_size}x{b.world_size}")
+
+
+@pytest.mark.parametrize("factory,src,dst,bf16_source",
+                         [p.values + ("cast",) for p in _switches()] +
+                         [p.values + ("copy",) for p in list(_switches())[:3]])
+def test_shares_leave_what_the_plan_leaves(gpu_device, factory, src, dst, bf16_source):
+    spec = factory()
+    print(f"shares {spec.name} {src.tensor_model_parallel_size}x{src.pipeline_model_parallel_size} -> "
+          f"{dst.tensor_model_parallel_size}x{dst.pipeline_model_parallel_size} bf16 {bf16_source}", flush=True)
+    space = build_virtual_model(spec)
+    _run(gpu_device, space.layout(src), space.layout(dst), "transfer", TransferManager(bf16_source=bf16_source))
+
+
+@pytest.mark.parametrize("factory,vocab,src,dst", REPAD_CASES[:2])
+def test_shares_of_a_repadded_switch(gpu_device, factory, vocab, src, dst):
+    spec = replace(factory(), vocab_size=vocab)
+    print(f"shares repad {spec.name} vocab {vocab}", flush=True)
+    sa, sb = repad_spaces(spec, (src.tensor_model_parallel_size, dst.tensor_model_parallel_size))
+    _run(gpu_device, sa.layout(src), sb.layout(dst), "transfer", TransferManager())
+
+
+@pytest.mark.parametrize("scale_up", [True, False], ids=["scale_up", "scale_down"])
+@pytest.mark.parametrize("name,small,big", GZ_CASES[:2], ids=[c[0] for c in GZ_CASES[:2]])
+def test_shares_of_a_group_zero_switch(gpu_device, name, small, big, scale_up):
+    print(f"shares group-zero {name} {'up' if scale_up else 'down'}", flush=True)
+    src, dst = (small, big) if scale_up else (big, small)
+    space = build_virtual_model(small_llama2())
+    _run(gpu_device, space.layout(src), space.layout(dst), "backup_up" if scale_up else "backup_down",
+         TransferManager(), group_zero=True)

@@ -1,0 +1,156 @@
+"""Destination-rank shares of a plan: the sub-plan one GPU would run with one rank per GPU.
+
+Run one after another on the same buffers, the shares must write exactly what
+the whole plan writes (numpy model of the kernel), bit for bit, on every small
+switch, both bf16 sources, re-padded vocabularies and Group-ZeRO switches.
+Each share writes only its own rank's fp32 region; only the bf16 remainder
+has a primary destination in the param arena.
+"""
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from elasticmegatron_amd import ParallelStrategy as PS
+from elasticmegatron_amd.resharding.layout import ARENA_PARAM, SEG_DUP, SEG_ZERO_FILL
+from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
+from elasticmegatron_amd.resharding.shares import destination_rank_shares, fp32_rank_of
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from tests.helpers import REPAD_CASES, SEED, SMALL_CASES, execute_numpy, new_arenas, piece_fill_numpy, repad_spaces
+from tests.test_group_zero import CASES as GZ_CASES
+
+
+def _switches():
+    for name, factory, seq in SMALL_CASES:
+        for a, b in zip(seq, seq[1:]):
+            yield pytest.param(factory, a, b, id=f"{name}-{a}-{b}".replace(" ", ""))
+
+
+def _check(ls, ld, table):
+    shares, bf16 = destination_rank_shares(table, ld)
+    assert len(shares) == ld.strategy.world_size
+    for g, t in enumerate(shares):
+        assert not np.any(t["flags"] & SEG_DUP & (fp32_rank_of(t["aux_off"], ld) != g))
+        assert np.all(t["dst_buf"] != ARENA_PARAM)
+        assert np.all(fp32_rank_of(t["dst_off"], ld) == g)
+    assert np.all(bf16["dst_buf"] == ARENA_PARAM)
+    # Same bytes written; a split duplicate reads its source once per share instead of once.
+    parts = list(shares) + [bf16]
+    assert sum(payload_bytes(t) for t in parts) == payload_bytes(table)
+    assert sum(read_bytes(t) for t in parts) >= read_bytes(table)
+    if not np.any(table["flags"] & SEG_DUP):
+        assert sum(read_bytes(t) for t in parts) == read_bytes(table)
+
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    whole, pieces = new_arenas(ld), new_arenas(ld)
+    execute_numpy(table, a, whole)
+    for t in parts:
+        execute_numpy(t, a, pieces)
+    for w, p in zip(whole, pieces):
+        assert np.array_equal(w, p)
+    return shares, bf16
+
+
+@pytest.mark.parametrize("factory,src,dst", list(_switches()))
+@pytest.mark.parametrize("bf16_source", ["cast", "copy"])
+def test_shares_write_what_the_plan_writes(factory, src, dst, bf16_source):
+    space = build_virtual_model(factory())
+    ls, ld = space.layout(src), space.layout(dst)
+    table = lower_transfer(ls, ld, bf16_source=bf16_source)
+    shares, bf16 = _check(ls, ld, table)
+    if bf16_source == "cast":
+        assert len(bf16) == 0  # every bf16 element rides on a main segment of some rank
+    else:
+        assert len(bf16) > 0
+
+
+@pytest.mark.parametrize("factory,vocab,src,dst", REPAD_CASES)
+def test_shares_of_a_repadded_switch(factory, vocab, src, dst):
+    spec = replace(factory(), vocab_size=vocab)
+    sa, sb = repad_spaces(spec, (src.tensor_model_parallel_size, dst.tensor_model_parallel_size))
+    ls, ld = sa.layout(src), sb.layout(dst)
+    table = lower_transfer(ls, ld)
+    shares, bf16 = _check(ls, ld, table)
+    zero = table[(table["flags"] & SEG_ZERO_FILL) != 0]
+    if len(zero):
+        assert sum(int(((t["flags"] & SEG_ZERO_FILL) != 0).sum()) for t in shares) + \
+            int(((bf16["flags"] & SEG_ZERO_FILL) != 0).sum()) == len(zero)
+
+
+@pytest.mark.parametrize("scale_up", [True, False], ids=["scale_up", "scale_down"])
+@pytest.mark.parametrize("name,small,big", GZ_CASES, ids=[c[0] for c in GZ_CASES])
+def test_shares_of_a_group_zero_switch(name, small, big, scale_up):
+    from tests.helpers import small_llama2
+
+    src, dst = (small, big) if scale_up else (big, small)
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(src), space.layout(dst)
+    table = lower_redundant_backup(ls, ld, scale_up=scale_up)
+    shares, bf16 = _check(ls, ld, table)
+    assert len(bf16) == 0
+    if scale_up:
+        # Each new instance's ranks pull their own copy: no share keeps a duplicate to another rank.
+        assert np.any(table["flags"] & SEG_DUP)
+        assert sum(len(t) for t in shares) > len(table)
+
+
+def test_a_segment_across_ranks_is_cut_or_refused():
+    """A one-row segment running on into the next rank's region is cut there, the source and the
+    bf16 image shifting with it; a strided one spanning two regions is refused."""
+    space = build_virtual_model(SMALL_CASES[0][1]())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 1))
+    row = lower_transfer(ls, ld)[:1].copy()
+    row["rows"], row["src_stride"], row["dst_stride"], row["aux_stride"] = 1, 0, 0, 0
+    row["dst_off"], row["len"], row["src_off"], row["aux_off"] = ld.rank_base[1] - 3, 5, 100, 200
+    row["flags"] = 1  # with its bf16 image
+    shares, bf16 = destination_rank_shares(row, ld)
+    got = [(g, int(t["src_off"]), int(t["dst_off"]), int(t["len"]), int(t["aux_off"]))
+           for g, ts in enumerate(shares) for t in ts]
+    assert got == [(0, 100, ld.rank_base[1] - 3, 3, 200), (1, 103, ld.rank_base[1], 2, 203)]
+    assert len(bf16) == 0
+    strided = row.copy()
+    strided["rows"], strided["len"], strided["src_stride"], strided["dst_stride"] = 2, 2, 4, 4
+    strided["aux_stride"] = 4
+    with pytest.raises(ValueError, match="one rank's fp32 region"):
+        destination_rank_shares(strided, ld)
+
+
+def test_compile_shares_builds_one_native_plan_per_rank():
+    """TransferManager.compile_shares: one checked native plan per destination rank plus the bf16
+    remainder, cached; the shares' bytes add up to the whole plan's."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(SMALL_CASES[0][1]())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 4, 1))
+    tm = TransferManager()
+    per_rank, bf16 = tm.compile_shares(ls, ld)
+    assert tm.compile_shares(ls, ld)[0] is per_rank
+    whole = tm.compile(ls, ld)
+    assert len(per_rank) == 8 and len(bf16.segments) == 0
+    assert sum(p.payload_bytes for p in per_rank) == whole.payload_bytes
+    assert sum(p.read_bytes for p in per_rank) == whole.read_bytes
+    for p in per_rank:
+        assert p.native.stats().n_segments >= len(p.segments) > 0
+
+
+def test_pull_bytes_add_up_to_the_reads():
+    """Each share's reads split by source rank add up to its read bytes, and a TP4 -> TP4 identity
+    switch reads almost all of it from the destination rank's own source shard: only the
+    replicated (non-tensor-parallel) parameters come from TP rank 0's replica, as the reference
+    sends them (resharding_tp.py:119-139)."""
+    from elasticmegatron_amd.resharding.shares import pull_bytes
+
+    space = build_virtual_model(SMALL_CASES[0][1]())
+    for a, b in ((PS(8, 2, 1), PS(8, 1, 1)), (PS(8, 4, 1), PS(8, 4, 1))):
+        ls, ld = space.layout(a), space.layout(b)
+        table = lower_transfer(ls, ld)
+        shares, _ = destination_rank_shares(table, ld)
+        for g, t in enumerate(shares):
+            fp32, param = pull_bytes(t, ls)
+            assert int(fp32.sum()) + param == read_bytes(t)
+            if a == b:
+                assert 0.99 * int(fp32.sum()) < int(fp32[g])
+                if g % 4 == 0:  # TP rank 0 holds the replica it reads
+                    assert int(fp32.sum()) == int(fp32[g])
