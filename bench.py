@@ -66,8 +66,8 @@ def workloads():
     }
 
 
-SHAPE_KEYS = ("lanes", "units", "chunk_index", "xcd_remap", "buffer_ops", "nontemporal", "persistent",
-              "blocks_per_cu", "run")
+SHAPE_KEYS = ("lanes", "units", "chunk_index", "warm_tables", "xcd_remap", "buffer_ops", "nontemporal",
+              "persistent", "blocks_per_cu", "run")
 
 
 def parse_shapes(text):
@@ -124,6 +124,8 @@ def parse():
                     help="16-byte units per lane (default 1; 0: a whole chunk per workgroup, 256 / lanes)")
     ap.add_argument("--chunk-index", type=int, default=1, choices=(0, 1),
                     help="1: each workgroup reads its segment from the plan's chunk table; 0: binary search")
+    ap.add_argument("--warm-tables", type=int, default=1, choices=(0, 1),
+                    help="1: read the chunk and segment tables just before each copy (with --chunk-index 1)")
     ap.add_argument("--persistent", type=int, default=0,
                     help="0: one workgroup per piece of a chunk; 1: persistent grid (--blocks-per-cu, --run)")
     ap.add_argument("--blocks-per-cu", type=int, default=0, help="persistent grid; 0: as many as can be resident")
@@ -236,7 +238,8 @@ def main():
     torch.cuda.set_device(dev)
     _native.load()
     _native.set_tuning(args.blocks_per_cu, bool(args.nontemporal), args.xcd_remap, args.run,
-                       bool(args.persistent), args.lanes, args.units, chunk_index=bool(args.chunk_index))
+                       bool(args.persistent), args.lanes, args.units, chunk_index=bool(args.chunk_index),
+                       warm_tables=bool(args.warm_tables))
     stream = torch.cuda.current_stream(dev)
 
     if args.copy_calibration_gib > 0:
@@ -320,6 +323,9 @@ def main():
     if verified is False:
         return 3
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    cold_ms = cold_launch_ms(lambda: step(a, b), flush, stream, 3)
+    del flush
     ms = sum(step_ms) / len(step_ms)
     payload = plan.payload_bytes
     gbps = payload / (ms / 1e3) / 1e9
@@ -351,6 +357,7 @@ def main():
                    "first_third_ms": round(sum(step_ms[:max(1, len(step_ms) // 3)]) / max(1, len(step_ms) // 3), 4),
                    "last_third_ms": round(sum(step_ms[-max(1, len(step_ms) // 3):]) / max(1, len(step_ms) // 3), 4),
                    "launch": launch_shape(),
+                   "cold_launch_ms": round(cold_ms, 4),
                    "reference_perf_line": {
                        "what": "the figures of the reference's perf log line (elastic_manager.py:158-178): GiB "
                                "of fp32 state the busiest rank would exchange with other ranks, per second of "
@@ -581,7 +588,8 @@ def shape_sweep(args, desc, tm, plan, a, b, backup, vocab_rows, stream):
 
     from elasticmegatron_amd import _native
 
-    rows = [{"shape": shp or "default", "ms": []} for shp in args.shape_sweep]
+    rows = [{"shape": shp or "default", "ms": [], "cold_ms": []} for shp in args.shape_sweep]
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=a.main.device)
     try:
         for r in range(args.rounds):
             for shp, row in zip(args.shape_sweep, rows):
@@ -612,15 +620,39 @@ def shape_sweep(args, desc, tm, plan, a, b, backup, vocab_rows, stream):
                 e1.record(stream)
                 torch.cuda.synchronize()
                 row["ms"].append(round(e0.elapsed_time(e1) / args.steps, 4))
+                row["cold_ms"].append(round(cold_launch_ms(lambda: tm.execute(plan, a, b, stream), flush, stream,
+                                                           args.steps), 4))
     finally:
         _native.set_tuning()
     for row in rows:
         row["best_ms"] = min(row["ms"])
+        row["best_cold_ms"] = min(row["cold_ms"])
         row["traffic_tbps_at_best"] = round(plan.traffic_bytes / (row["best_ms"] / 1e3) / 1e12, 3)
-    print(json.dumps({"workload": desc, "what": "launch shapes on the same allocations in one process",
+    print(json.dumps({"workload": desc, "what": "launch shapes on the same allocations in one process; ms: "
+                      "back-to-back launches, cold_ms: each launch after a fill of other memory",
                       "steps": args.steps, "warmup": args.warmup, "rounds": args.rounds,
                       "traffic_bytes": plan.traffic_bytes, "verified_bit_exact": True, "shapes": rows}), flush=True)
     return 0
+
+
+FLUSH_BYTES = 512 << 20  # more than the 256 MB memory-side cache
+
+
+def cold_launch_ms(run, flush, stream, n):
+    """Mean time of ``n`` launches of ``run``, each straight after a fill of ``flush`` (other memory,
+    larger than the memory-side cache), as a single switch in a training job follows other kernels."""
+    import torch
+
+    total = 0.0
+    for i in range(n):
+        flush.fill_(i & 0xFF)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1)
+    return total / n
 
 
 XGMI_INGRESS_GBPS = 7 * 153.0  # seven peer links per MI355X, each about 153 GB/s one way
@@ -698,7 +730,8 @@ def launch_shape():
         return {"grid": "persistent", "blocks_per_cu": t.blocks_per_cu, "run": t.run, "xcd_remap": t.xcd_remap,
                 "nontemporal": t.nontemporal}
     return {"grid": "one workgroup per piece", "lanes": t.lanes, "units_per_lane": t.units,
-            "piece_bytes": 16 * t.lanes * t.units, "chunk_index": t.chunk_index, "xcd_remap": t.xcd_remap,
+            "piece_bytes": 16 * t.lanes * t.units, "chunk_index": t.chunk_index, "warm_tables": t.warm_tables,
+            "xcd_remap": t.xcd_remap,
             "buffer_ops": t.buffer_ops, "nontemporal": t.nontemporal}
 
 
@@ -742,7 +775,7 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
     tu = _native.get_tuning()
     shape = dict(blocks_per_cu=tu.blocks_per_cu, nontemporal=bool(tu.nontemporal), xcd_remap=tu.xcd_remap,
                  run=tu.run, persistent=bool(tu.persistent), lanes=tu.lanes, buffer_ops=bool(tu.buffer_ops),
-                 chunk_index=bool(tu.chunk_index))
+                 chunk_index=bool(tu.chunk_index), warm_tables=bool(tu.warm_tables))
     _native.set_tuning(**shape, units=0)  # one workgroup per chunk
     try:
         w_ms = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))

@@ -69,7 +69,7 @@ class Tuning(ctypes.Structure):
     _fields_ = [("blocks_per_cu", ctypes.c_uint32), ("nontemporal", ctypes.c_uint32),
                 ("xcd_remap", ctypes.c_uint32), ("run", ctypes.c_uint32), ("persistent", ctypes.c_uint32),
                 ("lanes", ctypes.c_uint32), ("units", ctypes.c_uint32), ("buffer_ops", ctypes.c_uint32),
-                ("chunk_index", ctypes.c_uint32)]
+                ("chunk_index", ctypes.c_uint32), ("warm_tables", ctypes.c_uint32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -112,7 +112,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_plan_compare_static.argtypes = [P, P, P, P, P, U32, P, P]
     lib.emrs_xor_checksum.restype = I
     lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
-    if lib.emrs_abi_version() != 6:
+    if lib.emrs_abi_version() != 7:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib
@@ -149,16 +149,18 @@ def get_tuning() -> Tuning:
 
 def set_tuning(blocks_per_cu: int = 0, nontemporal: bool = True, xcd_remap: int = 1, run: int = 4,
                persistent: bool = False, lanes: int = 0, units: int = 1, buffer_ops: bool = False,
-               chunk_index: bool = True) -> None:
+               chunk_index: bool = True, warm_tables: bool = True) -> None:
     """Launch shape of every later execution.  The default runs one workgroup of ``lanes`` lanes
     (0: 64) with ``units`` 16-byte units each (0: a whole chunk of 256 units per workgroup) per piece
     of a chunk, each finding its segment in the plan's chunk table (``chunk_index``; False: by a
     bounded binary search); ``persistent=True`` selects a persistent grid, which ``blocks_per_cu``
     and ``run`` shape.  ``xcd_remap`` gives each of the 8 XCDs one contiguous eighth of the chunks:
     1 (or True) in the persistent grid and for plans of at least 2^19 chunks, 2 always, 0 (or False)
-    never."""
+    never.  ``warm_tables``: with the chunk table, a short kernel reads it and the segment
+    descriptors just before each copy, so that a launch after unrelated work starts from cached
+    tables."""
     t = Tuning(blocks_per_cu, 1 if nontemporal else 0, int(xcd_remap), run, 1 if persistent else 0, lanes,
-               units, 1 if buffer_ops else 0, 1 if chunk_index else 0)
+               units, 1 if buffer_ops else 0, 1 if chunk_index else 0, 1 if warm_tables else 0)
     _check(load().emrs_set_tuning(ctypes.byref(t)), "emrs_set_tuning")
 
 

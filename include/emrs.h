@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 6
+#define EMRS_ABI_VERSION 7
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -273,6 +273,10 @@ typedef struct emrs_tuning {
                              device and freed with the plan; when that allocation runs out of
                              memory, the launch searches instead); 0: a binary search bounded by
                              a hint in the kernel arguments */
+  uint32_t warm_tables;   /* with the chunk table, 1 (default): a short kernel reads the chunk table
+                             and the segment descriptors just before each copy, so that the copy's
+                             first load in every workgroup hits the memory-side cache even when the
+                             launch follows unrelated work; 0: the copy alone */
 } emrs_tuning;
 
 int emrs_get_tuning(emrs_tuning *out);

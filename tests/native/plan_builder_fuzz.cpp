@@ -60,6 +60,7 @@ int main(int argc, char **argv) {
   for (int i = 0; i < 200; ++i) {
     emrs_get_tuning(&tu);
     tu.lanes = (uint32_t)U(0, 300); tu.units = (uint32_t)U(0, 5); tu.xcd_remap = (uint32_t)U(0, 3);
+    tu.warm_tables = (uint32_t)U(0, 2);
     (void)emrs_set_tuning(&tu);
   }
   printf("ok %d rejected %d\n", ok, bad);

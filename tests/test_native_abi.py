@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol():
     assert set(declared) == set(_native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.emrs_abi_version() == 6
+    assert lib.emrs_abi_version() == 7
 
 
 def test_record_layouts_match_header():
@@ -232,10 +232,13 @@ def test_xor_checksum_rejects_bad_arguments_before_touching_a_device():
 def test_tuning_defaults_and_rejections():
     """emrs_tuning: the default launch shape reads back, settings round-trip, and values outside the
     documented ranges are refused without changing the current setting (no device needed)."""
-    assert ctypes.sizeof(_native.Tuning) == 36  # nine uint32 fields, as in emrs.h
+    assert ctypes.sizeof(_native.Tuning) == 40  # ten uint32 fields, as in emrs.h
     t = _native.get_tuning()
-    assert (t.persistent, t.lanes, t.units, t.nontemporal, t.run, t.chunk_index) == (0, 64, 1, 1, 4, 1)
+    assert (t.persistent, t.lanes, t.units, t.nontemporal, t.run, t.chunk_index, t.warm_tables) == \
+        (0, 64, 1, 1, 4, 1, 1)
     try:
+        _native.set_tuning(warm_tables=False)
+        assert _native.get_tuning().warm_tables == 0
         _native.set_tuning(lanes=128, units=0, persistent=True, run=7, blocks_per_cu=3, chunk_index=False)
         t = _native.get_tuning()
         assert (t.persistent, t.lanes, t.run, t.blocks_per_cu, t.chunk_index) == (1, 128, 7, 3, 0)
@@ -258,5 +261,5 @@ def test_tuning_defaults_and_rejections():
     finally:
         _native.set_tuning()
     t = _native.get_tuning()
-    assert (t.persistent, t.lanes, t.units, t.run, t.blocks_per_cu, t.xcd_remap, t.chunk_index) == \
-        (0, 64, 1, 4, 0, 1, 1)
+    assert (t.persistent, t.lanes, t.units, t.run, t.blocks_per_cu, t.xcd_remap, t.chunk_index, t.warm_tables) == \
+        (0, 64, 1, 4, 0, 1, 1, 1)
