@@ -41,7 +41,7 @@ EXPORTS = (
     "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
     "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
     "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare", "emrs_xor_checksum",
-    "emrs_plan_compare_static",
+    "emrs_plan_compare_static", "emrs_plan_prepare",
 )
 
 # struct emrs_compare_stats
@@ -96,6 +96,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_plan_stats_get.argtypes = [P, ctypes.POINTER(PlanStats)]
     lib.emrs_plan_execute.restype = I
     lib.emrs_plan_execute.argtypes = [P, P, P, P]
+    lib.emrs_plan_prepare.restype = I
+    lib.emrs_plan_prepare.argtypes = [P, P]
     lib.emrs_plan_destroy.restype = I
     lib.emrs_plan_destroy.argtypes = [P]
     lib.emrs_get_tuning.restype = I
@@ -191,6 +193,11 @@ class Plan:
         rc = load().emrs_plan_execute(self._handle, _ptr_array(src_ptrs), _ptr_array(dst_ptrs),
                                       ctypes.c_void_p(int(stream)))
         _check(rc, "emrs_plan_execute")
+
+    def prepare(self, stream: int = 0) -> None:
+        """Upload the plan's tables to the current device now (emrs_plan_prepare), so that its first
+        execution there runs as fast as later ones."""
+        _check(load().emrs_plan_prepare(self._handle, ctypes.c_void_p(int(stream))), "emrs_plan_prepare")
 
     def compare(self, src_ptrs: Sequence[int], dst_ptrs: Sequence[int], groups: Optional[np.ndarray] = None,
                 aux_groups: Optional[np.ndarray] = None, n_groups: int = 1, stream: int = 0,

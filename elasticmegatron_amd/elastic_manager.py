@@ -225,9 +225,11 @@ class ElasticMegatronManager:
                 verify: bool = False) -> Optional[TrainingState]:
         """Switch every rank's state to ``new_parallel_strategy``; returns the new state.
 
-        ``is_meta_device=True`` builds and caches the plan without touching
-        device memory and returns None (the reference's meta-device
-        pre-build, elastic_manager.py:268-304).
+        ``is_meta_device=True`` builds and caches the plan, uploads its tables
+        to the state's GPU (nothing else: no state is allocated or touched)
+        and returns None; the real switch then runs as fast as a repeated one.
+        This is the reference's meta-device pre-build, which runs a fake
+        transfer to build its NCCL connections (elastic_manager.py:268-304).
 
         ``verify=True`` compares the new state with the old one on the device
         before the old one is released (the reference's offline checkpoint
@@ -253,9 +255,10 @@ class ElasticMegatronManager:
             plan = self.transfer_manager.compile(src_state.layout, dst_layout,
                                                  "backup_up" if backup else "backup_down")
         kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
-        if self.low_memory:
-            self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind)
+        stages = self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind) if self.low_memory else ()
         if is_meta_device:
+            if src_state.device.type == "cuda":
+                self.transfer_manager.prepare(stages or plan, src_state.device)
             return None
         # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over.
         param = src_state.param if backup is not None else None

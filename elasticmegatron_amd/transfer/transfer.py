@@ -188,6 +188,21 @@ class TransferManager:
         self._plans[key] = stages
         return stages
 
+    def prepare(self, plans, device) -> None:
+        """Upload the tables of a compiled plan (or of several, such as the stages of
+        :meth:`compile_staged`) to ``device`` now, so that their first execution there runs as fast
+        as later ones: the counterpart of the reference's meta-device pass, which builds its NCCL
+        connections ahead of the switch (elastic_manager.py:282-304)."""
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("plans are prepared on a GPU: the reshard has no CPU path")
+        if isinstance(plans, (CompiledPlan, CompiledTensorPlan)):
+            plans = (plans,)
+        with torch.cuda.device(device):
+            st = torch.cuda.current_stream(device)
+            for p in plans:
+                p.native.prepare(st.cuda_stream)
+
     def compile_shares(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
                        include_bf16: bool = True) -> Tuple[Tuple[CompiledPlan, ...], CompiledPlan]:
         """The switch split by destination rank (``resharding.shares``): plan g writes rank g's

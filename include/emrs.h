@@ -154,8 +154,9 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
  * (EMRS_ERR_ALIAS): the copy is out of place.  Unreferenced buffers are not
  * checked and may be NULL.  The first call on a device uploads the plan's
  * tables (segment table, chunk table and, beyond 128 buffers a side, its
- * pointer table for these bases) synchronously; later calls with the same bases enqueue one kernel launch
- * and nothing else, so they may be captured into a HIP graph.  Calls with
+ * pointer table for these bases) synchronously; later calls with the same bases enqueue the copy
+ * kernel, preceded by the table pre-read of emrs_tuning.warm_tables, and
+ * nothing else, so they may be captured into a HIP graph.  Calls with
  * other bases than the first beyond 128 buffers allocate a stream-ordered
  * pointer table.  Neither the first call nor such a call may be captured:
  * while `stream` is capturing they return EMRS_ERR_CAPTURE and enqueue
@@ -165,6 +166,20 @@ int emrs_plan_stats_get(const emrs_plan *plan, emrs_plan_stats *out);
  */
 int emrs_plan_execute(emrs_plan *plan, void *const *src_bases,
                       void *const *dst_bases, void *stream);
+
+/*
+ * Do on the current device what the plan's first emrs_plan_execute there
+ * would do before copying: upload the segment table and, when
+ * emrs_tuning.chunk_index is on and emrs_tuning.persistent off (the
+ * default), build the chunk table on the device.  Nothing is copied and no buffer is touched, so the first switch
+ * then runs as fast as later ones.  Synchronous with `stream`; while it
+ * captures a graph, EMRS_ERR_CAPTURE.  Replaces the reference's meta-device
+ * pass, which runs a fake transfer to build its NCCL connections ahead of
+ * the real switch (build_nccl_connection_context and its use in
+ * ElasticMegatronManager.transfer_params, elastic_manager.py:115-117,
+ * :282-304).
+ */
+int emrs_plan_prepare(emrs_plan *plan, void *stream);
 
 /*
  * Free the plan.  It first waits for every device that holds its table, so a

@@ -1,0 +1,86 @@
+"""GPU: emrs_plan_prepare, the meta-device pre-build of a plan's device tables.
+
+A prepared plan's first execution needs no upload, so it can be the first
+call captured into a HIP graph; the graph replays bit-exact, with eager work
+and a check between replays.  Prepare itself uploads, so under capture it is
+refused and records nothing.  ElasticMegatronManager.reshard(is_meta_device=True)
+prepares the plan on the state's GPU without allocating any state, and the
+real switch that follows is bit-exact.
+"""
+
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager, _native
+from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
+from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+from elasticmegatron_amd.resharding.model_spec import tiny_llama2
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from elasticmegatron_amd.transfer.transfer import TransferManager
+from tests.helpers import SEED, small_llama2
+
+pytestmark = pytest.mark.gpu
+
+
+def _scramble(state):
+    for t in (state.main, state.exp_avg, state.exp_avg_sq):
+        t.view(torch.int32).fill_(-1)
+    state.param.view(torch.int16).fill_(-1)
+
+
+def test_prepared_plan_is_captured_on_its_first_call(gpu_device):
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 1))
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    tm = TransferManager()
+    # The library meets the device outside any capture first (device properties, kernel code).
+    other = space.layout(PS(8, 4, 1))
+    tm.execute(tm.compile(ls, other), a, TrainingState.allocate(other, gpu_device))
+    plan = tm.compile(ls, ld)
+    marker = torch.zeros(1, device=gpu_device)
+    torch.cuda.synchronize()
+
+    print("case prepare under capture", flush=True)
+    graph0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph0):
+        marker.fill_(1.0)
+        with pytest.raises(_native.EmrsError) as e:
+            tm.prepare(plan, gpu_device)
+    assert e.value.code == -9 and "capturing" in str(e.value)
+
+    print("case prepare, then capture the first execution", flush=True)
+    tm.prepare(plan, gpu_device)
+    tm.prepare(plan, gpu_device)  # a second prepare finds the tables in place
+    _scramble(b)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tm.execute(plan, a, b)
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] > 0   # captured, not run
+    for r in range(3):
+        _scramble(b)
+        marker.fill_(float(r))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert b.verify_synthetic(SEED)[0] == 0, r
+
+
+def test_meta_device_reshard_prepares_the_plan(gpu_device):
+    seq = [dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1),
+           dict(world_size=8, tensor_model_parallel_size=4, pipeline_model_parallel_size=1)]
+    for low_memory in (False, True):
+        print(f"case meta-device reshard, low_memory={low_memory}", flush=True)
+        mgr = ElasticMegatronManager(seq, tiny_llama2(), device=gpu_device, low_memory=low_memory)
+        mgr.training_state.fill_synthetic(SEED)
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated(gpu_device)
+        assert mgr.reshard(seq[1], is_meta_device=True) is None
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated(gpu_device) == before   # no state allocated
+        new = mgr.reshard(seq[1], verify=True)
+        assert mgr.last_verification.bit_exact
+        assert new.verify_synthetic(SEED)[0] == 0

@@ -161,11 +161,15 @@ def test_zero_fill_reads_nothing():
 def test_empty_plan_and_no_device_errors():
     plan = _native.Plan(np.zeros(0, dtype=SEGMENT_DTYPE), [16], [16])
     assert plan.stats().payload_bytes == 0
+    plan.prepare(0)  # nothing to upload: no device needed
     if _native.device_count() == 0:
         # Host-side checks happen before any device work; a real execution needs a GPU.
         t = _native.Plan(_seg(), [1024], [1024])
         with pytest.raises(_native.EmrsError) as e:
             t.execute([0x10000], [0x20000], 0)
+        assert e.value.code == -6
+        with pytest.raises(_native.EmrsError) as e:
+            t.prepare(0)
         assert e.value.code == -6
 
 
