@@ -5,6 +5,7 @@
 - Segments beyond 2^30 units, which emrs_plan_create splits so that the
   kernel's unit arithmetic stays in 32 bits: a 1-D and a 2-D byte segment
   of 1.5 GiB each (the element-wise path, where a unit is one byte).
+- 70,000 segments in one plan, with and without the chunk table.
 Expected results come from torch slicing on the device.
 """
 
@@ -216,3 +217,34 @@ def test_long_row_pitches_are_emitted_row_by_row(gpu_device, buffer_ops):
     for r in range(4):
         want[4 + n + r * 64:4 + n + r * 64 + 16] = src[8 + n + r * 64:8 + n + r * 64 + 16]
     assert torch.equal(dst, want)
+
+
+@pytest.mark.parametrize("chunk_index", [True, False])
+def test_more_than_65535_segments(gpu_device, chunk_index):
+    """70,000 one-chunk segments in a random order, every seventh a zero fill: more segments than
+    one grid row of the device-side chunk-table build, which then strides over them."""
+    n, unit = 70_000, 1024  # fp32 elements per segment: one 4 KB chunk
+    g = torch.Generator().manual_seed(7)
+    perm = torch.randperm(n, generator=g)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n * unit,), dtype=torch.int32, generator=g).to(gpu_device)
+    dst = torch.full((n * unit,), -1, dtype=torch.int32, device=gpu_device)
+    t = np.zeros(n, dtype=SEGMENT_DTYPE)
+    t["elem_bytes"] = 4
+    t["src_off"] = perm.numpy().astype(np.uint64) * unit
+    t["dst_off"] = np.arange(n, dtype=np.uint64) * unit
+    t["len"] = unit
+    t["rows"] = 1
+    zero = np.arange(n) % 7 == 3
+    t["flags"][zero] = 2
+    plan = _native.Plan(t, [n * unit * 4], [n * unit * 4])
+    assert plan.stats().n_device_segments >= n
+    print(f"case {n} segments, chunk_index={chunk_index}", flush=True)
+    try:
+        _native.set_tuning(chunk_index=chunk_index)
+        plan.execute([src.data_ptr()], [dst.data_ptr()], torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning()
+    want = src.view(n, unit)[perm.to(gpu_device)].clone()
+    want[torch.from_numpy(zero).to(gpu_device)] = 0
+    assert torch.equal(dst.view(n, unit), want)
