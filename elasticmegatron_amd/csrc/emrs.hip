@@ -1130,8 +1130,8 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_
   return EMRS_OK;
 }
 
-// The device segment of every chunk on device `dev`, built and uploaded on
-// first use and never written again.
+// The device segment of every chunk on device `dev`, written on the device
+// from its segment table `segs` on first use and never written again.
 int chunk_table(emrs_plan *plan, int dev, hipStream_t st, const DevSeg *segs, uint32_t **out) {
   std::lock_guard<std::mutex> lk(plan->mu);
   if ((int)plan->chunk_tables.size() <= dev) plan->chunk_tables.resize(dev + 1, nullptr);
