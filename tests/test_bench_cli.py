@@ -41,7 +41,11 @@ def test_launch_shape_flags_are_checked_before_any_device_work():
     assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""
     r = _run("--help")
     assert r.returncode == 0 and all(f in r.stdout for f in ("--lanes", "--units", "--persistent", "--megatron-buffers",
-                                                              "--low-memory", "--tensors"))
+                                                              "--low-memory", "--tensors", "--rank-shares",
+                                                              "--warm-tables"))
+    r = _run("--warm-tables", "2")
+    assert r.returncode == 2 and "invalid choice" in r.stderr and r.stdout == ""
+    assert bench.parse_shapes("warm_tables=0") == [{"warm_tables": 0}]
 
 
 @pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="checks the behaviour without a GPU")
