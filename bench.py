@@ -5,7 +5,8 @@ Default workload: Llama-2-7B shape (6.74e9 params), bf16 params + fp32 main /
 exp_avg / exp_avg_sq, world 8 simulated on one GPU, distributed optimizer with
 40M-element buckets, TP1 PP1 DP8 -> TP4 PP1 DP2, emitting every target shard.
 
-A step is one execution of the switch's copy plan (one kernel launch) with
+A step is one execution of the switch's copy plan (the copy kernel, after a
+short pre-read of the plan's lookup tables) with
 every source shard already resident in HBM.  Inputs are synthetic: seeded
 values ~N(0, 0.02) for bf16 params, main = their exact upcast, exp_avg
 ~N(0, 1e-3), exp_avg_sq = |N(0, 1e-6)|.  The destination is checked

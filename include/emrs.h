@@ -16,7 +16,7 @@
  *       elastic_megatron/transfer/communicator.py:61-96
  *
  * Here the whole transfer is one precomputed plan of copy segments executed
- * by one kernel launch over device-resident buffers.  Every segment copies
+ * by one copy kernel launch over device-resident buffers.  Every segment copies
  * `rows` rows of `len` elements of `elem_bytes` bytes each, bit for bit:
  *
  *   for r in [0, rows):

@@ -2,7 +2,7 @@
 
 After its first execution a plan's device table is uploaded (and, for a plan
 over more than 128 buffers, its pointer table is kept), so an execution with
-the same base pointers is one kernel launch with no allocation, no memset and
+the same base pointers is the table pre-read and the copy launch, with no allocation, no memset and
 no host synchronisation: it can be captured.  Each replay, with eager work
 on the same memory between replays, must give the same bit-exact result as
 an eager execution.
