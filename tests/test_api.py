@@ -310,3 +310,17 @@ def test_manager_transfer_methods_keep_the_reference_argument_order():
     log.setLevel(logging.INFO)
     msg = mgr.log_communication_info(12.5, None, log)
     assert seen == [msg] and msg.startswith("[ElasticMegatron-Perf] : transfer time: 12.50 ms")
+
+
+def test_prepare_needs_a_gpu_and_meta_reshard_on_cpu_skips_it():
+    """TransferManager.prepare refuses a CPU device (no CPU path); a meta-device reshard of CPU
+    states plans without preparing anything."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(tiny_llama2())
+    ls, ld = space.layout(ParallelStrategy(8, 2, 1)), space.layout(ParallelStrategy(8, 1, 1))
+    tm = TransferManager()
+    with pytest.raises(RuntimeError, match="GPU"):
+        tm.prepare(tm.compile(ls, ld), "cpu")
+    mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu", low_memory=True)
+    assert mgr.reshard(SEQ[1], is_meta_device=True) is None
