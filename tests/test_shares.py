@@ -24,7 +24,9 @@ from tests.test_group_zero import CASES as GZ_CASES
 def _switches():
     for name, factory, seq in SMALL_CASES:
         for a, b in zip(seq, seq[1:]):
-            yield pytest.param(factory, a, b, id=f"{name}-{a}-{b}".replace(" ", ""))
+            yield pytest.param(factory, a, b, id=f"{name}-{a.tensor_model_parallel_size}x{a.pipeline_model_parallel_size}x"
+                               f"{a.world_size}-{b.tensor_model_parallel_size}x{b.pipeline_model_parallel_size}x"
+                               f"{b.world_size}")
 
 
 def _check(ls, ld, table):
