@@ -125,18 +125,23 @@ def _check(rc: int, where: str) -> None:
         raise EmrsError(rc, where, load().emrs_last_error().decode(errors="replace"))
 
 
+def _u64_buffer(vals: Sequence[int]) -> np.ndarray:
+    a = np.array(vals if len(vals) else [0], dtype=np.uint64)
+    if a.ndim != 1:
+        raise ValueError("expected a flat sequence of integers")
+    return a
+
+
 def _ptr_array(ptrs: Sequence[int]):
-    arr = (ctypes.c_void_p * max(1, len(ptrs)))()
-    for i, p in enumerate(ptrs):
-        arr[i] = ctypes.c_void_p(int(p))
-    return arr
+    """A C array of device pointers over a numpy buffer (one conversion, no per-element ctypes
+    objects: a per-tensor plan passes thousands).  The array keeps the buffer alive."""
+    a = _u64_buffer(ptrs)
+    return (ctypes.c_void_p * a.size).from_buffer(a)
 
 
 def _u64_array(vals: Sequence[int]):
-    arr = (ctypes.c_uint64 * max(1, len(vals)))()
-    for i, v in enumerate(vals):
-        arr[i] = int(v)
-    return arr
+    a = _u64_buffer(vals)
+    return (ctypes.c_uint64 * a.size).from_buffer(a)
 
 
 def device_count() -> int:

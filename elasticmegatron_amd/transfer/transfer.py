@@ -94,6 +94,11 @@ class CompiledTensorPlan:
     dst: TensorBuffers
     payload_bytes: int
     read_bytes: int
+    buffer_nbytes: list = None   # bytes of every source, then every destination buffer
+
+    def __post_init__(self):
+        if self.buffer_nbytes is None:
+            self.buffer_nbytes = self.src.nbytes() + self.dst.nbytes()
 
 
 class TransferManager:
@@ -254,16 +259,19 @@ class TransferManager:
             return
         if len(src_tensors) != len(plan.src) or len(dst_tensors) != len(plan.dst):
             raise ValueError("tensor lists do not match the plan's buffers")
-        for t, nb in zip(list(src_tensors) + list(dst_tensors), plan.src.nbytes() + plan.dst.nbytes()):
-            if t.numel() * t.element_size() != nb or not t.is_contiguous():
-                raise ValueError("a tensor does not match its buffer (bytes or layout)")
-        dev = src_tensors[0].device if len(src_tensors) else dst_tensors[0].device
+        ts = list(src_tensors) + list(dst_tensors)
+        # One pass per property in list comprehensions: a per-tensor plan passes thousands of
+        # tensors, and this check runs before every launch.
+        if [t.nbytes for t in ts] != plan.buffer_nbytes or not all([t.is_contiguous() for t in ts]):
+            raise ValueError("a tensor does not match its buffer (bytes or layout)")
+        dev = ts[0].device
         if dev.type != "cuda":
             raise RuntimeError("tensors must live in GPU memory: the reshard has no CPU path")
         st = stream if stream is not None else torch.cuda.current_stream(dev)
+        ptrs = [t.data_ptr() for t in ts]
+        ns = len(plan.src)
         with torch.cuda.device(dev):
-            plan.native.execute([t.data_ptr() for t in src_tensors], [t.data_ptr() for t in dst_tensors],
-                                st.cuda_stream)
+            plan.native.execute(ptrs[:ns], ptrs[ns:], st.cuda_stream)
         self._payload_bytes += plan.payload_bytes
 
     def execute(self, plan: CompiledPlan, src: TrainingState, dst: TrainingState,
