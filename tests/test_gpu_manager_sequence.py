@@ -1,0 +1,49 @@
+"""GPU: a full-size elastic sequence through ElasticMegatronManager, as a job would run it.
+
+Llama-2-7B moves through TP1DP8 -> TP4DP2 -> TP2PP2DP2 -> DP6 (world 6) ->
+Group ZeRO with two instances (world 12) -> DP6 -> TP1DP8, one reshard() at a time:
+each switch pre-built by a meta-device pass, then run and verified on the
+device against the state it replaced, the old optimizer state released.  At
+the end every element must still hold the seeded generator's value, which a
+single wrong hop anywhere in the chain would break.  Run once with whole
+switches and once staged (low_memory), where each optimizer kind moves in a
+launch of its own.
+"""
+
+import gc
+
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager
+from elasticmegatron_amd.resharding import model_spec as ms
+
+pytestmark = pytest.mark.gpu
+SEED = 4321
+CHAIN = [dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+         dict(world_size=8, tensor_model_parallel_size=4, pipeline_model_parallel_size=1),
+         dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=2),
+         dict(world_size=6, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+         dict(world_size=12, tensor_model_parallel_size=1, pipeline_model_parallel_size=1,
+              num_distributed_optimizer_instances=2),
+         dict(world_size=6, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+         dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1)]
+
+
+@pytest.mark.parametrize("low_memory", [False, True], ids=["whole", "staged"])
+def test_full_size_chain_through_the_manager(gpu_device, low_memory):
+    mgr = ElasticMegatronManager(CHAIN, ms.llama2_7b(), device=gpu_device, low_memory=low_memory)
+    try:
+        mgr.training_state.fill_synthetic(SEED)
+        for k, nxt in enumerate(CHAIN[1:], 1):
+            print(f"chain hop {k}: -> {nxt}, low_memory={low_memory}", flush=True)
+            assert mgr.reshard(nxt, is_meta_device=True) is None
+            state = mgr.reshard(nxt, verify=True)
+            assert mgr.last_verification.bit_exact, k
+            assert state.parallel_strategy == mgr.training_state.parallel_strategy
+        bad, first = mgr.training_state.verify_synthetic(SEED)
+        assert bad == 0, first
+    finally:
+        mgr = None
+        gc.collect()
+        torch.cuda.empty_cache()
