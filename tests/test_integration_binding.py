@@ -4,9 +4,9 @@ The Python block under "The Python-side binding a maintainer would add" is
 executed with its library name pointed at the in-tree build.  On the CPU its
 segment record and flag values must equal the header's (as the product's
 binding states them), and it must create plans and surface the library's
-errors.  On the GPU the tiny LLaMA-2 switches run through it must reproduce
-the golden digests (tests/golden/tiny_llama2.json), which the oracle is pinned
-against.
+errors.  On the GPU the tiny LLaMA-2 switches run through it (the first one
+prepared ahead, as the meta-device pass would) must reproduce the golden
+digests (tests/golden/tiny_llama2.json), which the oracle is pinned against.
 """
 
 import json
@@ -94,6 +94,8 @@ def test_binding_runs_the_golden_switches(gpu_device, binding):
                for x in dst]
         h = binding["plan_create"](lower_transfer(ls, ld), _sizes(ls), _sizes(ld))
         try:
+            if i == 0:
+                binding["plan_prepare"](h, torch.cuda.current_stream(gpu_device))
             binding["plan_execute"](h, to_dev, out, torch.cuda.current_stream(gpu_device))
             torch.cuda.synchronize(gpu_device)
         finally:
