@@ -156,3 +156,24 @@ def test_pull_bytes_add_up_to_the_reads():
                 assert 0.99 * int(fp32.sum()) < int(fp32[g])
                 if g % 4 == 0:  # TP rank 0 holds the replica it reads
                     assert int(fp32.sum()) == int(fp32[g])
+
+
+def test_pull_bytes_splits_a_read_across_source_ranks():
+    """A one-row read that runs from one source rank's region into the next is split between the
+    two; a strided read across a boundary is refused; zero fills read nothing."""
+    from elasticmegatron_amd.resharding.shares import pull_bytes
+
+    space = build_virtual_model(SMALL_CASES[0][1]())
+    ls = space.layout(PS(8, 2, 1))
+    row = np.zeros(1, dtype=lower_transfer(ls, space.layout(PS(8, 1, 1))).dtype)
+    row["elem_bytes"], row["rows"], row["len"] = 4, 1, 10
+    row["src_off"] = ls.rank_base[3] - 4
+    fp32, param = pull_bytes(row, ls)
+    assert fp32[2] == 16 and fp32[3] == 24 and int(fp32.sum()) == 40 and param == 0
+    zero = row.copy()
+    zero["flags"] = SEG_ZERO_FILL
+    assert int(pull_bytes(zero, ls)[0].sum()) == 0
+    strided = row.copy()
+    strided["rows"], strided["len"], strided["src_stride"] = 2, 4, 8
+    with pytest.raises(ValueError, match="strided"):
+        pull_bytes(strided, ls)
