@@ -84,3 +84,22 @@ def test_meta_device_reshard_prepares_the_plan(gpu_device):
         new = mgr.reshard(seq[1], verify=True)
         assert mgr.last_verification.bit_exact
         assert new.verify_synthetic(SEED)[0] == 0
+
+
+def test_prepared_per_tensor_plan(gpu_device):
+    """A per-tensor plan (more than 128 buffers a side) prepared ahead: its tables are in place, and
+    the first execution, which still uploads the pointer table of its bases, is bit-exact."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 1, 1)), space.layout(PS(8, 4, 1))
+    tm = TransferManager()
+    plan = tm.compile_tensors(ls, ld)
+    assert len(plan.src) > 128
+    print("case prepare a per-tensor plan", flush=True)
+    tm.prepare(plan, gpu_device)
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    _scramble(b)
+    tm.execute_tensors(plan, plan.src.views(a), plan.dst.views(b))
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] == 0
