@@ -49,6 +49,7 @@ int main(int argc, char **argv) {
       if (emrs_plan_stats_get(p, &st) != EMRS_OK) { fprintf(stderr, "stats failed\n"); return 1; }
       std::vector<void *> s(ns, (void *)0x1000), d(nd, (void *)0x100000);
       (void)emrs_plan_execute(p, s.data(), d.data(), nullptr);  // no device: must refuse
+      (void)emrs_plan_prepare(p, nullptr);                       // likewise
       emrs_plan_destroy(p);
     } else {
       ++bad;
