@@ -41,7 +41,8 @@ EXPORTS = (
     "emrs_last_error", "emrs_abi_version", "emrs_device_count", "emrs_plan_create",
     "emrs_plan_stats_get", "emrs_plan_execute", "emrs_plan_destroy", "emrs_get_tuning",
     "emrs_set_tuning", "emrs_synth_fill", "emrs_synth_verify", "emrs_plan_compare", "emrs_xor_checksum",
-    "emrs_plan_compare_static", "emrs_plan_prepare",
+    "emrs_plan_compare_static", "emrs_plan_prepare", "emrs_ipc_export", "emrs_ipc_open", "emrs_ipc_close",
+    "emrs_ipc_open_count",
 )
 
 # struct emrs_compare_stats
@@ -114,7 +115,15 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.emrs_plan_compare_static.argtypes = [P, P, P, P, P, U32, P, P]
     lib.emrs_xor_checksum.restype = I
     lib.emrs_xor_checksum.argtypes = [P, U64, P, P]
-    if lib.emrs_abi_version() != 7:
+    lib.emrs_ipc_export.restype = I
+    lib.emrs_ipc_export.argtypes = [P, U64, P]
+    lib.emrs_ipc_open.restype = I
+    lib.emrs_ipc_open.argtypes = [P, ctypes.POINTER(P)]
+    lib.emrs_ipc_close.restype = I
+    lib.emrs_ipc_close.argtypes = [P]
+    lib.emrs_ipc_open_count.restype = I
+    lib.emrs_ipc_open_count.argtypes = []
+    if lib.emrs_abi_version() != 8:
         raise RuntimeError("libemrs ABI version mismatch")
     _lib = lib
     return lib
@@ -273,3 +282,35 @@ def synth_verify(pieces: np.ndarray, ptrs: Sequence[int], buf_bytes: Sequence[in
     _check(rc, "emrs_synth_verify")
     f = first.value
     return int(bad.value), (None if f == 2 ** 64 - 1 else (f >> 40, f & ((1 << 40) - 1)))
+
+
+# struct emrs_ipc_buffer: an exported buffer, as plain bytes that travel between processes.
+IPC_BUFFER_DTYPE = np.dtype([("handle", "u1", (64,)), ("offset", "<u8"), ("bytes", "<u8"),
+                             ("allocation_bytes", "<u8"), ("device", "<i4"), ("reserved", "<u4")])
+assert IPC_BUFFER_DTYPE.itemsize == 96
+EMRS_IPC_MAX_ALLOCATION_BYTES = 2 << 30  # exclusive
+
+
+def ipc_export(ptr: int, nbytes: int) -> np.ndarray:
+    """emrs_ipc_export: the record describing device buffer [ptr, ptr + nbytes) to another process."""
+    rec = np.zeros(1, dtype=IPC_BUFFER_DTYPE)
+    _check(load().emrs_ipc_export(ctypes.c_void_p(int(ptr)), int(nbytes), rec.ctypes.data), "emrs_ipc_export")
+    return rec[0]
+
+
+def ipc_open(record) -> int:
+    """emrs_ipc_open: map an exported buffer on the current device; returns its address."""
+    rec = np.ascontiguousarray(np.asarray(record, dtype=IPC_BUFFER_DTYPE).reshape(1))
+    out = ctypes.c_void_p()
+    _check(load().emrs_ipc_open(rec.ctypes.data, ctypes.byref(out)), "emrs_ipc_open")
+    return int(out.value)
+
+
+def ipc_close(ptr: int) -> None:
+    """emrs_ipc_close: drop one reference that :func:`ipc_open` returned."""
+    _check(load().emrs_ipc_close(ctypes.c_void_p(int(ptr))), "emrs_ipc_close")
+
+
+def ipc_open_count() -> int:
+    """Allocations this process holds open through :func:`ipc_open`."""
+    return int(load().emrs_ipc_open_count())

@@ -35,7 +35,8 @@ from .megatron_manager.training_state import ARENA_GRANULE_BYTES, TrainingState
 from .resharding.model_spec import ModelSpec
 from .resharding.util import Timer
 from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
-from .transfer.transfer import TransferManager
+from .transfer.ipc_manager import SharedTrainingState
+from .transfer.transfer import TransferManager, _granule_of
 from .transfer.verify import merge_stats, report_from_stats
 
 StrategyLike = Union[ParallelStrategy, Dict[str, int]]
@@ -51,7 +52,7 @@ class ElasticMegatronManager:
                  release_source: bool = True, repad_vocab: bool = False,
                  send_fn: Optional[Callable] = None, recv_fn: Optional[Callable] = None,
                  broadcast_fn: Optional[Callable] = None, use_p2p_to_collective: bool = True,
-                 low_memory: bool = False):
+                 low_memory: bool = False, share_granule_bytes: Optional[int] = None):
         """``model_spec`` and ``training_state`` stand in for the reference's live Megatron
         ``model`` / ``optimizer`` (elastic_manager.py:41-82).  ``send_fn``, ``recv_fn``,
         ``broadcast_fn`` and ``use_p2p_to_collective`` are accepted as the reference accepts
@@ -65,6 +66,14 @@ class ElasticMegatronManager:
         then allocated in 1 GiB granules, so that the memory a released source arena leaves serves
         the next destination arena without a call to the driver (a state passed in
         ``training_state`` should be allocated with ``granule_bytes=ARENA_GRANULE_BYTES`` too).
+
+        ``share_granule_bytes``: the states this manager allocates are
+        :class:`~.transfer.ipc_manager.SharedTrainingState`\ s with granules of that size, so that the
+        live state can be handed to another process at any time (``send_training_state``).  A
+        ``training_state`` passed in may be one as well, for instance one just received from the
+        process that held it (``receive_training_state``).  ``device="meta"`` allocates nothing: the
+        manager plans (``reshard(..., is_meta_device=True)``) until :meth:`attach_training_state`
+        hands it the real state, as the reference builds its new process on the meta device first.
         """
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
@@ -89,13 +98,44 @@ class ElasticMegatronManager:
         self.use_p2p_to_collective = use_p2p_to_collective
         self.release_source = release_source
         self.low_memory = low_memory
+        self.share_granule_bytes = share_granule_bytes
+        if low_memory and (share_granule_bytes is not None or isinstance(training_state, SharedTrainingState)):
+            raise NotImplementedError("staged switches run on TrainingState arenas, not on shared granules")
         self.last_stage_ms: List[Dict[str, float]] = []   # staged switches: per stage, allocate / execute ms
         self.last_transfer_ms = 0.0
         self.last_verification = None
         if training_state is None:
-            training_state = TrainingState.allocate(self.space_for(cur).layout(cur), device,
-                                                    granule_bytes=ARENA_GRANULE_BYTES if low_memory else 0)
+            training_state = self._allocate(self.space_for(cur).layout(cur), device)
         self.training_state = training_state
+
+    def _allocate(self, layout, device, param=None):
+        """A new state of ``layout`` of the kind this manager keeps (nothing on the meta device)."""
+        meta = device is not None and torch.device(device).type == "meta"
+        if self.share_granule_bytes is not None and not meta:
+            return SharedTrainingState.allocate(layout, device, self.share_granule_bytes, param_granules=param)
+        return TrainingState.allocate(layout, device, param=param,
+                                      granule_bytes=ARENA_GRANULE_BYTES if self.low_memory else 0)
+
+    def attach_training_state(self, state) -> None:
+        """Make ``state`` the live state: the state a meta-device manager was planning for, now
+        backed by memory, such as one received from the process that held it.  The reference swaps
+        the tensors it received into the optimizer of its meta-built model the same way
+        (tools/agent/env_utils.py:423-433).  It must use the current strategy and model."""
+        if state.parallel_strategy != self.training_state.parallel_strategy:
+            raise ValueError("the state does not use the manager's current strategy")
+        spec = state.layout.space.spec
+        if spec != self._spec_for(state.parallel_strategy):
+            raise ValueError("the state was laid out for another model")
+        if self.low_memory and isinstance(state, SharedTrainingState):
+            raise NotImplementedError("staged switches run on TrainingState arenas, not on shared granules")
+        space = state.layout.space
+        if space is not self._spaces.get(spec.padded_vocab_size):
+            # Adopt the state's virtual model, built for every strategy of the list it serves.
+            self._spaces[spec.padded_vocab_size] = space
+            for s in self.parallel_strategy_list:
+                if self._spec_for(s).padded_vocab_size == spec.padded_vocab_size:
+                    space.build_model_virtual_params(s)
+        self.training_state = state
 
     def _spec_for(self, strategy: ParallelStrategy) -> ModelSpec:
         pv = (self.model_spec.padded_vocab_for_tp(strategy.tensor_model_parallel_size) if self.repad_vocab
@@ -131,6 +171,13 @@ class ElasticMegatronManager:
         space = src.layout.space
         if space is dst.layout.space:
             space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
+        gs, gd = _granule_of(src), _granule_of(dst)
+        if gs is not None or gd is not None:   # shared granules: the re-based plan
+            plan = self.transfer_manager.compile_granules(src.layout, dst.layout, gs, gd)
+            with Timer() as t:
+                if not is_meta_device:
+                    self.transfer_manager.execute_states(plan, src, dst)
+            return t.elapsed
         plan = self.transfer_manager.compile(src.layout, dst.layout)
         # The states are the space's for the duration of the transfer only: the space outlives the
         # switch, and holding them would keep a released state's memory alive.
@@ -183,11 +230,24 @@ class ElasticMegatronManager:
                          is_meta_device: bool = False) -> float:
         """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
         ``is_meta_device`` plans and caches without moving data.  Returns the executor's ms."""
-        plan = self.transfer_manager.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
+        plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst),
+                                                     "backup_up" if is_scale_up else "backup_down")
         with Timer() as t:
             if not is_meta_device:
-                self.transfer_manager.execute(plan, src, dst)
+                self.transfer_manager.execute_states(plan, src, dst)
         return t.elapsed
+
+    @staticmethod
+    def _carried_params(src_state, dst_granule_bytes):
+        """The bf16 params a Group-ZeRO switch carries over unchanged: the source's own param arena
+        (or granules), which the new state shares."""
+        if isinstance(src_state, TrainingState) and dst_granule_bytes is None:
+            return src_state.param
+        if isinstance(src_state, SharedTrainingState) and not src_state.imported and \
+                src_state.granule_bytes == dst_granule_bytes:
+            return [src_state.tensors[b] for b in src_state.buffers.granules_of(3)]
+        raise NotImplementedError("a Group-ZeRO switch keeps the bf16 params in place: source and destination "
+                                  "must be states of the same kind, and a received state cannot be kept")
 
     def log_communication_info(self, transfer_time: float, union_world_group=None,
                                logger: Optional[logging.Logger] = None) -> str:
@@ -247,21 +307,21 @@ class ElasticMegatronManager:
         backup = ParallelStrategy.is_redundant_backup(src_strategy, dst_strategy)
         dst_space = self.space_for(dst_strategy)
         dst_layout = dst_space.layout(dst_strategy)
-        if backup is None:
-            if dst_space is space:
-                space.register_reshard(src_strategy, dst_strategy)
-            plan = self.transfer_manager.compile(src_state.layout, dst_layout)
-        else:
-            plan = self.transfer_manager.compile(src_state.layout, dst_layout,
-                                                 "backup_up" if backup else "backup_down")
+        if backup is None and dst_space is space:
+            space.register_reshard(src_strategy, dst_strategy)
         kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
+        gs = _granule_of(src_state)
+        gd = self.share_granule_bytes if src_state.device.type != "meta" else None
+        plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind)
         stages = self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind) if self.low_memory else ()
         if is_meta_device:
             if src_state.device.type == "cuda":
                 self.transfer_manager.prepare(stages or plan, src_state.device)
             return None
         # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over.
-        param = src_state.param if backup is not None else None
+        param = None
+        if backup is not None:
+            param = self._carried_params(src_state, gd)
         report = None
         if self.low_memory:
             dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),
@@ -270,7 +330,7 @@ class ElasticMegatronManager:
             if verify:
                 report = report_from_stats(*checked)
         else:
-            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param)
+            dst_state = self._allocate(dst_layout, src_state.device, param=param)
             if backup is None:
                 elapsed = self.transfer_params(src_state, dst_state)
             else:

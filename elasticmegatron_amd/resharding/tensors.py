@@ -123,19 +123,29 @@ class TensorBuffers:
         return [arenas[a][o:o + n] for a, o, n in zip(self.arena, self.offset, self.numel)]
 
 
-def rebase_on_tensors(table: np.ndarray, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
-    """The arena plan ``table`` re-expressed over per-tensor buffers.
+def rebase_on_tensors(table: np.ndarray, src, dst, return_origin: bool = False):
+    """The arena plan ``table`` re-expressed over separately allocated buffers.
 
-    A one-row segment that runs across tensor boundaries (tensors of one
-    parameter on consecutive ranks can be adjacent in an arena) is cut at
-    every boundary on the source, destination and second-destination (bf16
-    image or duplicate) sides; a strided segment always lies inside one
-    tensor on each side.  Segments that need no cut are mapped in bulk.
+    ``src`` and ``dst`` name the buffers and where each sits in its arena:
+    one per stored tensor (:class:`TensorBuffers`) or consecutive granules of
+    every arena (:class:`.granules.GranuleBuffers`); anything with their
+    ``locate`` / ``locate_many`` / ``boundaries`` works.  A segment that runs
+    across buffer boundaries on the source, destination or second-destination
+    (bf16 image or duplicate) side is cut at every one of them: a one-row
+    segment at the boundary, a strided one between rows, with a row that
+    straddles a boundary taken out as a row of its own.  Segments that need
+    no cut are mapped in bulk.
+
+    With ``return_origin`` also returns, per output row, the index of the
+    input row it came from (so that per-segment data such as verification
+    groups can follow the cuts).
     """
-    table = table[(table["len"] > 0)]
+    keep = np.flatnonzero(table["len"] > 0)
+    table = table[keep]
     n = len(table)
     if n == 0:
-        return np.zeros(0, dtype=SEGMENT_DTYPE)
+        out = np.zeros(0, dtype=SEGMENT_DTYPE)
+        return (out, np.zeros(0, dtype=np.int64)) if return_origin else out
     ln = table["len"].astype(np.int64)
     rows = table["rows"].astype(np.int64)
     zero = (table["flags"] & SEG_ZERO_FILL) != 0
@@ -155,17 +165,57 @@ def rebase_on_tensors(table: np.ndarray, src: TensorBuffers, dst: TensorBuffers)
     out["dst_buf"], out["dst_off"] = db[f], do[f]
     out["aux_buf"] = np.where(aux[f], ab[f], out["aux_buf"])
     out["aux_off"] = np.where(aux[f], ao[f], out["aux_off"])
-    rest = [_cut(s, src, dst) for s in table[~fits]]
-    if rest:
-        out = np.concatenate([out] + rest)
+    parts, origin = [out], [keep[f]]
+    for i in np.flatnonzero(~fits):
+        cut = _cut(table[i], src, dst)
+        parts.append(cut)
+        origin.append(np.full(len(cut), keep[i], dtype=np.int64))
+    out = np.concatenate(parts)
+    return (out, np.concatenate(origin).astype(np.int64)) if return_origin else out
+
+
+def _sides(s):
+    """(side, arena field, offset field, stride field) of every buffer a segment touches."""
+    flags = int(s["flags"])
+    out = []
+    if not flags & SEG_ZERO_FILL:
+        out.append(("src", "src_buf", "src_off", "src_stride"))
+    out.append(("dst", "dst_buf", "dst_off", "dst_stride"))
+    if flags & (SEG_CAST_BF16 | SEG_DUP):
+        out.append(("dst", "aux_buf", "aux_off", "aux_stride"))
     return out
 
 
-def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
-    """One segment that crosses tensor boundaries, cut at each of them."""
+def _rows_of(s, r0: int, r1: int):
+    """Rows [r0, r1) of a strided segment, as a segment of its own."""
+    r = s.copy()
+    for _, _, off, stride in (("", "", "src_off", "src_stride"), ("", "", "dst_off", "dst_stride"),
+                              ("", "", "aux_off", "aux_stride")):
+        r[off] = int(s[off]) + r0 * int(s[stride])
+    if int(s["flags"]) & SEG_ZERO_FILL:
+        r["src_off"] = s["src_off"]
+    r["rows"] = r1 - r0
+    return r
+
+
+def _cut(s, src, dst) -> np.ndarray:
+    """One segment that crosses buffer boundaries, cut at each of them."""
     n, rows = int(s["len"]), int(s["rows"])
+    sets = {"src": src, "dst": dst}
     if rows > 1:
-        raise AssertionError("a strided segment leaves its tensor")
+        # Walk down the rows: the leading rows clear of every side's next boundary form one
+        # piece; a row that straddles a boundary is cut on its own.
+        out, r = [], 0
+        while r < rows:
+            rest = _rows_of(s, r, rows)
+            take = _clean_rows(rest, sets, n, rows - r)
+            if take >= rows - r:
+                out.append(_cut_or_keep(rest, src, dst))
+                break
+            take = max(take, 1)
+            out.append(_cut_or_keep(_rows_of(s, r, r + take), src, dst))
+            r += take
+        return np.concatenate(out)
     zero = bool(int(s["flags"]) & SEG_ZERO_FILL)
     aux = bool(int(s["flags"]) & (SEG_CAST_BF16 | SEG_DUP))
     sa, da, aa = int(s["src_buf"]), int(s["dst_buf"]), int(s["aux_buf"])
@@ -189,4 +239,41 @@ def _cut(s, src: TensorBuffers, dst: TensorBuffers) -> np.ndarray:
             r["aux_buf"], r["aux_off"] = dst.locate(aa, ao + c0)
         r["len"] = c1 - c0
         out[i] = r
+    return out
+
+
+def _clean_rows(s, sets, n: int, rows: int) -> int:
+    """How many leading rows of a strided segment lie clear of every buffer boundary."""
+    clean = rows
+    for side, buf, off, stride in _sides(s):
+        o, st = int(s[off]), int(s[stride])
+        b = sets[side].boundaries(int(s[buf]), o, o + (rows - 1) * st + n)
+        if not b:
+            continue
+        if st == 0:     # every row reads the same elements: each is cut on its own
+            return 0
+        k, c = divmod(b[0] - o, st)
+        clean = min(clean, k + 1 if c >= n else k)
+    return clean
+
+
+def _cut_or_keep(s, src, dst) -> np.ndarray:
+    """``s`` re-based as one segment when it crosses no boundary, else cut."""
+    n, rows = int(s["len"]), int(s["rows"])
+    sets = {"src": src, "dst": dst}
+    for side, buf, off, stride in _sides(s):
+        o = int(s[off])
+        ext = (rows - 1) * int(s[stride]) + n if rows > 1 else n
+        if sets[side].boundaries(int(s[buf]), o, o + ext):
+            return _cut(s, src, dst)
+    r = s.copy()
+    if int(s["flags"]) & SEG_ZERO_FILL:
+        r["src_buf"], r["src_off"] = 0, 0
+    else:
+        r["src_buf"], r["src_off"] = src.locate(int(s["src_buf"]), int(s["src_off"]))
+    r["dst_buf"], r["dst_off"] = dst.locate(int(s["dst_buf"]), int(s["dst_off"]))
+    if int(s["flags"]) & (SEG_CAST_BF16 | SEG_DUP):
+        r["aux_buf"], r["aux_off"] = dst.locate(int(s["aux_buf"]), int(s["aux_off"]))
+    out = np.zeros(1, dtype=SEGMENT_DTYPE)
+    out[0] = r
     return out

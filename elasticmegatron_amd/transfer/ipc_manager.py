@@ -1,0 +1,335 @@
+"""Inter-process hand-off of a training state on one machine.
+
+Replaces elastic_megatron/transfer/ipc_manager.py.  There, the old process
+packs a CUDA-IPC handle for the storage of every optimizer tensor of every
+parameter (``_make_cuda_tensor_info``, :23-51), sends the pickled payload over
+a ZMQ socket and exits (``send_training_state``, :54-132); the new process
+rebuilds one tensor per handle (``receive_training_state``, :135-155), clones
+them into the optimizer of a model it built on the meta device and only then
+reshards (tools/agent/env_utils.py:326-483, the swap at :423-433).
+
+Here the old process holds its whole state in a :class:`SharedTrainingState`:
+the four arenas of a layout, each cut into granules of less than 2 GiB, one
+device allocation per granule, because device memory is shared one
+allocation at a time and only below that size.  ``send_training_state``
+exports every granule once (a few dozen handles for a 7B model instead of one
+per tensor) and writes a JSON payload: the model, the strategy, the granule
+size and the handle records.  ``receive_training_state`` maps the granules in
+the new process; the reshard then runs straight from the mapped memory into
+the new process's own state, one copy-plan launch re-based onto the granules
+(:class:`~..resharding.granules.GranuleBuffers`), with no clone.  The
+transport (a pipe, a socket, a file) is the caller's: the payload is one line
+of text, and holds nothing that runs when it is read.
+
+The memory stays owned by the old process, which must keep it until the new
+process has closed its mappings: :func:`notify_release` /
+:func:`wait_for_release` carry that signal over the same kind of channel.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import json
+import sys
+from typing import IO, Dict, List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from .. import _native
+from ..megatron_manager.parallel_strategy import ParallelStrategy
+from ..resharding.granules import DEFAULT_GRANULE_BYTES, GranuleBuffers
+from ..resharding.layout import ARENA_NAMES, ARENA_PARAM, StrategyLayout, split_vocab_rows
+from ..resharding.model_spec import ModelSpec
+
+PAYLOAD_FORMAT = "emrs-shared-state/1"
+RELEASED = "released"
+_STRATEGY_FIELDS = ("world_size", "tensor_model_parallel_size", "pipeline_model_parallel_size",
+                    "context_parallel_size", "num_distributed_optimizer_instances", "expert_model_parallel_size",
+                    "expert_tensor_parallel_size", "sequence_parallel")
+_DTYPES = (torch.float32, torch.float32, torch.float32, torch.bfloat16)
+
+
+class SharedTrainingState:
+    """Every rank's state of one strategy, held in granules that another process can map.
+
+    The same state as :class:`~..megatron_manager.training_state.TrainingState`
+    (fp32 ``main`` / ``exp_avg`` / ``exp_avg_sq`` of every rank, bf16 params of
+    every model-parallel shard), stored as ``buffers`` (arena granules in
+    buffer order).  Owned: the granules are torch tensors of this process.
+    Imported: they are another process's memory, mapped by
+    :func:`receive_training_state`, and :meth:`close` unmaps them.
+    """
+
+    def __init__(self, layout: StrategyLayout, buffers: GranuleBuffers, ptrs: Sequence[int],
+                 device: torch.device, tensors: Optional[List[torch.Tensor]] = None):
+        if len(ptrs) != len(buffers):
+            raise ValueError("one pointer per granule")
+        self.layout = layout
+        self.buffers = buffers
+        self._ptrs = list(ptrs)
+        self._device = torch.device(device)
+        self.tensors = tensors          # owned granules; None when imported
+        self._open = tensors is None    # imported mappings not yet closed
+        self._released = [False] * 4    # per arena
+
+    # ----- construction -----
+    @classmethod
+    def allocate(cls, layout: StrategyLayout, device=None, granule_bytes: int = DEFAULT_GRANULE_BYTES,
+                 param_granules: Optional[List[torch.Tensor]] = None) -> "SharedTrainingState":
+        """Uninitialised granules for ``layout``, one allocation each; ``param_granules`` may be the
+        bf16 granules of another state of the same model-parallel layout, shared instead."""
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if dev.type != "cuda":
+            raise RuntimeError("a shared state lives in GPU memory")
+        bufs = GranuleBuffers(layout, granule_bytes)
+        keep = list(bufs.granules_of(ARENA_PARAM))
+        if param_granules is not None and [t.numel() for t in param_granules] != [bufs.numel[b] for b in keep]:
+            raise ValueError("the shared param granules do not match the layout")
+        tensors = []
+        for b, (a, n) in enumerate(zip(bufs.arena, bufs.numel)):
+            if a == ARENA_PARAM and param_granules is not None:
+                tensors.append(param_granules[b - keep[0]])
+            else:
+                tensors.append(torch.empty(n, dtype=_DTYPES[a], device=dev))
+        return cls(layout, bufs, [t.data_ptr() for t in tensors], dev, tensors)
+
+    # ----- what the transfer manager reads -----
+    @property
+    def parallel_strategy(self) -> ParallelStrategy:
+        return self.layout.strategy
+
+    @property
+    def device(self) -> torch.device:
+        return self._device
+
+    @property
+    def granule_bytes(self) -> int:
+        return self.buffers.granule_bytes
+
+    @property
+    def imported(self) -> bool:
+        return self.tensors is None
+
+    def buffer_ptrs(self) -> List[int]:
+        if self.imported and not self._open:
+            raise RuntimeError("the shared state's mappings are closed")
+        return list(self._ptrs)
+
+    def buffer_bytes(self) -> List[int]:
+        """Bytes of every granule; 0 for the granules of a released arena."""
+        nb = self.buffers.nbytes()
+        return [0 if self._released[a] else n for a, n in zip(self.buffers.arena, nb)]
+
+    # ----- lifetime -----
+    def release_optimizer(self) -> None:
+        """Drop the fp32 state (training_state.py:313-315): owned granules are freed, and an
+        imported state is unmapped whole (its bf16 params went to the new state with the switch)."""
+        if self.imported:
+            self.close()
+            return
+        for a in range(3):
+            for b in self.buffers.granules_of(a):
+                self.tensors[b].untyped_storage().resize_(0)
+            self._released[a] = True
+
+    def close(self) -> None:
+        """Unmap every granule of an imported state (emrs_ipc_close).  Waits for the device first,
+        so work that still reads the mappings has finished."""
+        if not self.imported or not self._open:
+            return
+        with torch.cuda.device(self._device):
+            torch.cuda.synchronize(self._device)
+            for p in self._ptrs:
+                _native.ipc_close(p)
+        self._open = False
+        self._released = [True] * 4
+
+    # ----- synthetic workload -----
+    def _per_arena(self, pieces: np.ndarray):
+        """The pieces of each arena, addressed by granule within that arena (so that no call
+        passes more granules than one arena has)."""
+        pcs = self.buffers.split_pieces(pieces)
+        for a in range(4):
+            ids = self.buffers.granules_of(a)
+            sel = pcs[(pcs["buf"] >= ids.start) & (pcs["buf"] < ids.stop)].copy()
+            if len(sel) == 0:
+                continue
+            sel["buf"] -= ids.start
+            yield a, sel, [self._ptrs[b] for b in ids], [self.buffers.nbytes()[b] for b in ids]
+
+    def fill_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True) -> None:
+        """Write the seeded synthetic values of every stored element (see csrc/synth.hip)."""
+        st = torch.cuda.current_stream(self._device).cuda_stream
+        with torch.cuda.device(self._device):
+            for _, pcs, ptrs, nb in self._per_arena(self.layout.pieces(params, include_bf16=bf16,
+                                                                        include_fp32=fp32)):
+                _native.synth_fill(pcs, ptrs, nb, seed, st)
+
+    def verify_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True,
+                         vocab_rows: Optional[int] = None) -> Tuple[int, Optional[dict]]:
+        """(mismatching elements, first bad element) against the seeded synthetic values."""
+        pcs = self.layout.pieces(params, include_bf16=bf16, include_fp32=fp32)
+        if vocab_rows is not None:
+            pcs, zero = split_vocab_rows(self.layout, pcs, vocab_rows)
+            if zero:
+                raise NotImplementedError("re-padded vocabularies are checked on a TrainingState")
+        st = torch.cuda.current_stream(self._device).cuda_stream
+        bad, first = 0, None
+        with torch.cuda.device(self._device):
+            for a, sel, ptrs, nb in self._per_arena(pcs):
+                n, f = _native.synth_verify(sel, ptrs, nb, seed, st)
+                bad += n
+                if f is not None and first is None:
+                    p = sel[f[0]]
+                    first = dict(arena=ARENA_NAMES[a], param_id=int(p["param_id"]), kind=int(p["kind"]),
+                                 element=int(f[1]), granule=int(p["buf"]))
+        return bad, first
+
+    # ----- export -----
+    def export(self) -> List[np.ndarray]:
+        """One emrs_ipc_buffer record per granule (ipc_manager.py:23-51)."""
+        if self.imported:
+            raise RuntimeError("an imported state is exported by the process that owns it")
+        with torch.cuda.device(self._device):
+            return [_native.ipc_export(p, n) for p, n in zip(self._ptrs, self.buffers.nbytes())]
+
+
+def strategy_to_dict(s: ParallelStrategy) -> Dict:
+    return {k: getattr(s, k) for k in _STRATEGY_FIELDS}
+
+
+def _record_hex(rec) -> str:
+    return np.asarray(rec, dtype=_native.IPC_BUFFER_DTYPE).reshape(1).tobytes().hex()
+
+
+def _record_of(text: str) -> np.ndarray:
+    raw = bytes.fromhex(text)
+    if len(raw) != _native.IPC_BUFFER_DTYPE.itemsize:
+        raise ValueError("malformed buffer record")
+    return np.frombuffer(raw, dtype=_native.IPC_BUFFER_DTYPE)[0]
+
+
+def send_training_state(state: SharedTrainingState, wfile: Optional[IO[str]] = None,
+                        misc: Optional[Dict] = None) -> Dict:
+    """Export ``state`` for another process (ipc_manager.py:54-132).
+
+    Waits for the work queued on the state's device, so the exported memory
+    holds its final values, then returns the payload: the model, the
+    strategy, the granule size, one handle record per granule, and ``misc``
+    (any JSON-serialisable values the caller carries along, as the reference
+    carries its iteration, RNG and scheduler state).  With ``wfile`` it is
+    also written there as one line of JSON, flushed.  The caller keeps the
+    state alive until the importer has released it (:func:`wait_for_release`).
+    """
+    with torch.cuda.device(state.device):
+        torch.cuda.synchronize(state.device)
+    payload = {
+        "format": PAYLOAD_FORMAT,
+        "model_spec": dataclasses.asdict(state.layout.space.spec),
+        "strategy": strategy_to_dict(state.parallel_strategy),
+        "granule_bytes": state.granule_bytes,
+        "buffers": [{"key": list(k), "record": _record_hex(r)} for k, r in zip(state.buffers.keys, state.export())],
+        "misc": misc or {},
+    }
+    if wfile is not None:
+        wfile.write(json.dumps(payload) + "\n")
+        wfile.flush()
+    return payload
+
+
+def receive_training_state(source: Union[Dict, IO[str], str], device=None, space=None
+                           ) -> Tuple[SharedTrainingState, Dict]:
+    """Map an exported state into this process (ipc_manager.py:135-155); returns (state, misc).
+
+    ``source`` is the payload, its JSON text, or a file to read one line of
+    it from.  ``space``: the virtual model to lay the state out in (one is
+    built from the payload's model when None; it must describe the same
+    model).  The layout is rebuilt from the model and the strategy, and every
+    granule's size is checked against it before anything is mapped.
+    """
+    if isinstance(source, dict):
+        payload = source
+    else:
+        text = source if isinstance(source, str) else source.readline()
+        if not text:
+            raise EOFError("no payload: the exporting process sent nothing")
+        payload = json.loads(text)
+    if payload.get("format") != PAYLOAD_FORMAT:
+        raise ValueError(f"not a shared training state payload: {payload.get('format')!r}")
+    from ..resharding.virtual_param import build_virtual_model
+
+    spec = ModelSpec(**payload["model_spec"])
+    if space is None:
+        space = build_virtual_model(spec)
+    elif space.spec != spec:
+        raise ValueError("the payload describes another model than the given virtual model")
+    strategy = ParallelStrategy(**payload["strategy"])
+    layout = space.layout(strategy)
+    bufs = GranuleBuffers(layout, payload["granule_bytes"])
+    recs = [_record_of(b["record"]) for b in payload["buffers"]]
+    if [tuple(b["key"]) for b in payload["buffers"]] != [tuple(k) for k in bufs.keys] or \
+            [int(r["bytes"]) for r in recs] != bufs.nbytes():
+        raise ValueError("the payload's granules do not match the layout rebuilt from its model and strategy")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    ptrs: List[int] = []
+    with torch.cuda.device(dev):
+        try:
+            for r in recs:
+                ptrs.append(_native.ipc_open(r))
+        except Exception:
+            for p in ptrs:
+                _native.ipc_close(p)
+            raise
+    return SharedTrainingState(layout, bufs, ptrs, dev), payload.get("misc", {})
+
+
+def notify_release(wfile: IO[str]) -> None:
+    """Tell the exporting process that this process has closed its mappings."""
+    wfile.write(RELEASED + "\n")
+    wfile.flush()
+
+
+def wait_for_release(rfile: IO[str]) -> bool:
+    """Block until the importer's release notice (True) or the end of the channel (False)."""
+    while True:
+        line = rfile.readline()
+        if not line:
+            return False
+        if line.strip() == RELEASED:
+            return True
+
+
+def _export_main(argv: Sequence[str]) -> int:
+    """An exporting process for a synthetic state: allocate, fill, send on stdout, wait for the
+    release notice on stdin.  Stands in for the old training process of a hand-off."""
+    import argparse
+
+    ap = argparse.ArgumentParser(prog="python -m elasticmegatron_amd.transfer.ipc_manager export")
+    ap.add_argument("--model-spec", required=True, help="ModelSpec fields as JSON")
+    ap.add_argument("--strategy", required=True, help="ParallelStrategy fields as JSON")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--granule-bytes", type=int, default=DEFAULT_GRANULE_BYTES)
+    ap.add_argument("--device", type=int, default=0)
+    ap.add_argument("--misc", default="{}", help="JSON passed through in the payload")
+    args = ap.parse_args(argv)
+    from ..resharding.virtual_param import build_virtual_model
+
+    spec = ModelSpec(**json.loads(args.model_spec))
+    layout = build_virtual_model(spec).layout(ParallelStrategy(**json.loads(args.strategy)))
+    torch.cuda.set_device(args.device)
+    state = SharedTrainingState.allocate(layout, torch.device("cuda", args.device), args.granule_bytes)
+    state.fill_synthetic(args.seed)
+    print(f"[exporter] {len(state.buffers)} granules of {layout.strategy} filled", file=sys.stderr, flush=True)
+    send_training_state(state, sys.stdout, misc=json.loads(args.misc))
+    released = wait_for_release(sys.stdin)
+    print(f"[exporter] {'released' if released else 'channel closed'}; exiting", file=sys.stderr, flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    if len(sys.argv) < 2 or sys.argv[1] != "export":
+        print("usage: python -m elasticmegatron_amd.transfer.ipc_manager export --model-spec JSON "
+              "--strategy JSON [--seed N] [--granule-bytes B]", file=sys.stderr)
+        sys.exit(2)
+    sys.exit(_export_main(sys.argv[2:]))

@@ -27,6 +27,7 @@ from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
 from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, StrategyLayout
 from ..resharding.shares import destination_rank_shares
+from ..resharding.granules import GranuleBuffers
 from ..resharding.tensors import TensorBuffers, rebase_on_tensors
 from .verify import VerifyReport, report_from_stats
 
@@ -95,6 +96,7 @@ class CompiledTensorPlan:
     payload_bytes: int
     read_bytes: int
     buffer_nbytes: list = None   # bytes of every source, then every destination buffer
+    reference_comm_bytes: int = 0
 
     def __post_init__(self):
         if self.buffer_nbytes is None:
@@ -274,6 +276,57 @@ class TransferManager:
             plan.native.execute(ptrs[:ns], ptrs[ns:], st.cuda_stream)
         self._payload_bytes += plan.payload_bytes
 
+    def compile_granules(self, src: StrategyLayout, dst: StrategyLayout, src_granule_bytes: Optional[int],
+                         dst_granule_bytes: Optional[int], kind: str = "transfer",
+                         include_bf16: bool = True) -> CompiledTensorPlan:
+        """The switch between states whose arenas are cut into granules (``SharedTrainingState``,
+        handed between processes; ``None``: whole arenas, a ``TrainingState``).  ``plan.src`` /
+        ``plan.dst`` are the :class:`~..resharding.granules.GranuleBuffers` of each side."""
+        key = ("granules", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
+               self.bf16_source, src_granule_bytes, dst_granule_bytes)
+        cp = self._plans.get(key)
+        if cp is not None:
+            return cp
+        arena_plan = self.compile(src, dst, kind, include_bf16)
+        sb, db = GranuleBuffers(src, src_granule_bytes), GranuleBuffers(dst, dst_granule_bytes)
+        table = rebase_on_tensors(arena_plan.segments, sb, db)
+        cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,
+                                payload_bytes(table), read_bytes(table),
+                                reference_comm_bytes=arena_plan.reference_comm_bytes)
+        self._plans[key] = cp
+        return cp
+
+    def plan_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
+                        dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True):
+        """The arena plan when both sides are whole arenas, else the granule plan."""
+        if src_granule_bytes is None and dst_granule_bytes is None:
+            return self.compile(src_layout, dst_layout, kind, include_bf16)
+        return self.compile_granules(src_layout, dst_layout, src_granule_bytes, dst_granule_bytes, kind,
+                                     include_bf16)
+
+    def execute_states(self, plan, src, dst, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Run ``plan`` (from :meth:`plan_for_states`) between two states of either kind."""
+        if isinstance(plan, CompiledPlan):
+            self.execute(plan, src, dst, stream)
+            return
+        if self.fake_transfer:
+            return
+        if src.layout.strategy != plan.src.layout.strategy or dst.layout.strategy != plan.dst.layout.strategy:
+            raise ValueError("states do not match the plan's strategies")
+        if src.device != dst.device or src.device.type != "cuda":
+            raise RuntimeError("source and destination states must be on one GPU")
+        sp, sn = _buffers_of(src)
+        dp, dn = _buffers_of(dst)
+        for have, need, side in ((sn, plan.src.nbytes(), "source"), (dn, plan.dst.nbytes(), "destination")):
+            if len(have) != len(need) or any(h < n for h, n in zip(have, need)):
+                raise ValueError(f"the {side} state's buffers do not match the plan (released, or laid out "
+                                 "for another granule size)")
+        st = stream if stream is not None else torch.cuda.current_stream(src.device)
+        with torch.cuda.device(src.device):
+            plan.native.execute(sp, dp, st.cuda_stream)
+        self._payload_bytes += plan.payload_bytes
+        self._comm_bytes += plan.reference_comm_bytes
+
     def execute(self, plan: CompiledPlan, src: TrainingState, dst: TrainingState,
                 stream: Optional[torch.cuda.Stream] = None) -> None:
         if self.fake_transfer:
@@ -321,7 +374,9 @@ class TransferManager:
         if src.device.type != "cuda" or dst.device.type != "cuda":
             raise RuntimeError("training states must live in GPU memory: verification has no CPU path")
         sl, dl = src.layout, dst.layout
-        key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source, stage)
+        gs, gd = _granule_of(src), _granule_of(dst)
+        key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source, stage,
+               gs, gd)
         vp = self._verify_plans.get(key)
         if vp is None:
             if kind == "transfer":
@@ -335,15 +390,21 @@ class TransferManager:
             if stage is not None:
                 m = _stage_mask(table, stage)
                 table, groups, aux_groups = table[m], groups[m], aux_groups[m]
-            sb = [sl.fp32_numel * 4] * 3 + [sl.bf16_numel * 2]
-            db = [dl.fp32_numel * 4] * 3 + [dl.bf16_numel * 2]
+            if gs is None and gd is None:
+                sb = [sl.fp32_numel * 4] * 3 + [sl.bf16_numel * 2]
+                db = [dl.fp32_numel * 4] * 3 + [dl.bf16_numel * 2]
+            else:   # granules: the groups follow the segments through the cuts
+                sgb, dgb = GranuleBuffers(sl, gs), GranuleBuffers(dl, gd)
+                table, origin = rebase_on_tensors(table, sgb, dgb, return_origin=True)
+                groups, aux_groups = groups[origin], aux_groups[origin]
+                sb, db = sgb.nbytes(), dgb.nbytes()
             names = [p.name for p in dl.space.all_virtual_params]
             vp = (_native.Plan(table, sb, db), groups, aux_groups, names)
             self._verify_plans[key] = vp
         plan, groups, aux_groups, names = vp
         st = stream if stream is not None else torch.cuda.current_stream(src.device)
         with torch.cuda.device(src.device):
-            stats = plan.compare(src.arena_ptrs(), dst.arena_ptrs(), groups, aux_groups, 4 * len(names),
+            stats = plan.compare(_buffers_of(src)[0], _buffers_of(dst)[0], groups, aux_groups, 4 * len(names),
                                  st.cuda_stream)
         return stats, names
 
@@ -392,6 +453,18 @@ class TransferManager:
         b = self._payload_bytes
         self._payload_bytes = 0
         return b
+
+
+def _granule_of(state) -> Optional[int]:
+    """Granule size of a shared state's arenas; None for a TrainingState's whole arenas."""
+    return None if isinstance(state, TrainingState) else state.granule_bytes
+
+
+def _buffers_of(state):
+    """(base pointers, bytes) of a state's buffers in plan order: arenas or granules."""
+    if isinstance(state, TrainingState):
+        return state.arena_ptrs(), state.arena_bytes()
+    return state.buffer_ptrs(), state.buffer_bytes()
 
 
 def plan_dump(virtual_param_space) -> str:

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define EMRS_ABI_VERSION 7
+#define EMRS_ABI_VERSION 8
 
 #define EMRS_OK 0
 #define EMRS_ERR_INVALID_ARGUMENT (-1)
@@ -59,7 +59,8 @@ extern "C" {
 #define EMRS_ERR_TOO_MANY_BUFFERS (-7)
 #define EMRS_ERR_ALIAS (-8)
 #define EMRS_ERR_CAPTURE (-9) /* the call would allocate or upload while its stream captures a graph */
-#define EMRS_ERR_TOO_LARGE (-10) /* the call needs more than the static scratch of emrs_plan_compare_static */
+#define EMRS_ERR_TOO_LARGE (-10) /* more than the static scratch of emrs_plan_compare_static, or a shared
+                                    allocation of 2 GiB or more (emrs_ipc_*) */
 
 /* Maximum number of source (and, separately, destination) buffers.  Up to
  * 128 per side travel in kernel arguments; a plan with more on either side
@@ -357,6 +358,70 @@ int emrs_synth_verify(const emrs_piece *pieces, uint64_t n_pieces,
  * counterpart in the reference.
  */
 int emrs_xor_checksum(const void *p, uint64_t bytes, uint32_t *out, void *stream);
+
+/*
+ * Inter-process hand-off.
+ *
+ * The reference passes a process's optimizer state to its successor with a
+ * CUDA-IPC handle per tensor storage: _make_cuda_tensor_info packs each
+ * storage's handle, size and offset (elastic_megatron/transfer/ipc_manager.py:23-51,
+ * sent by send_training_state, :54-132) and receive_training_state rebuilds
+ * the tensors from them (:135-155, rebuild_cuda_tensor).  Here the exporting
+ * process holds its state in allocations of less than 2 GiB each, exports
+ * each allocation once, and the importing process opens them and runs the
+ * reshard straight from the mapped memory.
+ *
+ * An emrs_ipc_buffer is plain bytes: it can be written to a file, a pipe or
+ * a socket and read back in another process on the same machine.
+ */
+#define EMRS_IPC_HANDLE_BYTES 64
+#define EMRS_IPC_MAX_ALLOCATION_BYTES (2ull << 30) /* exclusive: allocations must be smaller */
+
+typedef struct emrs_ipc_buffer {
+  uint8_t handle[EMRS_IPC_HANDLE_BYTES]; /* hipIpcMemHandle_t of the allocation holding the buffer */
+  uint64_t offset;           /* bytes from the allocation's base to the buffer (multiple of 16) */
+  uint64_t bytes;            /* bytes of the buffer */
+  uint64_t allocation_bytes; /* bytes of the whole allocation, < EMRS_IPC_MAX_ALLOCATION_BYTES */
+  int32_t device;            /* device ordinal in the exporting process */
+  uint32_t reserved;         /* must be 0 */
+} emrs_ipc_buffer;
+
+/*
+ * Describe the device buffer [ptr, ptr + bytes) for another process: the
+ * handle of the allocation that holds it and the buffer's place in it
+ * (ipc_manager.py:23-51; the same fields as storage._share_cuda_'s handle,
+ * size and offset).  The memory stays owned by the caller, who must keep it
+ * allocated until every importer has closed it.
+ * Errors: INVALID_ARGUMENT (NULL, empty, not device memory), MISALIGNED (ptr
+ * not 16-byte aligned), TOO_LARGE (the allocation is 2 GiB or larger: it is
+ * refused, not split), OUT_OF_BOUNDS, HIP.
+ */
+int emrs_ipc_export(const void *ptr, uint64_t bytes, emrs_ipc_buffer *out);
+
+/*
+ * Map an exported buffer into this process on the current device and return
+ * its address in *ptr (ipc_manager.py:135-155).  Opening several buffers of
+ * one allocation, or one buffer several times, maps the allocation once and
+ * counts references.  The mapped memory is read and written like any device
+ * buffer; pass it to emrs_plan_execute as a source base.  Must be called from
+ * another process than the exporter's.
+ * Errors: INVALID_ARGUMENT, TOO_LARGE (allocation_bytes of 2 GiB or more, or
+ * 0: refused before the driver sees the handle), OUT_OF_BOUNDS, MISALIGNED,
+ * HIP (the handle could not be opened).
+ */
+int emrs_ipc_open(const emrs_ipc_buffer *buf, void **ptr);
+
+/*
+ * Drop one reference that emrs_ipc_open returned; the allocation is unmapped
+ * when its last reference goes.  The caller must first wait for the work
+ * that uses the mapping.
+ * Errors: INVALID_ARGUMENT (not a pointer emrs_ipc_open returned, or already
+ * closed as many times as it was opened), HIP.
+ */
+int emrs_ipc_close(void *ptr);
+
+/* Number of allocations this process holds open through emrs_ipc_open. */
+int emrs_ipc_open_count(void);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,149 @@
+"""Inter-process hand-off on one GPU: a reshard from a state another process exports.
+
+The reference's new process receives the old process's optimizer tensors as
+CUDA-IPC handles (elastic_megatron/transfer/ipc_manager.py:54-155), swaps them
+into its meta-built model and reshards (tools/agent/env_utils.py:326-483).
+Here a child process stands in for the old one: it allocates its state in
+granules of less than 2 GiB, fills it with the seeded values, sends the
+payload on its stdout and waits.  The test process builds its manager on the
+meta device, receives and maps the granules, attaches them, reshards straight
+from the mapped memory into its own state, releases the mappings and only
+then tells the child to exit.
+"""
+
+import dataclasses
+import json
+import os
+import select
+import subprocess
+import sys
+import time
+
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy as PS, _native
+from elasticmegatron_amd.resharding.model_spec import llama2_7b, tiny_llama2
+from elasticmegatron_amd.transfer import ipc_manager as ipc
+from tests.helpers import SEED, compare, extract, strat
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _spawn_exporter(spec, strategy, granule_bytes):
+    cmd = [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_manager", "export",
+           "--model-spec", json.dumps(dataclasses.asdict(spec)),
+           "--strategy", json.dumps(ipc.strategy_to_dict(strategy)),
+           "--seed", str(SEED), "--granule-bytes", str(granule_bytes), "--misc", json.dumps({"iteration": 42})]
+    return subprocess.Popen(cmd, cwd=ROOT, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
+
+
+def _payload_line(child, timeout_s):
+    ready, _, _ = select.select([child.stdout], [], [], timeout_s)
+    if not ready:
+        raise TimeoutError(f"the exporter sent nothing in {timeout_s} s")
+    line = child.stdout.readline()
+    if not line:
+        raise RuntimeError(f"the exporter exited with {child.wait(timeout=30)} before sending")
+    return line
+
+
+def _finish(child, state):
+    """Unmap what is still mapped, then let the exporter free its memory and exit."""
+    if state is not None:
+        state.close()
+    if child.poll() is None:
+        try:
+            ipc.notify_release(child.stdin)
+            child.stdin.close()
+        except BrokenPipeError:
+            pass
+        try:
+            child.wait(timeout=60)
+        except subprocess.TimeoutExpired:
+            child.kill()
+            child.wait()
+    return child.returncode
+
+
+def _host_arenas(state):
+    return [t.view(torch.int32).cpu().numpy().view("uint32") for t in (state.main, state.exp_avg, state.exp_avg_sq)] \
+        + [state.param.view(torch.int16).cpu().numpy().view("uint16")]
+
+
+def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s):
+    """Export in a child, receive, attach and reshard; returns (manager, new state, granules, mapped)."""
+    child = _spawn_exporter(spec, src, granule_bytes)
+    state = None
+    try:
+        mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+        assert mgr.reshard(dst, is_meta_device=True) is None
+        line = _payload_line(child, timeout_s)
+        print(f"  payload received ({len(line)} bytes)", flush=True)
+        state, misc = ipc.receive_training_state(line, gpu_device, space=mgr.virtual_param_space)
+        assert misc == {"iteration": 42}
+        n_granules, n_mapped = len(state.buffers), _native.ipc_open_count()
+        assert 0 < n_mapped <= n_granules
+        bad, first = state.verify_synthetic(SEED)     # the mapped memory holds the exporter's values
+        assert bad == 0, first
+        mgr.attach_training_state(state)
+        assert mgr.reshard(dst, is_meta_device=True) is None    # plan and tables for the granules
+        new = mgr.reshard(dst, verify=True)
+        torch.cuda.synchronize()
+        assert mgr.last_verification.bit_exact
+        assert _native.ipc_open_count() == 0          # the switch released the mappings
+        state = None
+        return mgr, new, n_granules, n_mapped
+    finally:
+        rc = _finish(child, state)
+        print(f"  exporter exit status {rc}", flush=True)
+    # (unreachable)
+
+
+def test_export_refuses_allocations_of_2gib_or_more(gpu_device):
+    big = torch.empty((2 << 30) + (2 << 20), dtype=torch.uint8, device=gpu_device)
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_export(big.data_ptr(), 4096)
+    assert e.value.code == -10
+    with pytest.raises(_native.EmrsError):
+        _native.ipc_export(big.data_ptr() + (1 << 30), 4096)   # any buffer inside it
+    del big
+    torch.cuda.empty_cache()
+    ok = torch.empty(1 << 30, dtype=torch.uint8, device=gpu_device)
+    rec = _native.ipc_export(ok.data_ptr() + 4096, 8192)
+    assert int(rec["bytes"]) == 8192 and int(rec["allocation_bytes"]) < (2 << 30)
+    assert int(rec["offset"]) >= 4096 and int(rec["device"]) == gpu_device.index
+
+
+def test_hand_off_tiny_matches_oracle1(gpu_device):
+    """Config 1's first switch (TP2 DP4 -> TP1 DP8) from another process's granules, bit-exact against
+    Oracle-1 on every parameter; granules of about 12 MiB, an odd multiple of 256 bytes, so that
+    boundaries fall inside segments."""
+    from oracle import model
+    from oracle import transfer as oracle1
+
+    spec, src, dst = tiny_llama2(), PS(8, 2, 1), PS(8, 1, 1)
+    print(f"case hand-off {spec.name} {src} -> {dst}", flush=True)
+    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, spec, src, dst, 3 * (1 << 22) + 256 * 7, 240)
+    print(f"  {n_granules} granules in {n_mapped} allocations; switch {mgr.last_transfer_ms:.3f} ms", flush=True)
+    assert new.verify_synthetic(SEED)[0] == 0
+    inv = model.inventory(spec)
+    world = oracle1.build_src_world(inv, spec, strat(src), SEED)
+    dw, dbf, _ = oracle1.transfer(inv, spec, strat(src), strat(dst), world)
+    got32, gotbf = extract(new.layout, _host_arenas(new))
+    assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []
+
+
+def test_hand_off_llama2_7b(gpu_device):
+    """Config 2 (Llama-2-7B TP1 DP8 -> TP4 DP2) from 1 GiB granules of another process: checked on
+    the device against the mapped source (emrs_plan_compare) and against the generator."""
+    spec, src, dst = llama2_7b(), PS(8, 1, 1), PS(8, 4, 1)
+    print(f"case hand-off {spec.name} {src} -> {dst}", flush=True)
+    t0 = time.perf_counter()
+    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, spec, src, dst, 1 << 30, 600)
+    gb = new.layout.payload_numel * 14 / 1e9
+    print(f"  {n_granules} granules; switch {mgr.last_transfer_ms:.2f} ms "
+          f"({gb / mgr.last_transfer_ms:.1f} TB/s payload); {time.perf_counter() - t0:.0f} s in all", flush=True)
+    bad, first = new.verify_synthetic(SEED)
+    assert bad == 0, first

@@ -1,0 +1,177 @@
+"""Inter-process hand-off: host-side checks that need no GPU.
+
+The reference exports one CUDA-IPC handle per optimizer tensor storage and
+rebuilds the tensors in the new process (elastic_megatron/transfer/ipc_manager.py:23-155).
+Here a state is exported as granules of less than 2 GiB.  These tests cover
+the payload's encoding, the checks made before any handle reaches the driver,
+and planning a switch from a received state on the meta device; the hand-off
+itself runs on the GPU (tests/test_gpu_ipc.py).
+"""
+
+import ctypes
+import dataclasses
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy as PS, _native
+from elasticmegatron_amd.resharding.granules import GranuleBuffers
+from elasticmegatron_amd.resharding.model_spec import ModelSpec, llama2_7b, tiny_llama2
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from elasticmegatron_amd.transfer import ipc_manager as ipc
+from elasticmegatron_amd.transfer.transfer import CompiledTensorPlan
+from tests.helpers import small_llama2
+
+
+def _record(**kw):
+    rec = np.zeros(1, dtype=_native.IPC_BUFFER_DTYPE)
+    rec["handle"] = np.arange(64, dtype=np.uint8)
+    for k, v in kw.items():
+        rec[k] = v
+    return rec[0]
+
+
+def test_record_layout_matches_the_header():
+    lib = _native.load()
+    assert _native.IPC_BUFFER_DTYPE.itemsize == 96
+    assert [n for n in _native.IPC_BUFFER_DTYPE.names] == ["handle", "offset", "bytes", "allocation_bytes",
+                                                          "device", "reserved"]
+    assert lib.emrs_ipc_open_count() == 0
+
+
+def test_record_round_trips_through_text():
+    rec = _record(offset=4096, bytes=1 << 20, allocation_bytes=1 << 30, device=3)
+    back = ipc._record_of(ipc._record_hex(rec))
+    assert back.tobytes() == np.asarray(rec).tobytes()
+    with pytest.raises(ValueError):
+        ipc._record_of("00" * 95)
+
+
+@pytest.mark.parametrize("alloc", [2 << 30, (2 << 30) + 4096, 0])
+def test_open_refuses_allocations_of_2gib_or_more_before_the_driver(alloc):
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_open(_record(offset=0, bytes=256, allocation_bytes=alloc))
+    assert e.value.code == -10   # EMRS_ERR_TOO_LARGE
+    assert _native.ipc_open_count() == 0
+
+
+def test_open_checks_the_record():
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_open(_record(offset=0, bytes=256, allocation_bytes=4096, reserved=1))
+    assert e.value.code == -1
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_open(_record(offset=4000, bytes=256, allocation_bytes=4096))
+    assert e.value.code == -2    # runs past its allocation
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_open(_record(offset=8, bytes=256, allocation_bytes=4096))
+    assert e.value.code == -3    # not 16-byte aligned
+
+
+def test_close_and_export_refuse_unknown_pointers():
+    with pytest.raises(_native.EmrsError) as e:
+        _native.ipc_close(0x1000)
+    assert e.value.code == -1
+    lib = _native.load()
+    rec = np.zeros(1, dtype=_native.IPC_BUFFER_DTYPE)
+    assert lib.emrs_ipc_export(None, 256, rec.ctypes.data) == -1
+    assert lib.emrs_ipc_export(ctypes.c_void_p(0x1008), 256, rec.ctypes.data) == -3
+
+
+def test_strategy_and_model_round_trip():
+    for s in (PS(8, 2, 1), PS(8, 1, 2, context_parallel_size=2), PS(12, 1, 1, num_distributed_optimizer_instances=2),
+              PS(8, 1, 1, expert_model_parallel_size=4)):
+        d = json.loads(json.dumps(ipc.strategy_to_dict(s)))
+        back = PS(**d)
+        assert back == s and back.sequence_parallel == s.sequence_parallel
+    spec = llama2_7b()
+    assert ModelSpec(**json.loads(json.dumps(dataclasses.asdict(spec)))) == spec
+
+
+def _payload(spec, strategy, granule):
+    layout = build_virtual_model(spec).layout(strategy)
+    bufs = GranuleBuffers(layout, granule)
+    return {"format": ipc.PAYLOAD_FORMAT, "model_spec": dataclasses.asdict(spec),
+            "strategy": ipc.strategy_to_dict(strategy), "granule_bytes": granule,
+            "buffers": [{"key": list(k), "record": ipc._record_hex(_record(offset=0, bytes=n, allocation_bytes=n))}
+                        for k, n in zip(bufs.keys, bufs.nbytes())], "misc": {"iteration": 7}}
+
+
+def test_receive_validates_before_mapping():
+    spec = small_llama2()
+    p = _payload(spec, PS(8, 2, 1), 1 << 16)
+    bad = dict(p, format="something-else")
+    with pytest.raises(ValueError):
+        ipc.receive_training_state(bad, device="cpu")
+    short = dict(p, buffers=p["buffers"][:-1])
+    with pytest.raises(ValueError):
+        ipc.receive_training_state(short, device="cpu")
+    other = dict(p, granule_bytes=1 << 15)
+    with pytest.raises(ValueError):
+        ipc.receive_training_state(other, device="cpu")
+    with pytest.raises(ValueError):
+        ipc.receive_training_state(p, device="cpu", space=build_virtual_model(tiny_llama2()))
+    with pytest.raises(EOFError):
+        ipc.receive_training_state(__import__("io").StringIO(""), device="cpu")
+    assert _native.ipc_open_count() == 0
+
+
+def test_release_notice_round_trip():
+    import io
+
+    buf = io.StringIO()
+    ipc.notify_release(buf)
+    assert ipc.wait_for_release(io.StringIO("noise\n" + buf.getvalue())) is True
+    assert ipc.wait_for_release(io.StringIO("")) is False
+
+
+def _fake_shared(layout, granule):
+    """A received state's description without mappings (host-side planning only)."""
+    bufs = GranuleBuffers(layout, granule)
+    return ipc.SharedTrainingState(layout, bufs, [0x10000 * (i + 1) for i in range(len(bufs))], torch.device("cpu"))
+
+
+def test_meta_manager_plans_then_attaches_a_received_state():
+    """The reference's new process: build on meta, pre-build the switch, swap the received state in
+    (tools/agent/env_utils.py:326-456).  Planning runs on the host; the launch needs a GPU."""
+    spec = small_llama2()
+    src, dst = PS(8, 2, 1), PS(8, 4, 1)
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+    assert mgr.training_state.device.type == "meta"
+    assert mgr.reshard(dst, is_meta_device=True) is None
+    state = _fake_shared(mgr.virtual_param_space.layout(src), 1 << 16)
+    with pytest.raises(ValueError):
+        mgr.attach_training_state(_fake_shared(mgr.virtual_param_space.layout(dst), 1 << 16))
+    mgr.attach_training_state(state)
+    assert mgr.training_state is state
+    assert mgr.reshard(dst, is_meta_device=True) is None   # plans the granule switch
+    plans = [p for k, p in mgr.transfer_manager._plans.items() if k[0] == "granules"]
+    assert len(plans) == 1 and isinstance(plans[0], CompiledTensorPlan)
+    assert len(plans[0].src) == len(state.buffers)
+
+
+def test_attach_adopts_a_separately_built_model():
+    spec = small_llama2()
+    src, dst = PS(8, 1, 1), PS(6, 1, 1)
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+    other_space = build_virtual_model(spec)
+    state = _fake_shared(other_space.layout(src), 1 << 18)
+    mgr.attach_training_state(state)
+    assert mgr.virtual_param_space is other_space
+    assert mgr.reshard(dst, is_meta_device=True) is None
+
+
+def test_group_zero_from_a_received_state_is_refused():
+    spec = small_llama2()
+    src, dst = PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+    mgr.attach_training_state(_fake_shared(mgr.virtual_param_space.layout(src), 1 << 16))
+    with pytest.raises(NotImplementedError):
+        mgr.reshard(dst)
+
+
+def test_low_memory_refuses_shared_states():
+    with pytest.raises(NotImplementedError):
+        ElasticMegatronManager([PS(8, 1, 1)], small_llama2(), device="meta", low_memory=True,
+                               share_granule_bytes=1 << 20)

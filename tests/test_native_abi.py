@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol():
     assert set(declared) == set(_native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.emrs_abi_version() == 7
+    assert lib.emrs_abi_version() == 8
 
 
 def test_record_layouts_match_header():
