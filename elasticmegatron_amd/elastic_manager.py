@@ -68,7 +68,7 @@ class ElasticMegatronManager:
         ``training_state`` should be allocated with ``granule_bytes=ARENA_GRANULE_BYTES`` too).
 
         ``share_granule_bytes``: the states this manager allocates are
-        :class:`~.transfer.ipc_manager.SharedTrainingState`\ s with granules of that size, so that the
+        :class:`~.transfer.ipc_manager.SharedTrainingState` objects with granules of that size, so that the
         live state can be handed to another process at any time (``send_training_state``).  A
         ``training_state`` passed in may be one as well, for instance one just received from the
         process that held it (``receive_training_state``).  ``device="meta"`` allocates nothing: the

@@ -1,0 +1,53 @@
+"""An exporting process for a synthetic training state.
+
+    python -m elasticmegatron_amd.transfer.ipc_export --model-spec JSON --strategy JSON [--seed N]
+        [--granule-bytes B] [--device D] [--misc JSON]
+
+Stands in for the old training process of a hand-off (the reference's
+send_training_state, elastic_megatron/transfer/ipc_manager.py:54-132): it
+allocates a :class:`~.ipc_manager.SharedTrainingState`, fills it with the
+seeded synthetic values, writes the payload as one line on stdout, and keeps
+the memory until a release notice arrives on stdin (or stdin closes).
+"""
+
+import json
+import sys
+from typing import Sequence
+
+import torch
+
+from ..megatron_manager.parallel_strategy import ParallelStrategy
+from ..resharding.granules import DEFAULT_GRANULE_BYTES
+from ..resharding.model_spec import ModelSpec
+from ..resharding.virtual_param import build_virtual_model
+from .ipc_manager import SharedTrainingState, send_training_state, wait_for_release
+
+
+def main(argv: Sequence[str]) -> int:
+    """An exporting process for a synthetic state: allocate, fill, send on stdout, wait for the
+    release notice on stdin.  Stands in for the old training process of a hand-off."""
+    import argparse
+
+    ap = argparse.ArgumentParser(prog="python -m elasticmegatron_amd.transfer.ipc_export")
+    ap.add_argument("--model-spec", required=True, help="ModelSpec fields as JSON")
+    ap.add_argument("--strategy", required=True, help="ParallelStrategy fields as JSON")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--granule-bytes", type=int, default=DEFAULT_GRANULE_BYTES)
+    ap.add_argument("--device", type=int, default=0)
+    ap.add_argument("--misc", default="{}", help="JSON passed through in the payload")
+    args = ap.parse_args(argv)
+
+    spec = ModelSpec(**json.loads(args.model_spec))
+    layout = build_virtual_model(spec).layout(ParallelStrategy(**json.loads(args.strategy)))
+    torch.cuda.set_device(args.device)
+    state = SharedTrainingState.allocate(layout, torch.device("cuda", args.device), args.granule_bytes)
+    state.fill_synthetic(args.seed)
+    print(f"[exporter] {len(state.buffers)} granules of {layout.strategy} filled", file=sys.stderr, flush=True)
+    send_training_state(state, sys.stdout, misc=json.loads(args.misc))
+    released = wait_for_release(sys.stdin)
+    print(f"[exporter] {'released' if released else 'channel closed'}; exiting", file=sys.stderr, flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

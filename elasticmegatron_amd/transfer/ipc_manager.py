@@ -30,7 +30,6 @@ from __future__ import annotations
 
 import dataclasses
 import json
-import sys
 from typing import IO, Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
@@ -298,38 +297,3 @@ def wait_for_release(rfile: IO[str]) -> bool:
             return False
         if line.strip() == RELEASED:
             return True
-
-
-def _export_main(argv: Sequence[str]) -> int:
-    """An exporting process for a synthetic state: allocate, fill, send on stdout, wait for the
-    release notice on stdin.  Stands in for the old training process of a hand-off."""
-    import argparse
-
-    ap = argparse.ArgumentParser(prog="python -m elasticmegatron_amd.transfer.ipc_manager export")
-    ap.add_argument("--model-spec", required=True, help="ModelSpec fields as JSON")
-    ap.add_argument("--strategy", required=True, help="ParallelStrategy fields as JSON")
-    ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--granule-bytes", type=int, default=DEFAULT_GRANULE_BYTES)
-    ap.add_argument("--device", type=int, default=0)
-    ap.add_argument("--misc", default="{}", help="JSON passed through in the payload")
-    args = ap.parse_args(argv)
-    from ..resharding.virtual_param import build_virtual_model
-
-    spec = ModelSpec(**json.loads(args.model_spec))
-    layout = build_virtual_model(spec).layout(ParallelStrategy(**json.loads(args.strategy)))
-    torch.cuda.set_device(args.device)
-    state = SharedTrainingState.allocate(layout, torch.device("cuda", args.device), args.granule_bytes)
-    state.fill_synthetic(args.seed)
-    print(f"[exporter] {len(state.buffers)} granules of {layout.strategy} filled", file=sys.stderr, flush=True)
-    send_training_state(state, sys.stdout, misc=json.loads(args.misc))
-    released = wait_for_release(sys.stdin)
-    print(f"[exporter] {'released' if released else 'channel closed'}; exiting", file=sys.stderr, flush=True)
-    return 0
-
-
-if __name__ == "__main__":
-    if len(sys.argv) < 2 or sys.argv[1] != "export":
-        print("usage: python -m elasticmegatron_amd.transfer.ipc_manager export --model-spec JSON "
-              "--strategy JSON [--seed N] [--granule-bytes B]", file=sys.stderr)
-        sys.exit(2)
-    sys.exit(_export_main(sys.argv[2:]))

@@ -32,7 +32,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _spawn_exporter(spec, strategy, granule_bytes):
-    cmd = [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_manager", "export",
+    cmd = [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_export",
            "--model-spec", json.dumps(dataclasses.asdict(spec)),
            "--strategy", json.dumps(ipc.strategy_to_dict(strategy)),
            "--seed", str(SEED), "--granule-bytes", str(granule_bytes), "--misc", json.dumps({"iteration": 42})]
@@ -98,7 +98,6 @@ def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s):
     finally:
         rc = _finish(child, state)
         print(f"  exporter exit status {rc}", flush=True)
-    # (unreachable)
 
 
 def test_export_refuses_allocations_of_2gib_or_more(gpu_device):
