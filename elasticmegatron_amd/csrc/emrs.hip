@@ -806,9 +806,85 @@ struct emrs_plan {
   // (units from abs_base, the lowest referenced base), per device.
   std::vector<DevSeg *> abs_tables;
   std::vector<uint64_t> abs_base;
+  // Per device: one event recorded after each launch that may still be running (an event is
+  // reused once its launch has finished).  Destroying the plan frees its tables in stream order
+  // after these launches, and waits for nothing else.
+  std::vector<std::vector<hipEvent_t>> launch_events;
+  bool captured = false;  // a launch was recorded into a graph: destroy drains the device first
 };
 
 namespace {
+
+// The plan's own device tables are stream-ordered allocations: made and
+// filled synchronously on first use, and freed by emrs_plan_destroy on a
+// library stream once the plan's launches have finished.
+hipError_t table_alloc(void **out, size_t bytes, hipStream_t st) {
+  *out = nullptr;
+  const hipError_t e = hipMallocAsync(out, bytes, st);
+  if (e != hipSuccess) *out = nullptr;
+  return e;
+}
+
+int table_upload(void **out, const void *host, size_t bytes, hipStream_t st, const char *what) {
+  hipError_t e = table_alloc(out, bytes, st);
+  if (e != hipSuccess) return hip_fail(e, what);
+  e = hipMemcpyAsync(*out, host, bytes, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);  // complete before any stream may read it
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(*out, st);
+    (void)hipStreamSynchronize(st);
+    *out = nullptr;
+    return hip_fail(e, what);
+  }
+  return EMRS_OK;
+}
+
+// Per device, the library's own stream on which destroyed plans free their
+// tables (default priority, not blocking the null stream); nullptr if it
+// could not be made.
+hipStream_t free_stream(int dev) {
+  static std::mutex mu;
+  static std::vector<hipStream_t> streams;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)streams.size() <= dev) streams.resize(dev + 1, nullptr);
+  if (!streams[dev]) {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess) streams[dev] = s;
+    else (void)hipGetLastError();
+  }
+  return streams[dev];
+}
+
+// Record that the plan's tables are in use by the work just enqueued on `st`.
+// Under graph capture nothing is recorded: the graph may replay any time, so
+// destroy then drains the device instead.
+int note_launch(emrs_plan *plan, int dev, hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  std::lock_guard<std::mutex> lk(plan->mu);
+  if (cs != hipStreamCaptureStatusNone) {
+    plan->captured = true;
+    return EMRS_OK;
+  }
+  if ((int)plan->launch_events.size() <= dev) plan->launch_events.resize(dev + 1);
+  std::vector<hipEvent_t> &evs = plan->launch_events[dev];
+  hipEvent_t ev = nullptr;
+  for (hipEvent_t x : evs)
+    if (hipEventQuery(x) == hipSuccess) {  // its launch has finished: reuse it
+      ev = x;
+      break;
+    }
+  (void)hipGetLastError();  // hipEventQuery reports hipErrorNotReady for the running ones
+  if (!ev) {
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags");
+    evs.push_back(ev);
+  }
+  e = hipEventRecord(ev, st);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+  return EMRS_OK;
+}
 
 // Second destination of a segment: its bf16 image (cast; offsets in units
 // of half the segment's unit) or a duplicate (dup; offsets in the segment's
@@ -1045,13 +1121,8 @@ int pointer_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_t
     } else {
       if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
       uint64_t *t = nullptr;
-      hipError_t e = hipMalloc(reinterpret_cast<void **>(&t), bytes);
-      if (e != hipSuccess) return hip_fail(e, "hipMalloc(pointer table)");
-      e = hipMemcpy(t, rb.ptrs.data(), bytes, hipMemcpyHostToDevice);
-      if (e != hipSuccess) {
-        (void)hipFree(t);
-        return hip_fail(e, "hipMemcpy(pointer table)");
-      }
+      if (int rc = table_upload(reinterpret_cast<void **>(&t), rb.ptrs.data(), bytes, st, "uploading the pointer table"))
+        return rc;
       plan->ptr_tables[dev] = t;
       plan->ptr_contents[dev] = rb.ptrs;
       *out = t;
@@ -1115,13 +1186,8 @@ int resolved_table(emrs_plan *plan, int dev, const ResolvedBases &rb, hipStream_
     }
     const size_t bytes = segs.size() * sizeof(DevSeg);
     DevSeg *t = nullptr;
-    hipError_t e = hipMalloc(&t, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(resolved plan table)");
-    e = hipMemcpy(t, segs.data(), bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      (void)hipFree(t);
-      return hip_fail(e, "hipMemcpy(resolved plan table)");
-    }
+    if (int rc = table_upload(reinterpret_cast<void **>(&t), segs.data(), bytes, st, "uploading the resolved plan table"))
+      return rc;
     plan->abs_tables[dev] = t;
     plan->abs_base[dev] = lo;
   }
@@ -1136,11 +1202,20 @@ int chunk_table(emrs_plan *plan, int dev, hipStream_t st, const DevSeg *segs, ui
   std::lock_guard<std::mutex> lk(plan->mu);
   if ((int)plan->chunk_tables.size() <= dev) plan->chunk_tables.resize(dev + 1, nullptr);
   if (!plan->chunk_tables[dev]) {
-    if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
+    // The table only spares each workgroup its search.  While the stream captures a graph it
+    // cannot be built (that would record an allocation), so the launch searches instead; a
+    // later call outside a capture builds it.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t ce = hipStreamIsCapturing(st, &cs);
+    if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone) {
+      *out = nullptr;
+      return EMRS_OK;
+    }
     if (plan->segs.size() > 0xffffffffull) return fail(EMRS_ERR_INVALID_ARGUMENT, "too many device segments");
     const size_t bytes = plan->n_chunks * sizeof(uint32_t);
     uint32_t *t = nullptr;
-    hipError_t e = hipMalloc(&t, bytes);
+    hipError_t e = table_alloc(reinterpret_cast<void **>(&t), bytes, st);
     if (e == hipErrorOutOfMemory) {
       // The table only spares each workgroup its search: with no room for it,
       // this launch searches instead, and the next call tries again.
@@ -1148,7 +1223,7 @@ int chunk_table(emrs_plan *plan, int dev, hipStream_t st, const DevSeg *segs, ui
       *out = nullptr;
       return EMRS_OK;
     }
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(chunk table)");
+    if (e != hipSuccess) return hip_fail(e, "hipMallocAsync(chunk table)");
     const uint32_t nseg = (uint32_t)plan->segs.size();
     hipLaunchKernelGGL(fill_chunk_table_kernel, dim3(std::min<uint32_t>(nseg, 65535)), dim3(256), 0, st, segs, nseg,
                        plan->n_chunks, t);
@@ -1156,7 +1231,8 @@ int chunk_table(emrs_plan *plan, int dev, hipStream_t st, const DevSeg *segs, ui
     // Later calls may come on other streams: the table is complete before it is published.
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) {
-      (void)hipFree(t);
+      (void)hipFreeAsync(t, st);
+      (void)hipStreamSynchronize(st);
       return hip_fail(e, "building the chunk table");
     }
     plan->chunk_tables[dev] = t;
@@ -1173,13 +1249,8 @@ int device_table(emrs_plan *plan, int dev, hipStream_t st, DevSeg **table) {
     if (int rc = refuse_capture(st, "the first call of a plan on a device")) return rc;
     const size_t bytes = plan->segs.size() * sizeof(DevSeg);
     DevSeg *t = nullptr;
-    hipError_t e = hipMalloc(&t, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(plan table)");
-    e = hipMemcpy(t, plan->segs.data(), bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      (void)hipFree(t);
-      return hip_fail(e, "hipMemcpy(plan table)");
-    }
+    if (int rc = table_upload(reinterpret_cast<void **>(&t), plan->segs.data(), bytes, st, "uploading the plan table"))
+      return rc;
     plan->dev_tables[dev] = t;
   }
   *table = plan->dev_tables[dev];
@@ -1762,6 +1833,7 @@ int emrs_plan_prepare(emrs_plan *plan, void *stream) {
   int rc = current_device(&dev, &cus, &resident_nt, &resident_t);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((rc = refuse_capture(st, "emrs_plan_prepare"))) return rc;
   DevSeg *table = nullptr;
   rc = device_table(plan, dev, st, &table);
   if (rc) return rc;
@@ -1843,7 +1915,7 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
     hipError_t le = hipGetLastError();
     if (tab_owned) (void)hipFreeAsync(tab, st);
     if (le != hipSuccess) return hip_fail(le, "copy_plan_kernel launch");
-    return EMRS_OK;
+    return note_launch(plan, dev, st);
   }
 
   // Persistent grid.  A run of N counts N steps of kUnroll chunks.
@@ -1883,7 +1955,7 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases, void *const *dst_
   hipError_t le = hipGetLastError();
   if (tab_owned) (void)hipFreeAsync(tab, st);
   if (le != hipSuccess) return hip_fail(le, "copy_plan_persistent_kernel launch");
-  return EMRS_OK;
+  return note_launch(plan, dev, st);
 }
 
 int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
@@ -1994,21 +2066,29 @@ int emrs_plan_destroy(emrs_plan *plan) {
   int prev = 0;
   (void)hipGetDevice(&prev);
   const size_t n_dev = std::max({plan->dev_tables.size(), plan->ptr_tables.size(), plan->abs_tables.size(),
-                                  plan->chunk_tables.size()});
+                                  plan->chunk_tables.size(), plan->launch_events.size()});
   for (size_t d = 0; d < n_dev; ++d) {
     DevSeg *segs = d < plan->dev_tables.size() ? plan->dev_tables[d] : nullptr;
     uint64_t *ptrs = d < plan->ptr_tables.size() ? plan->ptr_tables[d] : nullptr;
     DevSeg *abs = d < plan->abs_tables.size() ? plan->abs_tables[d] : nullptr;
     uint32_t *chunks = d < plan->chunk_tables.size() ? plan->chunk_tables[d] : nullptr;
-    if (segs || ptrs || abs || chunks) {
-      (void)hipSetDevice((int)d);
-      // Launches enqueued on any stream may still read the tables.
+    std::vector<hipEvent_t> evs = d < plan->launch_events.size() ? plan->launch_events[d] : std::vector<hipEvent_t>();
+    if (!(segs || ptrs || abs || chunks || !evs.empty())) continue;
+    (void)hipSetDevice((int)d);
+    // A graph may replay the plan's launches at any time: only a drained device is safe.
+    if (plan->captured) (void)hipDeviceSynchronize();
+    // The tables are freed on the library's stream after the launches that read them, and only
+    // after those: work on other streams is not waited for, and the host does not block.
+    hipStream_t fs = free_stream((int)d);
+    if (!fs) {
       (void)hipDeviceSynchronize();
-      if (segs) (void)hipFree(segs);
-      if (ptrs) (void)hipFree(ptrs);
-      if (abs) (void)hipFree(abs);
-      if (chunks) (void)hipFree(chunks);
+    } else {
+      for (hipEvent_t ev : evs) (void)hipStreamWaitEvent(fs, ev, 0);
     }
+    for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
+    for (void *t : {static_cast<void *>(segs), static_cast<void *>(ptrs), static_cast<void *>(abs),
+                    static_cast<void *>(chunks)})
+      if (t) (void)hipFreeAsync(t, fs);
   }
   (void)hipSetDevice(prev);
   delete plan;

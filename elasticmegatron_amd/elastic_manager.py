@@ -159,14 +159,19 @@ class ElasticMegatronManager:
     def parallel_strategy(self) -> ParallelStrategy:
         return self.training_state.parallel_strategy
 
+    def _prepare(self, plan, state) -> None:
+        """The meta-device pass's upload of a plan's tables, on the state's GPU (none elsewhere)."""
+        if state.device.type == "cuda":
+            self.transfer_manager.prepare(plan, state.device)
+
     def transfer_params(self, src: TrainingState, dst: TrainingState, union_world_group=None,
                         is_meta_device: bool = False) -> float:
         """Plan (cached) and move the state; returns the executor's time in ms.
 
         The arguments keep the reference's order (elastic_manager.py:106-122).  One process holds
         every rank's state, so ``union_world_group`` is accepted and unused; ``is_meta_device``
-        plans and caches without moving data, as the reference's fake transfer does
-        (elastic_manager.py:115-117, 282-285).
+        plans, caches and uploads the plan's tables to the state's GPU without moving data, as the
+        reference's fake transfer builds its connections (elastic_manager.py:115-117, 282-285).
         """
         space = src.layout.space
         if space is dst.layout.space:
@@ -174,11 +179,15 @@ class ElasticMegatronManager:
         gs, gd = _granule_of(src), _granule_of(dst)
         if gs is not None or gd is not None:   # shared granules: the re-based plan
             plan = self.transfer_manager.compile_granules(src.layout, dst.layout, gs, gd)
+            if is_meta_device:
+                self._prepare(plan, src)
             with Timer() as t:
                 if not is_meta_device:
                     self.transfer_manager.execute_states(plan, src, dst)
             return t.elapsed
         plan = self.transfer_manager.compile(src.layout, dst.layout)
+        if is_meta_device:
+            self._prepare(plan, src)
         # The states are the space's for the duration of the transfer only: the space outlives the
         # switch, and holding them would keep a released state's memory alive.
         space.src_state, space.dst_state = src, dst
@@ -229,9 +238,12 @@ class ElasticMegatronManager:
     def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool,
                          is_meta_device: bool = False) -> float:
         """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
-        ``is_meta_device`` plans and caches without moving data.  Returns the executor's ms."""
+        ``is_meta_device`` plans, caches and uploads the plan's tables without moving data.  Returns
+        the executor's ms."""
         plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst),
                                                      "backup_up" if is_scale_up else "backup_down")
+        if is_meta_device:
+            self._prepare(plan, src)
         with Timer() as t:
             if not is_meta_device:
                 self.transfer_manager.execute_states(plan, src, dst)
@@ -315,8 +327,7 @@ class ElasticMegatronManager:
         plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind)
         stages = self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind) if self.low_memory else ()
         if is_meta_device:
-            if src_state.device.type == "cuda":
-                self.transfer_manager.prepare(stages or plan, src_state.device)
+            self._prepare(stages or plan, src_state)
             return None
         # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over.
         param = None

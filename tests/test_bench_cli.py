@@ -121,3 +121,18 @@ def test_cpu_baseline_covers_every_parameter(src, dst):
                                         "transfer" if dst.num_distributed_optimizer_instances == 1
                                         else "backup_up").payload_bytes
     assert f"{payload / 1e9:.1f} GB payload" in out["sample"]
+
+
+def test_each_line_names_its_own_workload():
+    """The headline metric belongs to the headline switch only; every other workload's line names its
+    own switch, so that a line quoted on its own says what it measured."""
+    assert bench.metric_for(bench.HEADLINE, bench.workloads()[bench.HEADLINE][0]) == bench.METRIC
+    seen = set()
+    for name, (desc, *_) in bench.workloads().items():
+        m = bench.metric_for(name, desc)
+        if name != bench.HEADLINE:
+            assert m != bench.METRIC and desc in m and m.endswith("1 GPU"), name
+        seen.add(m)
+    assert len(seen) == len(bench.workloads())
+    gz = bench.metric_for("llama2-7b-groupzero-1-2", bench.workloads()["llama2-7b-groupzero-1-2"][0])
+    assert "Group ZeRO" in gz and "TP1DP8" not in gz

@@ -386,6 +386,36 @@ def test_destroy_right_after_execute(gpu_device):
         assert torch.equal(dst, src)
 
 
+def test_destroy_waits_only_for_its_own_launches(gpu_device):
+    """Destroying a plan frees its tables after its own launches and does not wait for other work:
+    a long queue of copies on another stream is still running when destroy returns."""
+    n = 1 << 24
+    src = torch.arange(n, dtype=torch.int32, device=gpu_device)
+    dst = torch.zeros(n, dtype=torch.int32, device=gpu_device)
+    big_a = torch.full((1 << 28,), 7, dtype=torch.int32, device=gpu_device)    # 1 GiB each
+    big_b = torch.empty_like(big_a)
+    side, other = torch.cuda.Stream(device=gpu_device), torch.cuda.Stream(device=gpu_device)
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0, 0, 0, 0, 0)
+    plan = _native.Plan(t, [n * 4], [n * 4])
+    plan.execute([src.data_ptr()], [dst.data_ptr()], side.cuda_stream)    # uploads the tables
+    torch.cuda.synchronize()
+    dst.zero_()
+    torch.cuda.synchronize()
+    done = torch.cuda.Event()
+    with torch.cuda.stream(other):
+        for i in range(120):                     # about 40 ms of copies
+            (big_b if i % 2 == 0 else big_a).copy_(big_a if i % 2 == 0 else big_b)
+        done.record(other)
+    plan.execute([src.data_ptr()], [dst.data_ptr()], side.cuda_stream)
+    plan.close()
+    assert not done.query(), "destroy waited for another stream's work"
+    side.synchronize()
+    assert torch.equal(dst, src)
+    other.synchronize()
+    assert bool((big_b == 7).all())
+
+
 def test_manager_sequence(gpu_device):
     """ElasticMegatronManager.reshard through the tiny TP2DP4 -> TP1DP8 -> TP4DP2 sequence."""
     from elasticmegatron_amd import ElasticMegatronManager, tiny_llama2

@@ -103,3 +103,92 @@ def test_prepared_per_tensor_plan(gpu_device):
     tm.execute_tensors(plan, plan.src.views(a), plan.dst.views(b))
     torch.cuda.synchronize()
     assert b.verify_synthetic(SEED)[0] == 0
+
+
+def _capture_first_execute(tm, plan, a, b, gpu_device):
+    """Capture the plan's first execution after a meta pass and replay it bit-exact, with eager work
+    on the destination between replays."""
+    _scramble(b)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tm.execute(plan, a, b)
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] > 0   # captured, not run
+    for r in range(3):
+        _scramble(b)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert b.verify_synthetic(SEED)[0] == 0, r
+
+
+def test_capture_after_the_chunk_table_was_turned_on(gpu_device):
+    """Prepared with the chunk table off, then turned on: the captured first execution finds its
+    segments by search (the table cannot be built under capture) and replays bit-exact."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 1))
+    a = TrainingState.allocate(ls, gpu_device)
+    b = TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    tm = TransferManager()
+    other = space.layout(PS(8, 4, 1))
+    tm.execute(tm.compile(ls, other), a, TrainingState.allocate(other, gpu_device))
+    plan = tm.compile(ls, ld)
+    print("case prepare without the chunk table, capture with it", flush=True)
+    try:
+        _native.set_tuning(chunk_index=False)
+        tm.prepare(plan, gpu_device)
+        _native.set_tuning(chunk_index=True)
+        _capture_first_execute(tm, plan, a, b, gpu_device)
+        # Outside a capture the next call builds the table, and the result is the same.
+        _scramble(b)
+        tm.execute(plan, a, b)
+        torch.cuda.synchronize()
+        assert b.verify_synthetic(SEED)[0] == 0
+    finally:
+        _native.set_tuning()
+
+
+@pytest.mark.parametrize("kind", ["transfer", "backup_up"])
+def test_manager_meta_passes_prepare(gpu_device, kind):
+    """transfer_params / redundant_backup with is_meta_device=True upload the plan's tables, as
+    reshard(is_meta_device=True) does: the first real execution can then be captured."""
+    spec = small_llama2()
+    if kind == "transfer":
+        src, dst = PS(8, 2, 1), PS(8, 1, 2)
+    else:
+        src, dst = PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
+    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device, release_source=False)
+    a = mgr.training_state
+    a.fill_synthetic(SEED)
+    # The library meets the device outside any capture first.
+    warm = mgr.space_for(PS(8, 4, 1)).layout(PS(8, 4, 1))
+    mgr.transfer_manager.execute(mgr.transfer_manager.compile(a.layout, warm), a,
+                                 TrainingState.allocate(warm, gpu_device))
+    ld = mgr.space_for(dst).layout(dst)
+    b = TrainingState.allocate(ld, gpu_device, param=a.param if kind != "transfer" else None)
+    print(f"case meta pass of {kind}, then capture", flush=True)
+    if kind == "transfer":
+        mgr.transfer_params(a, b, None, True)
+        plan = mgr.transfer_manager.compile(a.layout, ld)
+    else:
+        mgr.redundant_backup(a, b, True, is_meta_device=True)
+        plan = mgr.transfer_manager.compile(a.layout, ld, "backup_up")
+    if kind == "transfer":
+        _capture_first_execute(mgr.transfer_manager, plan, a, b, gpu_device)
+        return
+    # Group ZeRO writes only the fp32 arenas (the bf16 params are shared): check those.
+    for t in (b.main, b.exp_avg, b.exp_avg_sq):
+        t.view(torch.int32).fill_(-1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mgr.transfer_manager.execute(plan, a, b)
+    for r in range(2):
+        for t in (b.main, b.exp_avg, b.exp_avg_sq):
+            t.view(torch.int32).fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert b.verify_synthetic(SEED, bf16=False)[0] == 0, r

@@ -130,6 +130,32 @@ def test_compare_through_pointer_table(gpu_device):
     assert int(stats["mismatches"][0]) == (1 if 7 in _covered(tp, ld) else 0)
 
 
+def test_repeated_tensor_lists_skip_the_layout_check(gpu_device):
+    """The same tensors again skip the layout check; a tensor at another address is checked again."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 1, 1)), space.layout(PS(8, 4, 1))
+    tm = TransferManager()
+    tp = tm.compile_tensors(ls, ld)
+    a, b = TrainingState.allocate(ls, gpu_device), TrainingState.allocate(ld, gpu_device)
+    a.fill_synthetic(SEED)
+    src_v, dst_v = tp.src.views(a), tp.dst.views(b)
+    print("case repeated tensor lists", flush=True)
+    for _ in range(3):
+        b.main.zero_()
+        tm.execute_tensors(tp, src_v, dst_v)
+        torch.cuda.synchronize()
+        assert b.verify_synthetic(SEED)[0] == 0
+    assert tm._checked_tensors[id(tp)][1] == [t.data_ptr() for t in list(src_v) + list(dst_v)]
+    strided = torch.empty(2 * dst_v[0].numel(), dtype=dst_v[0].dtype, device=gpu_device)[::2]
+    assert strided.nbytes == dst_v[0].nbytes and not strided.is_contiguous()
+    with pytest.raises(ValueError):
+        tm.execute_tensors(tp, src_v, [strided] + list(dst_v[1:]))
+    b.main.zero_()
+    tm.execute_tensors(tp, src_v, dst_v)
+    torch.cuda.synchronize()
+    assert b.verify_synthetic(SEED)[0] == 0
+
+
 def _covered(tp, ld):
     """Element indices of the main arena that some fp32 tensor holds (the checked ones)."""
     out = set()

@@ -120,3 +120,47 @@ def test_static_compare_refuses_more_than_its_scratch():
     with pytest.raises(_native.EmrsError) as e:
         plan.compare([1 << 20], [1 << 30], None, None, 1, 0, no_alloc=True)
     assert e.value.code == -10 and "scratch" in str(e.value)
+
+
+@pytest.mark.gpu
+def test_static_compare_allocates_nothing(gpu_device):
+    """The defining property: on a fresh plan, arena or per-tensor, the static comparison leaves the
+    device's free memory unchanged and uploads none of the plan's tables (its first execution is
+    still refused under graph capture, as an execution that would upload is), and only then is
+    it compared with the allocating path."""
+    print("case no-alloc 4: allocates nothing on fresh plans", flush=True)
+    # The library meets the device first: kernel code, device properties, the array's address.
+    _, wls, wld, wa, wb, wt, wg, wag = _switched(tiny_llama2, PS(8, 2, 1), PS(8, 4, 1), gpu_device, 3)
+    warm = _native.Plan(wt, [wls.fp32_numel * 4] * 3 + [wls.bf16_numel * 2],
+                        [wld.fp32_numel * 4] * 3 + [wld.bf16_numel * 2])
+    _both(warm, wa.arena_ptrs(), wb.arena_ptrs(), wg, wag, 4)
+    space, ls, ld, a, b, table, groups, aux_groups = _switched(small_llama2, PS(8, 1, 1), PS(8, 4, 1),
+                                                               gpu_device, 17)
+    n = 4 * len(space.all_virtual_params)
+    sb, db = TensorBuffers(ls), TensorBuffers(ld)
+    tt = rebase_on_tensors(table, sb, db)
+    cases = [
+        ("arena", _native.Plan(table, [ls.fp32_numel * 4] * 3 + [ls.bf16_numel * 2],
+                               [ld.fp32_numel * 4] * 3 + [ld.bf16_numel * 2]),
+         a.arena_ptrs(), b.arena_ptrs(), groups, aux_groups, n),
+        ("per-tensor", _native.Plan(tt, sb.nbytes(), db.nbytes()),
+         [x.data_ptr() for x in sb.views(a)], [x.data_ptr() for x in db.views(b)], None, None, 1),
+    ]
+    assert len(sb) > 128
+    st = torch.cuda.current_stream()
+    marker = torch.zeros(1, device=gpu_device)
+    for name, plan, sp, dp, g, ag, ng in cases:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info(gpu_device)[0]
+        got = plan.compare(sp, dp, g, ag, ng, st.cuda_stream, no_alloc=True)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info(gpu_device)[0] == free0, name
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            marker.fill_(1.0)
+            with pytest.raises(_native.EmrsError) as e:
+                plan.execute(sp, dp, torch.cuda.current_stream().cuda_stream)
+        assert e.value.code == -9, name   # the plan's tables are still to be uploaded
+        want = plan.compare(sp, dp, g, ag, ng, st.cuda_stream)
+        _same(got, want)
+        assert int(want["mismatches"].sum()) >= 20, name
