@@ -94,6 +94,7 @@ constexpr uint64_t kMaxGridY = 65535;                     // rows of a one-workg
 // it cost 5.8% and 1.4%, the launch being too short for per-XCD windows.
 constexpr uint64_t kXcdRemapMinChunks = 1ull << 19;
 constexpr uint64_t kMaxUnitsPerSeg = 1ull << 30;       // keeps unit math in 32 bits
+constexpr int kDifferBlocksPerCu = 4;                  // workgroups per CU of a comparison's first pass
 // Row pitches of multi-row segments stay below this many bytes, so that a piece
 // of at most 256 rows spans less than 2^31 bytes from its first row: the
 // buffer-instruction path addresses it with 32-bit offsets.  Segments with
@@ -1384,6 +1385,123 @@ __device__ __forceinline__ void compare_chunk(const DevSeg &s, const char *sbase
   }
 }
 
+// Bits of a that differ from b, folded into one word (0: the units are equal).
+__device__ __forceinline__ uint32_t differ(const u32x4 &a, const u32x4 &b) {
+  return (a.x ^ b.x) | (a.y ^ b.y) | (a.z ^ b.z) | (a.w ^ b.w);
+}
+__device__ __forceinline__ uint32_t differ(uint64_t a, uint64_t b) {
+  const uint64_t d = a ^ b;
+  return (uint32_t)d | (uint32_t)(d >> 32);
+}
+__device__ __forceinline__ uint32_t differ(uint32_t a, uint32_t b) { return a ^ b; }
+__device__ __forceinline__ uint32_t differ(uint16_t a, uint16_t b) { return (uint32_t)(a ^ b); }
+__device__ __forceinline__ uint32_t differ(uint8_t a, uint8_t b) { return (uint32_t)(a ^ b); }
+__device__ __forceinline__ uint32_t differ(const CastOf<u32x4>::type &a, const CastOf<u32x4>::type &b) {
+  return (a.x ^ b.x) | (a.y ^ b.y);
+}
+
+// The bit-level pass over units [u0, u_end) of segment s: `dm` collects the
+// bits in which the destination differs from the source, `dx` those of the
+// second destination (bf16 image or duplicate).  Loads, addresses and order
+// are compare_chunk's; only the arithmetic is left out.
+template <typename T>
+__device__ __forceinline__ void differ_chunk(const DevSeg &s, const char *sbase, const char *dbase,
+                                             const char *abase, uint32_t u0, uint32_t u_end, uint32_t &dm,
+                                             uint32_t &dx) {
+  typedef typename std::conditional<sizeof(T) == 16 || sizeof(T) == 4, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
+  const T *src = reinterpret_cast<const T *>(sbase);
+  const T *dst = reinterpret_cast<const T *>(dbase);
+  const A *aux = reinterpret_cast<const A *>(abase);
+  const T *dup = reinterpret_cast<const T *>(abase);
+  const uint32_t ops = s.ops();
+  for (uint32_t j = 0; j < kUnroll; ++j) {
+    const uint32_t u = u0 + j * kThreads + threadIdx.x;
+    if (u >= u_end) break;
+    uint64_t so = s.src_off + u, dof = s.dst_off + u, ao = s.aux_off + u;
+    if (s.rows > 1) {
+      const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2()), col = u - row * s.len;
+      so = s.src_off + (uint64_t)row * s.src_stride + col;
+      dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
+      ao = s.aux_off + (uint64_t)row * s.aux_stride + col;
+    }
+    const T e = (ops & 2) ? T{} : ld<T, true>(src + so);
+    dm |= differ(e, ld<T, true>(dst + dof));
+    if (ops & 4) dx |= differ(e, ld<T, true>(dup + ao));
+    if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
+      if (ops & 1) dx |= differ(C::cast(e), ld<A, true>(aux + ao));
+    }
+  }
+}
+
+// Mark the groups whose elements differ: one atomic per wave that saw a
+// difference, none for a wave that saw none.  No barrier: each wave marks on
+// its own.
+__device__ __forceinline__ void mark_differ(uint32_t &dm, uint32_t &dx, uint32_t g, uint32_t ga, bool aux,
+                                            GroupAcc *acc) {
+  const bool lead = (threadIdx.x & 63) == 0;
+  if (__any(dm != 0) && lead) atomicOr(&acc[g].mismatches, 1ull);
+  if (aux && __any(dx != 0) && lead) atomicOr(&acc[ga].mismatches, 1ull);
+  dm = dx = 0;
+}
+
+// First pass of a comparison: which groups differ at all.  The schedule is
+// compare_plan_kernel's; per lane only two words of differing bits are kept,
+// so the pass reads at the rate of a plain read.  Only the groups it marks
+// are compared again for compare_ckpt's figures (compare_plan_kernel), which
+// costs about 4% more time on Llama-2-7B than reading alone.
+template <bool kTable>
+__global__ __launch_bounds__(kThreads) void differ_plan_kernel(
+    const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
+    uint32_t n_segs, uint64_t n_chunks, uint32_t run, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
+    const uint64_t *__restrict__ dst_tab, GroupAcc *__restrict__ acc) {
+  const uint64_t xcd = blockIdx.x & 7;
+  const uint64_t c1 = n_chunks * (xcd + 1) / 8;
+  const uint64_t step = (uint64_t)(gridDim.x >> 3) * run;
+  uint32_t dm = 0, dx = 0, cur_g = 0, cur_ga = 0;
+  bool open = false, cur_aux = false;
+  for (uint64_t c = n_chunks * xcd / 8 + (uint64_t)(blockIdx.x >> 3) * run; c < c1; c += step) {
+    const uint64_t c_end = min(c + run, c1);
+    uint32_t lo = 0, hi = n_segs - 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (segs[mid].chunk_begin <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    uint32_t si = lo;
+    uint64_t s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+    for (uint64_t q = c, nq; q < c_end; q += nq) {
+      while (q >= s_end) {
+        ++si;
+        s_end = (si + 1 < n_segs) ? segs[si + 1].chunk_begin : n_chunks;
+      }
+      nq = min(min(c_end, s_end) - q, (uint64_t)kUnroll);
+      const DevSeg s = segs[si];
+      const uint32_t g = groups[si], ga = aux_groups[si];
+      const bool aux = (s.ops() & 5) != 0;
+      if (open && (g != cur_g || aux != cur_aux || (aux && ga != cur_ga))) mark_differ(dm, dx, cur_g, cur_ga, cur_aux, acc);
+      open = true;
+      cur_g = g;
+      cur_ga = ga;
+      cur_aux = aux;
+      const uint32_t total = s.len * s.rows;
+      const uint32_t u0 = (uint32_t)(q - s.chunk_begin) * kChunkUnits;
+      const uint32_t u_end = min(u0 + (uint32_t)nq * kChunkUnits, total);
+      const char *sb = base_of<kTable>(src, src_tab, s.src_buf());
+      const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf());
+      const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf());
+      switch (s.unit_log2()) {
+        case 4: differ_chunk<u32x4>(s, sb, db, ab, u0, u_end, dm, dx); break;
+        case 3: differ_chunk<uint64_t>(s, sb, db, ab, u0, u_end, dm, dx); break;
+        case 2: differ_chunk<uint32_t>(s, sb, db, ab, u0, u_end, dm, dx); break;
+        case 1: differ_chunk<uint16_t>(s, sb, db, ab, u0, u_end, dm, dx); break;
+        default: differ_chunk<uint8_t>(s, sb, db, ab, u0, u_end, dm, dx); break;
+      }
+    }
+  }
+  if (open) mark_differ(dm, dx, cur_g, cur_ga, cur_aux, acc);
+}
+
 // Sum / max over the workgroup; the result is valid in thread 0.
 __device__ void block_reduce(LaneAcc &a, double *lds_d, uint32_t *lds_u, float *lds_f) {
   for (int off = 32; off > 0; off >>= 1) {
@@ -1429,10 +1547,12 @@ __device__ void flush(const LaneAcc &a, GroupAcc *g) {
 // Add the workgroup's lane sums to their groups and clear them: the values
 // compared, and with `aux` the second destination's.  Every thread calls it.
 __device__ void flush_block(LaneAcc &m, LaneAcc &x, uint32_t g, uint32_t ga, bool aux, GroupAcc *acc,
-                            double *lds_d, uint32_t *lds_u, float *lds_f) {
-  block_reduce(m, lds_d, lds_u, lds_f);
-  if (threadIdx.x == 0) flush(m, acc + g);
-  if (aux) {
+                            const uint8_t *active, double *lds_d, uint32_t *lds_u, float *lds_f) {
+  if (active[g]) {
+    block_reduce(m, lds_d, lds_u, lds_f);
+    if (threadIdx.x == 0) flush(m, acc + g);
+  }
+  if (aux && active[ga]) {
     block_reduce(x, lds_d, lds_u, lds_f);
     if (threadIdx.x == 0) flush(x, acc + ga);
   }
@@ -1448,12 +1568,14 @@ __device__ void flush_block(LaneAcc &m, LaneAcc &x, uint32_t g, uint32_t ga, boo
 // chunks share their (group, aux group); they are reduced over the workgroup
 // only when that pair changes and at the end.  Every decision depends on the
 // segment alone, so it is uniform across the workgroup, and every thread
-// reaches every barrier.
+// reaches every barrier.  Only segments with a group marked in `active` are
+// compared, and only marked groups are accumulated: the second pass of a
+// comparison, over the groups the first pass (differ_plan_kernel) found to differ.
 template <bool kTable>
 __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
     const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
     uint32_t n_segs, uint64_t n_chunks, uint32_t run, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
-    const uint64_t *__restrict__ dst_tab, GroupAcc *__restrict__ acc) {
+    const uint64_t *__restrict__ dst_tab, GroupAcc *__restrict__ acc, const uint8_t *__restrict__ active) {
   __shared__ double lds_d[2 * kThreads / 64];
   __shared__ uint32_t lds_u[2 * kThreads / 64];
   __shared__ float lds_f[2 * kThreads / 64];
@@ -1482,8 +1604,9 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
       const DevSeg s = segs[si];
       const uint32_t g = groups[si], ga = aux_groups[si];
       const bool aux = (s.ops() & 5) != 0;  // cast or duplicate
+      if (!active[g] && !(aux && active[ga])) continue;  // no group of this segment differs
       if (open && (g != cur_g || aux != cur_aux || (aux && ga != cur_ga)))
-        flush_block(m, x, cur_g, cur_ga, cur_aux, acc, lds_d, lds_u, lds_f);
+        flush_block(m, x, cur_g, cur_ga, cur_aux, acc, active, lds_d, lds_u, lds_f);
       open = true;
       cur_g = g;
       cur_ga = ga;
@@ -1503,7 +1626,7 @@ __global__ __launch_bounds__(kThreads) void compare_plan_kernel(
       }
     }
   }
-  if (open) flush_block(m, x, cur_g, cur_ga, cur_aux, acc, lds_d, lds_u, lds_f);
+  if (open) flush_block(m, x, cur_g, cur_ga, cur_aux, acc, active, lds_d, lds_u, lds_f);
 }
 
 // Zero n 32-bit words (accumulators are cleared by a kernel rather than a memset).
@@ -1521,6 +1644,7 @@ struct CompareJob {
   std::vector<uint32_t> g_host;  // per device segment: its group, then its aux group
   int cus = 0;
   int resident = 0;              // compare_plan_kernel workgroups per CU
+  int resident_differ = 0;       // differ_plan_kernel workgroups per CU
 };
 
 int compare_setup(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
@@ -1565,27 +1689,81 @@ int compare_device(CompareJob *job, int *dev) {
     (void)hipGetLastError();
     job->resident = 4;
   }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&job->resident_differ, differ_plan_kernel<false>, kThreads, 0) !=
+          hipSuccess ||
+      job->resident_differ <= 0) {
+    (void)hipGetLastError();
+    job->resident_differ = job->resident;
+  }
   return EMRS_OK;
 }
 
 // A persistent grid of resident workgroups, a multiple of 8 (one eighth of
 // the plan per XCD), in runs of up to 32 steps: at most a quarter of each
-// workgroup's share, so that small plans still spread out.
+// workgroup's share, so that small plans still spread out.  `active` null:
+// the first pass (differ_plan_kernel); else the second (compare_plan_kernel).
 hipError_t compare_launch(const emrs_plan *plan, const CompareJob &job, const DevSeg *table, const uint32_t *grp,
-                          const uint64_t *tab, GroupAcc *acc, hipStream_t st) {
+                          const uint64_t *tab, GroupAcc *acc, const uint8_t *active, hipStream_t st) {
   const size_t nd = plan->segs.size();
-  uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)job.cus * (uint32_t)job.resident);
+  // The first pass could hold 8 workgroups per CU; 3-6 read at the plain read rate and 8 is up to
+  // 7% slower (Llama-2-7B, Mixtral and Group-ZeRO switches, same allocations): 4.
+  const uint32_t resident = (uint32_t)(active ? job.resident : std::min(job.resident_differ, kDifferBlocksPerCu));
+  uint64_t blocks = std::min<uint64_t>(plan->n_chunks, (uint64_t)job.cus * resident);
   blocks = std::max<uint64_t>(8, blocks / 8 * 8);
   const uint32_t run =
       (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32 * kUnroll, plan->n_chunks / (blocks * 4)));
   const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
-  if (job.rb.table)
-    hipLaunchKernelGGL(compare_plan_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                       grp + nd, (uint32_t)nd, plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
-  else
-    hipLaunchKernelGGL(compare_plan_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, st, table, grp,
-                       grp + nd, (uint32_t)nd, plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
+  const dim3 grid((uint32_t)blocks), block(kThreads);
+  if (!active) {
+    if (job.rb.table)
+      hipLaunchKernelGGL(differ_plan_kernel<true>, grid, block, 0, st, table, grp, grp + nd, (uint32_t)nd,
+                         plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
+    else
+      hipLaunchKernelGGL(differ_plan_kernel<false>, grid, block, 0, st, table, grp, grp + nd, (uint32_t)nd,
+                         plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc);
+  } else if (job.rb.table) {
+    hipLaunchKernelGGL(compare_plan_kernel<true>, grid, block, 0, st, table, grp, grp + nd, (uint32_t)nd,
+                       plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc, active);
+  } else {
+    hipLaunchKernelGGL(compare_plan_kernel<false>, grid, block, 0, st, table, grp, grp + nd, (uint32_t)nd,
+                       plan->n_chunks, run, job.rb.src, job.rb.dst, tab, dtab, acc, active);
+  }
   return hipGetLastError();
+}
+
+// Zero the accumulators with a kernel (no memset node if the stream's work is ever captured).
+hipError_t clear_acc(GroupAcc *acc, uint32_t n_groups, hipStream_t st) {
+  const uint64_t words = (uint64_t)n_groups * sizeof(GroupAcc) / sizeof(uint32_t);
+  hipLaunchKernelGGL(clear_words_kernel, dim3((uint32_t)std::min<uint64_t>(1024, (words + 255) / 256)), dim3(256), 0,
+                     st, reinterpret_cast<uint32_t *>(acc), words);
+  return hipGetLastError();
+}
+
+// Both passes of a comparison, on device buffers the caller provides (acc:
+// n_groups accumulators; active: n_groups bytes), leaving the accumulators
+// in `host`.  The first pass marks the groups that differ in any bit; when
+// none does (a correct switch), every figure is 0 and the second pass does
+// not run.  Otherwise the marked groups are compared again with every figure.
+hipError_t compare_passes(const emrs_plan *plan, const CompareJob &job, const DevSeg *table, const uint32_t *grp,
+                          const uint64_t *tab, GroupAcc *acc, uint8_t *active, uint32_t n_groups, hipStream_t st,
+                          std::vector<GroupAcc> &host) {
+  const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
+  hipError_t e = clear_acc(acc, n_groups, st);
+  if (e == hipSuccess) e = compare_launch(plan, job, table, grp, tab, acc, nullptr, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return e;
+  std::vector<uint8_t> mark(n_groups, 0);
+  bool any = false;
+  for (uint32_t g = 0; g < n_groups; ++g)
+    if (host[g].mismatches) mark[g] = 1, any = true;
+  if (!any) return hipSuccess;
+  e = hipMemcpyAsync(active, mark.data(), n_groups, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = clear_acc(acc, n_groups, st);
+  if (e == hipSuccess) e = compare_launch(plan, job, table, grp, tab, acc, active, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
+  const hipError_t se = hipStreamSynchronize(st);  // `mark` is read by the copy above
+  return e == hipSuccess ? se : e;
 }
 
 void compare_finish(const std::vector<GroupAcc> &host, emrs_compare_stats *stats) {
@@ -1975,23 +2153,23 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   rc = device_table(plan, dev, st, &table);
   if (rc) return rc;
 
-  const size_t acc_bytes = (size_t)n_groups * sizeof(GroupAcc);
-  const size_t grp_bytes = job.g_host.size() * sizeof(uint32_t);
+  const size_t acc_bytes = align256((size_t)n_groups * sizeof(GroupAcc));
+  const size_t grp_bytes = align256(job.g_host.size() * sizeof(uint32_t));
   char *buf = nullptr;
-  hipError_t e = hipMalloc(&buf, acc_bytes + grp_bytes);
+  hipError_t e = hipMalloc(&buf, acc_bytes + grp_bytes + n_groups);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(compare buffers)");
   GroupAcc *acc = reinterpret_cast<GroupAcc *>(buf);
   uint32_t *grp = reinterpret_cast<uint32_t *>(buf + acc_bytes);
+  uint8_t *active = reinterpret_cast<uint8_t *>(buf + acc_bytes + grp_bytes);
   std::vector<GroupAcc> host(n_groups);
-  e = hipMemsetAsync(acc, 0, acc_bytes, st);
-  if (e == hipSuccess) e = hipMemcpyAsync(grp, job.g_host.data(), grp_bytes, hipMemcpyHostToDevice, st);
+  e = hipMemcpyAsync(grp, job.g_host.data(), job.g_host.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st);
   uint64_t *tab = nullptr;
   bool tab_owned = false;
   int table_rc = EMRS_OK;  // a pointer-table failure keeps its own message
   if (e == hipSuccess) table_rc = pointer_table(plan, dev, job.rb, st, &tab, &tab_owned);
-  if (e == hipSuccess && table_rc == EMRS_OK) e = compare_launch(plan, job, table, grp, tab, acc, st);
+  if (e == hipSuccess && table_rc == EMRS_OK)
+    e = compare_passes(plan, job, table, grp, tab, acc, active, n_groups, st, host);
   if (tab_owned) (void)hipFreeAsync(tab, st);
-  if (e == hipSuccess && table_rc == EMRS_OK) e = hipMemcpyAsync(host.data(), acc, acc_bytes, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   (void)hipFree(buf);
   if (table_rc != EMRS_OK) return table_rc;
@@ -2014,7 +2192,8 @@ int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *cons
   const size_t grp_bytes = align256(job.g_host.size() * sizeof(uint32_t));
   const size_t seg_bytes = align256(nd * sizeof(DevSeg));
   const size_t ptr_bytes = job.rb.table ? align256(job.rb.ptrs.size() * sizeof(uint64_t)) : 0;
-  const size_t need = acc_bytes + grp_bytes + seg_bytes + ptr_bytes;
+  const size_t act_bytes = align256(n_groups);
+  const size_t need = acc_bytes + grp_bytes + seg_bytes + ptr_bytes + act_bytes;
   if (need > EMRS_STATIC_SCRATCH_BYTES) {
     char msg[200];
     snprintf(msg, sizeof msg,
@@ -2039,20 +2218,15 @@ int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *cons
   uint32_t *grp = reinterpret_cast<uint32_t *>(base + acc_bytes);
   DevSeg *table = reinterpret_cast<DevSeg *>(base + acc_bytes + grp_bytes);
   uint64_t *tab = job.rb.table ? reinterpret_cast<uint64_t *>(base + acc_bytes + grp_bytes + seg_bytes) : nullptr;
-  // The previous call's accumulators are still there: clear them with a kernel (no memset node).
-  const uint64_t acc_words = (uint64_t)n_groups * sizeof(GroupAcc) / sizeof(uint32_t);
-  hipLaunchKernelGGL(clear_words_kernel, dim3((uint32_t)std::min<uint64_t>(1024, (acc_words + 255) / 256)),
-                     dim3(256), 0, st, reinterpret_cast<uint32_t *>(acc), acc_words);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(grp, job.g_host.data(), job.g_host.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st);
+  uint8_t *active = base + acc_bytes + grp_bytes + seg_bytes + ptr_bytes;
+  // The previous call's accumulators are still there: compare_passes clears them with a kernel.
+  hipError_t e =
+      hipMemcpyAsync(grp, job.g_host.data(), job.g_host.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st);
   if (e == hipSuccess) e = hipMemcpyAsync(table, plan->segs.data(), nd * sizeof(DevSeg), hipMemcpyHostToDevice, st);
   if (e == hipSuccess && tab)
     e = hipMemcpyAsync(tab, job.rb.ptrs.data(), job.rb.ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice, st);
-  if (e == hipSuccess) e = compare_launch(plan, job, table, grp, tab, acc, st);
   std::vector<GroupAcc> host(n_groups);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(host.data(), acc, (size_t)n_groups * sizeof(GroupAcc), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = compare_passes(plan, job, table, grp, tab, acc, active, n_groups, st, host);
   // The host copies above read job's and plan's vectors: wait before they can go.
   const hipError_t se = hipStreamSynchronize(st);
   if (e == hipSuccess) e = se;

@@ -210,7 +210,8 @@ typedef struct emrs_compare_stats {
   uint64_t nonfinite;       /* mismatching fp32/bf16 elements with a NaN or infinite difference */
   uint64_t reserved;
   double sum_sq_diff;       /* sum of (actual - expected)^2 over finite differences */
-  double sum_sq_expected;   /* sum of expected^2 over finite expected fp32/bf16 values */
+  double sum_sq_expected;   /* sum of expected^2 over finite expected fp32/bf16 values; 0 for a group
+                               without mismatches (its RMS and relative RMS are 0 either way) */
   float max_abs_diff;       /* max |actual - expected| over finite differences */
   float max_rel_diff;       /* max |actual - expected| / (|expected| + 1e-12) */
   uint64_t reserved2;
@@ -218,7 +219,11 @@ typedef struct emrs_compare_stats {
 
 /*
  * Compare the destination buffers with what `plan` writes from the source
- * buffers, and accumulate the differences per group.
+ * buffers, and accumulate the differences per group.  Two passes: the first
+ * only finds the groups in which any bit differs, at the rate of a plain read;
+ * only if there are such groups does a second pass compute every figure for
+ * them.  A correct switch therefore costs one read of the source and the
+ * destination.
  *   groups[i]:     group of input segment i's elements (NULL: all group 0)
  *   aux_groups[i]: group of input segment i's bf16 image (NULL: groups[i])
  *   stats:         n_groups host records, filled when the call returns

@@ -188,7 +188,9 @@ def compare_numpy(table, groups, aux_groups, n_groups, src, dst):
 
     Returns ``n_groups`` records of _native.COMPARE_DTYPE.  fp32 and bf16
     differences are taken in fp32, squared in fp64, as compare_ckpt.py's
-    figures define them (tools/ckpt/compare_ckpt.py:52-66).
+    figures define them (tools/ckpt/compare_ckpt.py:52-66).  A group with no
+    mismatching element reports 0 in every figure, its sum of squares of the
+    expected values included (its RMS and relative RMS are 0 either way).
     """
     from elasticmegatron_amd._native import COMPARE_DTYPE
 
@@ -240,6 +242,7 @@ def compare_numpy(table, groups, aux_groups, n_groups, src, dst):
         if int(s["flags"]) & 4:
             aux = dst[int(s["aux_buf"])].view(udt[eb])
             acc(int(ga), exp, _view(aux, int(s["aux_off"]), rows, n, int(s["aux_stride"])).reshape(-1), eb)
+    out["sum_sq_expected"][out["mismatches"] == 0] = 0.0
     return out
 
 

@@ -130,10 +130,10 @@ def test_static_compare_allocates_nothing(gpu_device):
     it compared with the allocating path."""
     print("case no-alloc 4: allocates nothing on fresh plans", flush=True)
     # The library meets the device first: kernel code, device properties, the array's address.
-    _, wls, wld, wa, wb, wt, wg, wag = _switched(tiny_llama2, PS(8, 2, 1), PS(8, 4, 1), gpu_device, 3)
+    wspace, wls, wld, wa, wb, wt, wg, wag = _switched(tiny_llama2, PS(8, 2, 1), PS(8, 4, 1), gpu_device, 3)
     warm = _native.Plan(wt, [wls.fp32_numel * 4] * 3 + [wls.bf16_numel * 2],
                         [wld.fp32_numel * 4] * 3 + [wld.bf16_numel * 2])
-    _both(warm, wa.arena_ptrs(), wb.arena_ptrs(), wg, wag, 4)
+    _both(warm, wa.arena_ptrs(), wb.arena_ptrs(), wg, wag, 4 * len(wspace.all_virtual_params))
     space, ls, ld, a, b, table, groups, aux_groups = _switched(small_llama2, PS(8, 1, 1), PS(8, 4, 1),
                                                                gpu_device, 17)
     n = 4 * len(space.all_virtual_params)
