@@ -147,6 +147,10 @@ def parse():
     ap.add_argument("--megatron-buffers", action="store_true",
                     help="run the per-tensor plan on views of Megatron-shaped flat buffers (a DDP param buffer per "
                          "model shard, flat DP shards per rank, padding in place), allocated separately")
+    ap.add_argument("--ipc", action="store_true",
+                    help="the switch from another process's state: a child exports the source in granules "
+                         "(--ipc-granule-bytes), this process maps them and reshards into its own arenas")
+    ap.add_argument("--ipc-granule-bytes", type=int, default=1 << 30)
     ap.add_argument("--low-memory", action="store_true",
                     help="time staged switches through ElasticMegatronManager(low_memory=True), alternating "
                          "directions: one optimizer kind per launch, arenas allocated and released as it goes")
@@ -259,6 +263,8 @@ def main():
         return bench_low_memory(args, desc, spec_fn, src, dst, dev)
     if args.megatron_buffers:
         return bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream)
+    if args.ipc:
+        return bench_ipc(args, desc, spec_fn, src, dst, dev, stream)
     repad = bool(opt and opt[0])
     backup = ParallelStrategy.is_redundant_backup(src, dst)
     spec = spec_fn()
@@ -376,6 +382,21 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
     }
+    if tplan is not None:
+        # The arena plan on the same allocations in this process, alternating with the per-tensor
+        # plan, so that the two compare without the spread of placements between processes.
+        rounds = {"tensors": [], "arenas": []}
+        for _ in range(3):
+            for name, run in (("tensors", lambda: step(a, b)), ("arenas", lambda: tm.execute(plan, a, b, stream))):
+                run()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(5):
+                    run()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                rounds[name].append(round(e0.elapsed_time(e1) / 5, 4))
+        out["config"]["same_process_ms"] = rounds
     if args.placement_trials:
         import gc
 
@@ -405,8 +426,23 @@ def main():
         t_v = time.perf_counter()
         report = tm.verify(a, b, kind)
         v_ms = (time.perf_counter() - t_v) * 1e3
-        out["config"]["plan_verification"] = {"bit_exact": report.bit_exact, "elements": report.elements,
-                                              "wall_ms": round(v_ms, 3)}
+        # The read ceiling of the same bytes in this process: emrs_xor_checksum over every arena the
+        # check reads (placement moves a read-heavy launch by several percent between processes).
+        word = torch.zeros(1, dtype=torch.int32, device=dev)
+        read = [a.main, a.exp_avg, a.exp_avg_sq, b.main, b.exp_avg, b.exp_avg_sq]
+        if backup is None:
+            read.append(b.param)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for t in read:
+            _native.xor_checksum(t.data_ptr(), t.numel() * t.element_size() // 16 * 16, word.data_ptr(),
+                                 stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out["config"]["plan_verification"] = {
+            "bit_exact": report.bit_exact, "elements": report.elements, "wall_ms": round(v_ms, 3),
+            "read_ceiling_ms": round(e0.elapsed_time(e1), 3),
+            "read_ceiling_bytes": sum(t.numel() * t.element_size() // 16 * 16 for t in read)}
         if not report.bit_exact:
             print(f"[bench] plan verification FAILED: {report.lines()[:3]}", file=sys.stderr)
             return 3
@@ -581,6 +617,107 @@ def bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream):
                    "buffers": f"{len(ms_.specs)} source, {len(md.specs)} destination flat buffers; "
                               f"{len(plan.src)} / {len(plan.dst)} tensor views",
                    "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
+                   "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
+        "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
+    """The switch from another process's exported state (the reference's inter-process hand-off,
+    ipc_manager.py:54-155): a child process allocates the source in granules, fills it and sends
+    the payload; this process maps the granules and times the switch from them into its own
+    arenas.  The mappings are closed before the child is told to exit."""
+    import dataclasses
+    import select
+    import subprocess
+
+    import torch
+
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer import ipc_manager as ipc
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    backup = ParallelStrategy.is_redundant_backup(src, dst)
+    if backup is not None:
+        print("bench.py --ipc: a Group-ZeRO switch keeps the bf16 params in place and cannot start from a "
+              "received state", file=sys.stderr)
+        return 2
+    spec = spec_fn()
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    child = subprocess.Popen(
+        [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_export", "--model-spec",
+         json.dumps(dataclasses.asdict(spec)), "--strategy", json.dumps(ipc.strategy_to_dict(src)), "--seed",
+         str(SEED), "--granule-bytes", str(args.ipc_granule_bytes)],
+        cwd=ROOT, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
+    state = None
+    try:
+        tm = TransferManager(bf16_source=args.bf16_source)
+        plan = tm.compile_granules(ls, ld, args.ipc_granule_bytes, None)
+        arena_plan = tm.compile(ls, ld)
+        b = TrainingState.allocate(ld, dev)
+        if not select.select([child.stdout], [], [], 600)[0]:
+            print("bench.py --ipc: the exporting process sent nothing in 600 s", file=sys.stderr)
+            return 1
+        line = child.stdout.readline()
+        if not line:
+            print(f"bench.py --ipc: the exporting process exited with {child.wait()}", file=sys.stderr)
+            return 1
+        state, _ = ipc.receive_training_state(line, dev, space=space)
+        print(f"[bench] {args.workload}: {len(state.buffers)} granules mapped, {plan.segments.shape[0]} segments",
+              file=sys.stderr, flush=True)
+        tm.prepare(plan, dev)
+        for _ in range(args.warmup):
+            tm.execute_states(plan, state, b, stream)
+        torch.cuda.synchronize()
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        events[0].record(stream)
+        for i in range(args.steps):
+            tm.execute_states(plan, state, b, stream)
+            events[i + 1].record(stream)
+        torch.cuda.synchronize()
+        verified = None
+        if not args.no_verify:
+            bad, first = b.verify_synthetic(SEED)
+            report = tm.verify(state, b)
+            verified = bad == 0 and report.bit_exact
+            if not verified:
+                print(f"[bench] verification FAILED: {bad} elements, first {first}; "
+                      f"{report.lines()[:3]}", file=sys.stderr)
+                return 3
+        n_granules = len(state.buffers)
+    finally:
+        if state is not None:
+            state.close()
+        if child.poll() is None:
+            try:
+                ipc.notify_release(child.stdin)
+                child.stdin.close()
+            except BrokenPipeError:
+                pass
+            try:
+                child.wait(timeout=120)
+            except subprocess.TimeoutExpired:
+                child.kill()
+                child.wait()
+    step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
+    ms = sum(step_ms) / len(step_ms)
+    traffic_gbps = arena_plan.traffic_bytes / (ms / 1e3) / 1e9
+    out = {
+        "metric": metric_for(args.workload, desc), "value": round(plan.payload_bytes / (ms / 1e3) / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
+        "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
+        "config": {"workload": desc + f", from another process's state in {args.ipc_granule_bytes}-byte granules",
+                   "params": spec.num_params(), "payload_bytes": plan.payload_bytes, "granules": n_granules,
+                   "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
+                   "exporter_exit_status": child.returncode,
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},

@@ -51,3 +51,11 @@ def test_rank_shares_line(gpu_device):
     assert all(r["segments"] > 0 and r["ms"] > 0 for r in d["shares"])
     assert sum(r["payload_bytes"] for r in d["shares"]) > 0
     assert d["whole_plan_ms"] > 0 and d["sum_of_shares_ms"] >= d["max_share_ms"] > 0
+
+
+@pytest.mark.gpu
+def test_ipc_line(gpu_device):
+    """--ipc: the switch from a child process's exported granules, checked after the timed steps."""
+    d = _bench("--ipc", "--ipc-granule-bytes", str(3 << 22), "--steps", "2", "--warmup", "1")
+    assert d["config"]["verified_bit_exact"] is True and d["config"]["exporter_exit_status"] == 0
+    assert d["config"]["granules"] > 4 and d["ms_per_step"] > 0
