@@ -871,12 +871,18 @@ int note_launch(emrs_plan *plan, int dev, hipStream_t st) {
   if ((int)plan->launch_events.size() <= dev) plan->launch_events.resize(dev + 1);
   std::vector<hipEvent_t> &evs = plan->launch_events[dev];
   hipEvent_t ev = nullptr;
-  for (hipEvent_t x : evs)
-    if (hipEventQuery(x) == hipSuccess) {  // its launch has finished: reuse it
+  bool not_ready = false;
+  for (hipEvent_t x : evs) {
+    const hipError_t q = hipEventQuery(x);
+    if (q == hipSuccess) {  // its launch has finished: reuse it
       ev = x;
       break;
     }
-  (void)hipGetLastError();  // hipEventQuery reports hipErrorNotReady for the running ones
+    not_ready = not_ready || q == hipErrorNotReady;
+  }
+  // A running launch's query answers hipErrorNotReady, which is no failure: do not leave it
+  // behind as this thread's last error.
+  if (not_ready) (void)hipGetLastError();
   if (!ev) {
     e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags");

@@ -2,6 +2,7 @@
 // segment tables through emrs_plan_create / stats / destroy, plus tuning calls.
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <random>
 #include <vector>
@@ -63,6 +64,33 @@ int main(int argc, char **argv) {
     tu.lanes = (uint32_t)U(0, 300); tu.units = (uint32_t)U(0, 5); tu.xcd_remap = (uint32_t)U(0, 3);
     tu.warm_tables = (uint32_t)U(0, 2);
     (void)emrs_set_tuning(&tu);
+  }
+  // Hand-off records refused on the host, before any driver call: allocations of 2 GiB or more,
+  // buffers past their allocation, misaligned offsets, a set reserved field; unknown pointers.
+  for (int i = 0; i < 2000; ++i) {
+    emrs_ipc_buffer b;
+    memset(&b, 0, sizeof b);
+    for (auto &x : b.handle) x = (uint8_t)rng();
+    const int kind = (int)(rng() % 4);
+    b.allocation_bytes = kind == 0 ? EMRS_IPC_MAX_ALLOCATION_BYTES + U(0, 1ull << 40) : U(1, 1ull << 30);
+    b.offset = kind == 2 ? U(0, 15) | 1 : U(0, b.allocation_bytes) & ~15ull;
+    b.bytes = kind == 1 ? b.allocation_bytes - std::min(b.offset, b.allocation_bytes) + U(1, 100) : 0;
+    b.reserved = kind == 3 ? (uint32_t)U(1, 9) : 0;
+    void *ptr = (void *)0x1;
+    const int rc = emrs_ipc_open(&b, &ptr);
+    if (rc == EMRS_OK || ptr != nullptr || !emrs_last_error()[0]) {
+      fprintf(stderr, "ipc record %d (kind %d) not refused: rc %d\n", i, kind, rc);
+      return 1;
+    }
+    if (emrs_ipc_close((void *)(uintptr_t)U(1, 1ull << 48)) == EMRS_OK) {
+      fprintf(stderr, "close of an unknown pointer accepted\n");
+      return 1;
+    }
+  }
+  if (emrs_ipc_open_count() != 0 || emrs_ipc_open(nullptr, nullptr) == EMRS_OK ||
+      emrs_ipc_export(nullptr, 16, nullptr) == EMRS_OK) {
+    fprintf(stderr, "ipc argument checks\n");
+    return 1;
   }
   printf("ok %d rejected %d\n", ok, bad);
   return 0;

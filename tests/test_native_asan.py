@@ -2,7 +2,8 @@
 
 ``tests/native/plan_builder_fuzz.cpp`` sends random segment tables, valid and not, through
 ``emrs_plan_create`` / ``emrs_plan_stats_get`` / ``emrs_plan_execute`` (which must refuse without a
-device) / ``emrs_plan_destroy``, and random launch shapes through ``emrs_set_tuning``.  The library
+device) / ``emrs_plan_destroy``, random launch shapes through ``emrs_set_tuning``, and malformed
+hand-off records through ``emrs_ipc_open`` / ``emrs_ipc_close`` (refused before the driver).  The library
 is rebuilt for the test with the host half sanitized (``-Xarch_host``); its device code is the
 ordinary gfx950 build and is never launched here.
 """
