@@ -1248,6 +1248,12 @@ int chunk_table(emrs_plan *plan, int dev, hipStream_t st, const DevSeg *segs, ui
   return EMRS_OK;
 }
 
+// The chunk table already on device `dev`, or nullptr: allocates nothing.
+const uint32_t *existing_chunk_table(emrs_plan *plan, int dev) {
+  std::lock_guard<std::mutex> lk(plan->mu);
+  return (int)plan->chunk_tables.size() > dev ? plan->chunk_tables[dev] : nullptr;
+}
+
 // The plan's segment table on device `dev`, uploaded on first use.
 int device_table(emrs_plan *plan, int dev, hipStream_t st, DevSeg **table) {
   std::lock_guard<std::mutex> lk(plan->mu);
@@ -1440,6 +1446,88 @@ __device__ __forceinline__ void differ_chunk(const DevSeg &s, const char *sbase,
   }
 }
 
+// First pass of a comparison on the copy kernel's schedule: one 64-lane
+// workgroup per piece of U units of a chunk (U = 4: one workgroup per 4 KB
+// chunk), its segment from the plan's chunk table, dispatched in order and,
+// on large plans, each XCD on its own eighth of the pieces.  Every lane issues
+// its U units' source and destination loads before it compares them.  Faster
+// than the persistent grid on every full-size switch (2-4%, same allocations):
+// a segment's rows or gathered runs are spread over many workgroups in flight.
+template <typename T, int U>
+__device__ __forceinline__ void differ_units(const DevSeg &s, const char *sbase, const char *dbase,
+                                             const char *abase, uint32_t u0, uint32_t total, uint32_t &dm,
+                                             uint32_t &dx) {
+  typedef typename std::conditional<sizeof(T) == 16 || sizeof(T) == 4, CastOf<T>, CastOf<uint32_t>>::type C;
+  typedef typename C::type A;
+  const T *src = reinterpret_cast<const T *>(sbase);
+  const T *dst = reinterpret_cast<const T *>(dbase);
+  const A *aux = reinterpret_cast<const A *>(abase);
+  const T *dup = reinterpret_cast<const T *>(abase);
+  const uint32_t ops = s.ops();
+  T e[U], g[U];
+  uint64_t ao[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * 64 + threadIdx.x;
+    e[j] = T{};
+    g[j] = T{};
+    ao[j] = 0;
+    if (u < total) {
+      uint64_t so = s.src_off + u, dof = s.dst_off + u;
+      ao[j] = s.aux_off + u;
+      if (s.rows > 1) {
+        const uint32_t row = magic_div(u, s.magic, s.sh1(), s.sh2()), col = u - row * s.len;
+        so = s.src_off + (uint64_t)row * s.src_stride + col;
+        dof = s.dst_off + (uint64_t)row * s.dst_stride + col;
+        ao[j] = s.aux_off + (uint64_t)row * s.aux_stride + col;
+      }
+      if (!(ops & 2)) e[j] = ld<T, true>(src + so);
+      g[j] = ld<T, true>(dst + dof);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint32_t u = u0 + j * 64 + threadIdx.x;
+    if (u < total) {
+      dm |= differ(e[j], g[j]);
+      if (ops & 4) dx |= differ(e[j], ld<T, true>(dup + ao[j]));
+      if constexpr (sizeof(T) == 16 || sizeof(T) == 4) {
+        if (ops & 1) dx |= differ(C::cast(e[j]), ld<A, true>(aux + ao[j]));
+      }
+    }
+  }
+}
+
+template <bool kTable, int U>
+__global__ __launch_bounds__(64) void differ_piece_kernel(
+    const DevSeg *__restrict__ segs, uint64_t n_chunks, Bases src, Bases dst, const uint64_t *__restrict__ src_tab,
+    const uint64_t *__restrict__ dst_tab, uint64_t xcd_share, const uint32_t *__restrict__ chunk_seg,
+    const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups, GroupAcc *__restrict__ acc) {
+  constexpr uint32_t kPieces = kChunkUnits / (64 * U);
+  uint64_t w = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  if (w < xcd_share * 8) w = (w & 7) * xcd_share + (w >> 3);
+  const uint64_t c = w / kPieces;
+  if (c >= n_chunks) return;
+  const uint32_t lo = chunk_seg[c];
+  const DevSeg s = segs[lo];
+  const uint32_t total = s.len * s.rows;
+  const uint32_t u0 = (uint32_t)(c - s.chunk_begin) * kChunkUnits + (uint32_t)(w % kPieces) * (64 * U);
+  if (kPieces > 1 && u0 >= total) return;
+  const char *sb = base_of<kTable>(src, src_tab, s.src_buf());
+  const char *db = base_of<kTable>(dst, dst_tab, s.dst_buf());
+  const char *ab = base_of<kTable>(dst, dst_tab, s.aux_buf());
+  uint32_t dm = 0, dx = 0;
+  switch (s.unit_log2()) {
+    case 4: differ_units<u32x4, U>(s, sb, db, ab, u0, total, dm, dx); break;
+    case 3: differ_units<uint64_t, U>(s, sb, db, ab, u0, total, dm, dx); break;
+    case 2: differ_units<uint32_t, U>(s, sb, db, ab, u0, total, dm, dx); break;
+    case 1: differ_units<uint16_t, U>(s, sb, db, ab, u0, total, dm, dx); break;
+    default: differ_units<uint8_t, U>(s, sb, db, ab, u0, total, dm, dx); break;
+  }
+  if (__any(dm != 0) && threadIdx.x == 0) atomicOr(&acc[groups[lo]].mismatches, 1ull);
+  if ((s.ops() & 5) && __any(dx != 0) && threadIdx.x == 0) atomicOr(&acc[aux_groups[lo]].mismatches, 1ull);
+}
+
 // Mark the groups whose elements differ: one atomic per wave that saw a
 // difference, none for a wave that saw none.  No barrier: each wave marks on
 // its own.
@@ -1451,11 +1539,13 @@ __device__ __forceinline__ void mark_differ(uint32_t &dm, uint32_t &dx, uint32_t
   dm = dx = 0;
 }
 
-// First pass of a comparison: which groups differ at all.  The schedule is
-// compare_plan_kernel's; per lane only two words of differing bits are kept,
-// so the pass reads at the rate of a plain read.  Only the groups it marks
-// are compared again for compare_ckpt's figures (compare_plan_kernel), which
-// costs about 4% more time on Llama-2-7B than reading alone.
+// First pass of a comparison when the plan has no chunk table on the device
+// (it did not fit, or emrs_plan_compare_static meets a plan that has never
+// run there): which groups differ at all, on compare_plan_kernel's persistent
+// schedule.  Per lane only two words of differing bits are kept.  Only the
+// groups it marks are compared again for compare_ckpt's figures
+// (compare_plan_kernel), whose per-element fp64 work costs about 4% more time
+// on Llama-2-7B than reading alone.
 template <bool kTable>
 __global__ __launch_bounds__(kThreads) void differ_plan_kernel(
     const DevSeg *__restrict__ segs, const uint32_t *__restrict__ groups, const uint32_t *__restrict__ aux_groups,
@@ -1651,6 +1741,7 @@ struct CompareJob {
   int cus = 0;
   int resident = 0;              // compare_plan_kernel workgroups per CU
   int resident_differ = 0;       // differ_plan_kernel workgroups per CU
+  const uint32_t *cseg = nullptr;  // the plan's chunk table on this device, if there is one
 };
 
 int compare_setup(emrs_plan *plan, void *const *src_bases, void *const *dst_bases, const uint32_t *groups,
@@ -1707,7 +1798,8 @@ int compare_device(CompareJob *job, int *dev) {
 // A persistent grid of resident workgroups, a multiple of 8 (one eighth of
 // the plan per XCD), in runs of up to 32 steps: at most a quarter of each
 // workgroup's share, so that small plans still spread out.  `active` null:
-// the first pass (differ_plan_kernel); else the second (compare_plan_kernel).
+// the first pass (differ_piece_kernel with the plan's chunk table, else
+// differ_plan_kernel); else the second (compare_plan_kernel).
 hipError_t compare_launch(const emrs_plan *plan, const CompareJob &job, const DevSeg *table, const uint32_t *grp,
                           const uint64_t *tab, GroupAcc *acc, const uint8_t *active, hipStream_t st) {
   const size_t nd = plan->segs.size();
@@ -1720,6 +1812,22 @@ hipError_t compare_launch(const emrs_plan *plan, const CompareJob &job, const De
       (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(32 * kUnroll, plan->n_chunks / (blocks * 4)));
   const uint64_t *dtab = tab ? tab + plan->stats.n_src_bufs : nullptr;
   const dim3 grid((uint32_t)blocks), block(kThreads);
+  if (!active && job.cseg) {  // the first pass on the copy kernel's schedule
+    constexpr int U = 4;
+    const uint64_t n_wg = plan->n_chunks * (kChunkUnits / (64 * U));
+    const uint64_t gx = std::min<uint64_t>(n_wg, std::max<uint64_t>(1ull << 16, (n_wg + kMaxGridY - 1) / kMaxGridY));
+    const dim3 pgrid((uint32_t)gx, (uint32_t)((n_wg + gx - 1) / gx));
+    const uint32_t remap = g_tuning.xcd_remap.load();
+    const bool by_xcd = remap == 2 || (remap == 1 && plan->n_chunks >= kXcdRemapMinChunks);
+    const uint64_t xcd_share = by_xcd ? n_wg / 8 : 0;
+    if (job.rb.table)
+      hipLaunchKernelGGL((differ_piece_kernel<true, U>), pgrid, dim3(64), 0, st, table, plan->n_chunks, job.rb.src,
+                         job.rb.dst, tab, dtab, xcd_share, job.cseg, grp, grp + nd, acc);
+    else
+      hipLaunchKernelGGL((differ_piece_kernel<false, U>), pgrid, dim3(64), 0, st, table, plan->n_chunks, job.rb.src,
+                         job.rb.dst, tab, dtab, xcd_share, job.cseg, grp, grp + nd, acc);
+    return hipGetLastError();
+  }
   if (!active) {
     if (job.rb.table)
       hipLaunchKernelGGL(differ_plan_kernel<true>, grid, block, 0, st, table, grp, grp + nd, (uint32_t)nd,
@@ -2173,6 +2281,11 @@ int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_
   bool tab_owned = false;
   int table_rc = EMRS_OK;  // a pointer-table failure keeps its own message
   if (e == hipSuccess) table_rc = pointer_table(plan, dev, job.rb, st, &tab, &tab_owned);
+  if (e == hipSuccess && table_rc == EMRS_OK) {
+    uint32_t *cseg = nullptr;  // null when it does not fit: the first pass then runs as a persistent grid
+    table_rc = chunk_table(plan, dev, st, table, &cseg);
+    job.cseg = cseg;
+  }
   if (e == hipSuccess && table_rc == EMRS_OK)
     e = compare_passes(plan, job, table, grp, tab, acc, active, n_groups, st, host);
   if (tab_owned) (void)hipFreeAsync(tab, st);
@@ -2232,6 +2345,7 @@ int emrs_plan_compare_static(emrs_plan *plan, void *const *src_bases, void *cons
   if (e == hipSuccess && tab)
     e = hipMemcpyAsync(tab, job.rb.ptrs.data(), job.rb.ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice, st);
   std::vector<GroupAcc> host(n_groups);
+  job.cseg = existing_chunk_table(plan, dev);  // never built here: that would allocate
   if (e == hipSuccess) e = compare_passes(plan, job, table, grp, tab, acc, active, n_groups, st, host);
   // The host copies above read job's and plan's vectors: wait before they can go.
   const hipError_t se = hipStreamSynchronize(st);
