@@ -314,6 +314,9 @@ class ElasticMegatronManager:
             raise NotImplementedError("checkpoint saving is not part of the reshard data path")
         dst_strategy = _as_strategy(new_parallel_strategy)
         src_state = self.training_state
+        if src_state.device.type == "meta" and not is_meta_device:
+            raise RuntimeError("the manager was built on the meta device and holds no state yet: "
+                               "attach_training_state first (or reshard with is_meta_device=True)")
         src_strategy = src_state.parallel_strategy
         space = src_state.layout.space
         backup = ParallelStrategy.is_redundant_backup(src_strategy, dst_strategy)

@@ -151,6 +151,12 @@ def test_meta_manager_plans_then_attaches_a_received_state():
     assert len(plans[0].src) == len(state.buffers)
 
 
+def test_meta_manager_refuses_a_real_switch_before_attach():
+    mgr = ElasticMegatronManager([PS(8, 1, 1), PS(8, 2, 1)], small_llama2(), device="meta")
+    with pytest.raises(RuntimeError):
+        mgr.reshard(PS(8, 2, 1))
+
+
 def test_attach_adopts_a_separately_built_model():
     spec = small_llama2()
     src, dst = PS(8, 1, 1), PS(6, 1, 1)
