@@ -183,8 +183,13 @@ int emrs_plan_execute(emrs_plan *plan, void *const *src_bases,
 int emrs_plan_prepare(emrs_plan *plan, void *stream);
 
 /*
- * Free the plan.  It first waits for every device that holds its table, so a
- * plan may be destroyed while launches that use it are still queued.
+ * Free the plan.  Its device tables are freed in stream order after the
+ * launches of emrs_plan_execute that use them (an event recorded after each
+ * launch), so a plan may be destroyed while those launches are still queued;
+ * the call neither blocks the host nor waits for other work on the device.
+ * A plan whose launches were captured into a graph may be replayed at any
+ * time, so for it the call first waits for the whole device; a graph that
+ * holds its launches must not be replayed after the plan is destroyed.
  */
 int emrs_plan_destroy(emrs_plan *plan);
 
