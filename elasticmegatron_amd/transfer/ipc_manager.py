@@ -145,24 +145,29 @@ class SharedTrainingState:
         self._released = [True] * 4
 
     # ----- synthetic workload -----
+    _SYNTH_MAX_BUFFERS = 128   # buffers per emrs_synth_fill / emrs_synth_verify call
+
     def _per_arena(self, pieces: np.ndarray):
-        """The pieces of each arena, addressed by granule within that arena (so that no call
-        passes more granules than one arena has)."""
+        """The pieces of each arena in batches of at most 128 granules, addressed by granule within
+        the batch: (arena, pieces, granule pointers, granule bytes, first granule's buffer id)."""
         pcs = self.buffers.split_pieces(pieces)
+        nbytes = self.buffers.nbytes()
         for a in range(4):
             ids = self.buffers.granules_of(a)
-            sel = pcs[(pcs["buf"] >= ids.start) & (pcs["buf"] < ids.stop)].copy()
-            if len(sel) == 0:
-                continue
-            sel["buf"] -= ids.start
-            yield a, sel, [self._ptrs[b] for b in ids], [self.buffers.nbytes()[b] for b in ids]
+            for lo in range(ids.start, ids.stop, self._SYNTH_MAX_BUFFERS):
+                hi = min(lo + self._SYNTH_MAX_BUFFERS, ids.stop)
+                sel = pcs[(pcs["buf"] >= lo) & (pcs["buf"] < hi)].copy()
+                if len(sel) == 0:
+                    continue
+                sel["buf"] -= lo
+                yield a, sel, self._ptrs[lo:hi], nbytes[lo:hi], lo
 
     def fill_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True) -> None:
         """Write the seeded synthetic values of every stored element (see csrc/synth.hip)."""
         st = torch.cuda.current_stream(self._device).cuda_stream
         with torch.cuda.device(self._device):
-            for _, pcs, ptrs, nb in self._per_arena(self.layout.pieces(params, include_bf16=bf16,
-                                                                        include_fp32=fp32)):
+            for _, pcs, ptrs, nb, _ in self._per_arena(self.layout.pieces(params, include_bf16=bf16,
+                                                                           include_fp32=fp32)):
                 _native.synth_fill(pcs, ptrs, nb, seed, st)
 
     def verify_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True,
@@ -176,13 +181,13 @@ class SharedTrainingState:
         st = torch.cuda.current_stream(self._device).cuda_stream
         bad, first = 0, None
         with torch.cuda.device(self._device):
-            for a, sel, ptrs, nb in self._per_arena(pcs):
+            for a, sel, ptrs, nb, lo in self._per_arena(pcs):
                 n, f = _native.synth_verify(sel, ptrs, nb, seed, st)
                 bad += n
                 if f is not None and first is None:
                     p = sel[f[0]]
                     first = dict(arena=ARENA_NAMES[a], param_id=int(p["param_id"]), kind=int(p["kind"]),
-                                 element=int(f[1]), granule=int(p["buf"]))
+                                 element=int(f[1]), granule=lo + int(p["buf"]))
         return bad, first
 
     # ----- export -----

@@ -146,3 +146,27 @@ def test_hand_off_llama2_7b(gpu_device):
           f"({gb / mgr.last_transfer_ms:.1f} TB/s payload); {time.perf_counter() - t0:.0f} s in all", flush=True)
     bad, first = new.verify_synthetic(SEED)
     assert bad == 0, first
+
+
+def test_manager_keeps_shareable_states_through_a_chain(gpu_device):
+    """share_granule_bytes: every state the manager allocates is held in granules (here 64 KiB, so
+    plans pass more than 128 buffers a side through pointer tables), through a chain of switches
+    with a Group-ZeRO scale-up (bf16 granules shared) and back.  Each hop is verified on the device
+    against the state it replaced, and the end state holds the generator's values."""
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+    from tests.helpers import small_llama2
+
+    seq = [PS(8, 1, 1), PS(8, 4, 1), PS(6, 1, 1), PS(12, 1, 1, num_distributed_optimizer_instances=2),
+           PS(6, 1, 1), PS(8, 2, 2)]
+    mgr = ElasticMegatronManager(seq, small_llama2(), device=gpu_device, share_granule_bytes=1 << 16)
+    st = mgr.training_state
+    assert isinstance(st, SharedTrainingState) and not st.imported and len(st.buffers) > 128
+    st.fill_synthetic(SEED)
+    assert st.verify_synthetic(SEED)[0] == 0
+    for s in seq[1:]:
+        print(f"case shareable chain -> {s}", flush=True)
+        mgr.reshard(s, is_meta_device=True)
+        new = mgr.reshard(s, verify=True)
+        torch.cuda.synchronize()
+        assert isinstance(new, SharedTrainingState) and mgr.last_verification.bit_exact
+        assert new.verify_synthetic(SEED, bf16=True)[0] == 0
