@@ -426,23 +426,10 @@ def main():
         t_v = time.perf_counter()
         report = tm.verify(a, b, kind)
         v_ms = (time.perf_counter() - t_v) * 1e3
-        # The read ceiling of the same bytes in this process: emrs_xor_checksum over every arena the
-        # check reads (placement moves a read-heavy launch by several percent between processes).
-        word = torch.zeros(1, dtype=torch.int32, device=dev)
-        read = [a.main, a.exp_avg, a.exp_avg_sq, b.main, b.exp_avg, b.exp_avg_sq]
-        if backup is None:
-            read.append(b.param)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for t in read:
-            _native.xor_checksum(t.data_ptr(), t.numel() * t.element_size() // 16 * 16, word.data_ptr(),
-                                 stream.cuda_stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        r_ms, r_bytes = read_ceiling(a, b, backup is None, stream)
         out["config"]["plan_verification"] = {
             "bit_exact": report.bit_exact, "elements": report.elements, "wall_ms": round(v_ms, 3),
-            "read_ceiling_ms": round(e0.elapsed_time(e1), 3),
-            "read_ceiling_bytes": sum(t.numel() * t.element_size() // 16 * 16 for t in read)}
+            "read_ceiling_ms": round(r_ms, 3), "read_ceiling_bytes": r_bytes}
         if not report.bit_exact:
             print(f"[bench] plan verification FAILED: {report.lines()[:3]}", file=sys.stderr)
             return 3
@@ -880,6 +867,25 @@ def launch_shape():
             "piece_bytes": 16 * t.lanes * t.units, "chunk_index": t.chunk_index, "warm_tables": t.warm_tables,
             "xcd_remap": t.xcd_remap,
             "buffer_ops": t.buffer_ops, "nontemporal": t.nontemporal}
+
+
+def read_ceiling(a, b, with_param, stream):
+    """(ms, bytes) of emrs_xor_checksum over every arena the verification reads, in this process: the
+    placement of the arenas moves a read-heavy launch by several percent between processes."""
+    import torch
+
+    from elasticmegatron_amd import _native
+
+    word = torch.zeros(1, dtype=torch.int32, device=a.main.device)
+    arenas = [a.main, a.exp_avg, a.exp_avg_sq, b.main, b.exp_avg, b.exp_avg_sq] + ([b.param] if with_param else [])
+    spans = [(t.data_ptr(), t.numel() * t.element_size() // 16 * 16) for t in arenas]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for p, n in spans:
+        _native.xor_checksum(p, n, word.data_ptr(), stream.cuda_stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1), sum(n for _, n in spans)
 
 
 def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):

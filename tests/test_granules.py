@@ -9,6 +9,8 @@ inside one-row and strided segments, bf16 images and duplicates.
 
 import numpy as np
 import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from elasticmegatron_amd import _native
 from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy as PS
@@ -18,6 +20,7 @@ from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lowe
 from elasticmegatron_amd.resharding.tensors import rebase_on_tensors
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from tests.helpers import SEED, SMALL_CASES, execute_numpy, new_arenas, piece_fill_numpy, small_llama2
+from tests.test_plan_properties import _lowered, switches
 
 # Granule sizes as (source, destination) numbers of granules per fp32 arena; None: whole arenas.
 GRANULES = [(37, 41), (23, None), (None, 29), (3, 64)]
@@ -155,3 +158,23 @@ def test_empty_table():
     gt, origin = rebase_on_tensors(np.zeros(0, dtype=SEGMENT_DTYPE), GranuleBuffers(lay, 4096),
                                    GranuleBuffers(lay, 4096), return_origin=True)
     assert len(gt) == 0 and len(origin) == 0
+
+
+@st.composite
+def _granule_switches(draw):
+    spec, a, b = draw(switches())
+    # Granule sizes in 256-byte steps, from a few KB (boundaries inside most segments) up to a
+    # size that holds a whole arena; None keeps whole arenas on that side.
+    sizes = st.one_of(st.none(), st.integers(1, 400).map(lambda k: 256 * k), st.integers(1, 64).map(lambda k: 4096 * k))
+    return spec, a, b, draw(sizes), draw(sizes)
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.filter_too_much, HealthCheck.too_slow])
+@given(_granule_switches())
+def test_random_granules_write_what_the_arena_plan_writes(sw):
+    """Random models, switches and granule sizes on either side: the re-based plan, run on
+    separate granule arrays, writes exactly what the arena plan writes."""
+    spec, a, b, gs, gd = sw
+    space = build_virtual_model(spec)
+    la, lb, table = _lowered(space, a, b)
+    _run(la, lb, table, gs, gd)
