@@ -627,13 +627,13 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
     from elasticmegatron_amd.megatron_manager.training_state import TrainingState
     from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
     from elasticmegatron_amd.transfer import ipc_manager as ipc
-    from elasticmegatron_amd.transfer.transfer import TransferManager
+    from elasticmegatron_amd.transfer.transfer import TransferManager, backup_kind
 
+    # A Group-ZeRO switch copies the bf16 params here: the exporter frees its memory.
     backup = ParallelStrategy.is_redundant_backup(src, dst)
+    kind = "transfer" if backup is None else backup_kind(backup, copy_bf16=True)
     if backup is not None:
-        print("bench.py --ipc: a Group-ZeRO switch keeps the bf16 params in place and cannot start from a "
-              "received state", file=sys.stderr)
-        return 2
+        desc = desc.replace(", fp32 only", "") + ", fp32 and the bf16 params copied"
     spec = spec_fn()
     space = build_virtual_model(spec)
     ls, ld = space.layout(src), space.layout(dst)
@@ -645,8 +645,8 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
     state = None
     try:
         tm = TransferManager(bf16_source=args.bf16_source)
-        plan = tm.compile_granules(ls, ld, args.ipc_granule_bytes, None)
-        arena_plan = tm.compile(ls, ld)
+        plan = tm.compile_granules(ls, ld, args.ipc_granule_bytes, None, kind)
+        arena_plan = tm.compile(ls, ld, kind)
         b = TrainingState.allocate(ld, dev)
         if not select.select([child.stdout], [], [], 600)[0]:
             print("bench.py --ipc: the exporting process sent nothing in 600 s", file=sys.stderr)
@@ -671,7 +671,7 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
         verified = None
         if not args.no_verify:
             bad, first = b.verify_synthetic(SEED)
-            report = tm.verify(state, b)
+            report = tm.verify(state, b, kind)
             verified = bad == 0 and report.bit_exact
             if not verified:
                 print(f"[bench] verification FAILED: {bad} elements, first {first}; "

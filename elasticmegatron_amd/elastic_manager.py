@@ -36,7 +36,7 @@ from .resharding.model_spec import ModelSpec
 from .resharding.util import Timer
 from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
 from .transfer.ipc_manager import SharedTrainingState
-from .transfer.transfer import TransferManager, _granule_of
+from .transfer.transfer import TransferManager, _granule_of, backup_kind, shares_params
 from .transfer.verify import merge_stats, report_from_stats
 
 StrategyLike = Union[ParallelStrategy, Dict[str, int]]
@@ -238,10 +238,11 @@ class ElasticMegatronManager:
     def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool,
                          is_meta_device: bool = False) -> float:
         """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
-        ``is_meta_device`` plans, caches and uploads the plan's tables without moving data.  Returns
-        the executor's ms."""
-        plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst),
-                                                     "backup_up" if is_scale_up else "backup_down")
+        ``is_meta_device`` plans, caches and uploads the plan's tables without moving data.  The
+        bf16 params stay where they are when ``dst`` shares ``src``'s, and are copied otherwise.
+        Returns the executor's ms."""
+        kind = backup_kind(is_scale_up, not shares_params(src, dst))
+        plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst), kind)
         if is_meta_device:
             self._prepare(plan, src)
         with Timer() as t:
@@ -252,14 +253,15 @@ class ElasticMegatronManager:
     @staticmethod
     def _carried_params(src_state, dst_granule_bytes):
         """The bf16 params a Group-ZeRO switch carries over unchanged: the source's own param arena
-        (or granules), which the new state shares."""
+        (or granules), which the new state shares.  None when the new state cannot share them: the
+        source was received from another process, which frees it, or the two states are held
+        differently (arenas and granules, or granules of two sizes); the switch then copies them."""
         if isinstance(src_state, TrainingState) and dst_granule_bytes is None:
             return src_state.param
         if isinstance(src_state, SharedTrainingState) and not src_state.imported and \
                 src_state.granule_bytes == dst_granule_bytes:
             return [src_state.tensors[b] for b in src_state.buffers.granules_of(3)]
-        raise NotImplementedError("a Group-ZeRO switch keeps the bf16 params in place: source and destination "
-                                  "must be states of the same kind, and a received state cannot be kept")
+        return None
 
     def log_communication_info(self, transfer_time: float, union_world_group=None,
                                logger: Optional[logging.Logger] = None) -> str:
@@ -324,18 +326,17 @@ class ElasticMegatronManager:
         dst_layout = dst_space.layout(dst_strategy)
         if backup is None and dst_space is space:
             space.register_reshard(src_strategy, dst_strategy)
-        kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
         gs = _granule_of(src_state)
         gd = self.share_granule_bytes if src_state.device.type != "meta" else None
+        # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over
+        # (or are copied, when the new state cannot share them).
+        param = self._carried_params(src_state, gd) if backup is not None else None
+        kind = "transfer" if backup is None else backup_kind(backup, param is None)
         plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind)
         stages = self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind) if self.low_memory else ()
         if is_meta_device:
             self._prepare(stages or plan, src_state)
             return None
-        # Under Group ZeRO the model-parallel shards are unchanged, so the bf16 params carry over.
-        param = None
-        if backup is not None:
-            param = self._carried_params(src_state, gd)
         report = None
         if self.low_memory:
             dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),

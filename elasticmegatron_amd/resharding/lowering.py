@@ -278,7 +278,8 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
     return _assemble(fp32.table(), bf16.table(), fp32.group_array(), bf16.group_array(), with_groups)
 
 
-def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False):
+def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False,
+                           copy_bf16: bool = False):
     """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
 
     On a scale-up every new instance of a shard is filled from instance 0's
@@ -286,12 +287,20 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     taken in pairs, each pair as one duplicating segment: the shard is read
     once per two copies written.
 
+    The model-parallel shards are the same on both sides, so the bf16 params
+    normally carry over in place (the new state shares the old one's param
+    arena).  ``copy_bf16`` is for a destination that cannot share it, such
+    as one built from another process's state, which that process frees: the
+    bf16 params are then copied shard by shard, the same bits the shared
+    arena would hold (4 bytes of traffic per parameter).
+
     ``with_groups``: as for :func:`lower_transfer`.
     """
     space = src.space
     if src.strategy.optimizer_data_parallel_size != dst.strategy.optimizer_data_parallel_size:
         raise AssertionError("Group-ZeRO switch must keep the optimizer DP size")
     b = SegmentBuilder()
+    bf16 = SegmentBuilder()
     for vp in space.all_virtual_params:
         if not (src.has_param(vp) and dst.has_param(vp)):
             continue
@@ -311,8 +320,14 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
                 b.add(0, 0, 4, s.offset, hs[i].offset, n, 1, 0, 0, aux=(0, hs[i + 1].offset, 0), group=g, dup=True)
             if len(hs) % 2:
                 b.add(0, 0, 4, s.offset, hs[-1].offset, n, 1, 0, 0, group=g)
-    return _assemble(b.table(), np.zeros(0, dtype=SEGMENT_DTYPE), b.group_array(), np.zeros(0, dtype=np.int64),
-                     with_groups)
+        if copy_bf16:
+            src_bf = {h.tp_rank: h for h in src.bf16_holders(vp)}
+            for h in dst.bf16_holders(vp):
+                s = src_bf.get(h.tp_rank)
+                if s is None or (s.lo, s.hi) != (h.lo, h.hi):
+                    raise AssertionError(f"{vp.name}: no matching source bf16 shard for a Group-ZeRO copy")
+                bf16.add(ARENA_PARAM, ARENA_PARAM, 2, s.offset, h.offset, h.hi - h.lo, 1, 0, 0, group=g)
+    return _assemble(b.table(), bf16.table(), b.group_array(), bf16.group_array(), with_groups)
 
 
 # Largest interleaved piece: 64 MiB of fp32.  Timed on the same arenas in one process, pieces of

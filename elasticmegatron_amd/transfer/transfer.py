@@ -52,6 +52,28 @@ class CompiledPlan:
         return self.payload_bytes + self.read_bytes
 
 
+# Group-ZeRO kinds: (scale-up, bf16 params copied).  Without the copy the new state shares the old
+# one's bf16 params; with it the new state holds its own.
+BACKUP_KINDS = {"backup_up": (True, False), "backup_down": (False, False),
+                "backup_up_bf16": (True, True), "backup_down_bf16": (False, True)}
+
+
+def backup_kind(scale_up: bool, copy_bf16: bool = False) -> str:
+    """The plan kind of a Group-ZeRO switch."""
+    return ("backup_up" if scale_up else "backup_down") + ("_bf16" if copy_bf16 else "")
+
+
+def _lower(src: StrategyLayout, dst: StrategyLayout, kind: str, include_bf16: bool, bf16_source: str,
+           with_groups: bool = False):
+    """The segment table of a plan kind (with groups for verification)."""
+    if kind == "transfer":
+        return lower_transfer(src, dst, include_bf16=include_bf16, bf16_source=bf16_source, with_groups=with_groups)
+    if kind in BACKUP_KINDS:
+        up, copy = BACKUP_KINDS[kind]
+        return lower_redundant_backup(src, dst, scale_up=up, with_groups=with_groups, copy_bf16=copy)
+    raise ValueError(kind)
+
+
 def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
     """The model the reference would run a switch in: it keeps the padded vocabulary fixed
     (virtual_param.py:480-481), so a re-padding switch is priced in whichever of the two
@@ -151,19 +173,14 @@ class TransferManager:
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        if kind == "transfer":
-            table = lower_transfer(src, dst, include_bf16=include_bf16, bf16_source=self.bf16_source)
-        elif kind in ("backup_up", "backup_down"):
-            table = lower_redundant_backup(src, dst, scale_up=kind == "backup_up")
-        else:
-            raise ValueError(kind)
+        table = _lower(src, dst, kind, include_bf16, self.bf16_source)
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
         if kind == "transfer":
             space = _fixed_padding_space(src, dst)
             comm = max(reference_comm_bytes(space, src.strategy, dst.strategy).values(), default=0) \
                 if space is not None else 0
-        elif kind == "backup_up":  # every rank joins the broadcast of its whole shard (transfer.py:377-388)
+        elif BACKUP_KINDS[kind][0]:  # every rank joins the broadcast of its whole shard (transfer.py:377-388)
             comm = max(dst.rank_numel) * FP32_TENSORS_BYTES
         else:  # param_migrate is a local copy (training_state.py:40-60)
             comm = 0
@@ -390,14 +407,7 @@ class TransferManager:
                gs, gd)
         vp = self._verify_plans.get(key)
         if vp is None:
-            if kind == "transfer":
-                table, groups, aux_groups = lower_transfer(sl, dl, include_bf16=include_bf16,
-                                                           bf16_source=self.bf16_source, with_groups=True)
-            elif kind in ("backup_up", "backup_down"):
-                table, groups, aux_groups = lower_redundant_backup(sl, dl, scale_up=kind == "backup_up",
-                                                                   with_groups=True)
-            else:
-                raise ValueError(kind)
+            table, groups, aux_groups = _lower(sl, dl, kind, include_bf16, self.bf16_source, with_groups=True)
             if stage is not None:
                 m = _stage_mask(table, stage)
                 table, groups, aux_groups = table[m], groups[m], aux_groups[m]
@@ -444,8 +454,10 @@ class TransferManager:
 
     def redundant_backup(self, is_scale_up: bool, src: TrainingState, dst: TrainingState,
                          stream=None) -> CompiledPlan:
-        """Group-ZeRO switch (transfer.py:343-388): fp32 shards replicated or dropped."""
-        plan = self.compile(src.layout, dst.layout, "backup_up" if is_scale_up else "backup_down")
+        """Group-ZeRO switch (transfer.py:343-388): fp32 shards replicated or dropped.  As in the
+        reference, only the optimizer tensors move; ``ElasticMegatronManager`` also copies the bf16
+        params when the new state cannot share them."""
+        plan = self.compile(src.layout, dst.layout, backup_kind(is_scale_up))
         self.execute(plan, src, dst, stream)
         return plan
 
@@ -469,6 +481,18 @@ class TransferManager:
 def _granule_of(state) -> Optional[int]:
     """Granule size of a shared state's arenas; None for a TrainingState's whole arenas."""
     return None if isinstance(state, TrainingState) else state.granule_bytes
+
+
+def shares_params(src, dst) -> bool:
+    """Whether ``dst`` holds its bf16 params in ``src``'s memory, as a state built for a Group-ZeRO
+    switch normally does (the switch then leaves them in place)."""
+    def param_ptrs(state):
+        ptrs = _buffers_of(state)[0]
+        if isinstance(state, TrainingState):
+            return [ptrs[ARENA_PARAM]]
+        return [ptrs[b] for b in state.buffers.granules_of(ARENA_PARAM)]
+
+    return param_ptrs(src) == param_ptrs(dst)
 
 
 def _buffers_of(state):

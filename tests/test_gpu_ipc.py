@@ -170,3 +170,24 @@ def test_manager_keeps_shareable_states_through_a_chain(gpu_device):
         torch.cuda.synchronize()
         assert isinstance(new, SharedTrainingState) and mgr.last_verification.bit_exact
         assert new.verify_synthetic(SEED, bf16=True)[0] == 0
+
+
+def test_hand_off_group_zero_copies_the_params(gpu_device):
+    """A Group-ZeRO scale-up (one optimizer instance -> two, config 5b's switch on the small model)
+    from another process's granules.  The exporter frees its memory, so the new state gets its own
+    copy of the bf16 params.  fp32 state bit-exact against Oracle-1's redundant backup, bf16 params
+    against the generator, and the switch checked on the device against the mapped source."""
+    from oracle import model
+    from oracle import transfer as oracle1
+    from tests.helpers import small_llama2
+
+    spec, src, dst = small_llama2(), PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
+    print(f"case hand-off {spec.name} {src} -> {dst}", flush=True)
+    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, spec, src, dst, (1 << 20) + 256 * 3, 240)
+    print(f"  {n_granules} granules in {n_mapped} allocations; switch {mgr.last_transfer_ms:.3f} ms", flush=True)
+    assert new.verify_synthetic(SEED, fp32=False)[0] == 0
+    inv = model.inventory(spec)
+    world = oracle1.build_src_world(inv, spec, strat(src), SEED)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, strat(src), strat(dst), world, True))
+    got32, _ = extract(new.layout, _host_arenas(new))
+    assert compare(got32, {}, want, {}) == []

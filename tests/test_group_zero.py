@@ -17,7 +17,7 @@ from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, payl
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from oracle import model
 from oracle import transfer as oracle1
-from tests.helpers import SEED, compare, execute_numpy, extract, new_arenas, piece_fill_numpy, small_llama2, strat
+from tests.helpers import SEED, compare, compare_numpy, execute_numpy, extract, new_arenas, piece_fill_numpy, small_llama2, strat
 
 CASES = [
     ("1to2", PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
@@ -76,3 +76,40 @@ def test_duplicates_land_in_their_own_kind():
     dup = table[(table["flags"] & SEG_DUP) != 0]
     assert np.array_equal(dup["aux_buf"], dup["dst_buf"])
     assert set(np.unique(dup["dst_buf"]).tolist()) == {0, 1, 2}
+
+
+@pytest.mark.parametrize("up", [True, False], ids=["up", "down"])
+@pytest.mark.parametrize("name,small,big", CASES, ids=[c[0] for c in CASES])
+def test_bf16_copy_writes_the_generator_params(name, small, big, up):
+    """A destination that cannot share the source's bf16 params (one built from another process's
+    state) gets them copied: every bf16 element equals the generator's value for its full index,
+    the fp32 arenas are what the shared-params plan writes, and the copy reads and writes each
+    stored param element once."""
+    src, dst = (small, big) if up else (big, small)
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(src), space.layout(dst)
+    plain = lower_redundant_backup(ls, ld, up)
+    table = lower_redundant_backup(ls, ld, up, copy_bf16=True)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    b, c = new_arenas(ld), new_arenas(ld)
+    execute_numpy(table, a, b)
+    execute_numpy(plain, a, c)
+    for k in range(3):
+        assert np.array_equal(b[k], c[k])
+    want = new_arenas(ld)
+    piece_fill_numpy(ld.pieces(include_fp32=False), want, SEED)
+    assert np.array_equal(b[3], want[3])
+    stored = sum(h.hi - h.lo for vp in space.all_virtual_params if ld.has_param(vp) for h in ld.bf16_holders(vp))
+    assert payload_bytes(table) - payload_bytes(plain) == 2 * stored
+    assert read_bytes(table) - read_bytes(plain) == 2 * stored
+    # The grouped plan of the same switch checks the copied params too (kind 0 of each parameter).
+    tg, groups, aux_groups = lower_redundant_backup(ls, ld, up, with_groups=True, copy_bf16=True)
+    n_groups = 4 * len(space.all_virtual_params)
+    stats = compare_numpy(tg, groups, aux_groups, n_groups, a, b)
+    assert int(stats["mismatches"].sum()) == 0
+    assert int(stats["elements"][0::4].sum()) == stored
+    h = ld.bf16_holders(space.all_virtual_params[3])[0]
+    b[3][h.offset + 5] ^= 1
+    stats = compare_numpy(tg, groups, aux_groups, n_groups, a, b)
+    assert np.flatnonzero(stats["mismatches"]).tolist() == [4 * 3]

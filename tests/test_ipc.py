@@ -168,13 +168,24 @@ def test_attach_adopts_a_separately_built_model():
     assert mgr.reshard(dst, is_meta_device=True) is None
 
 
-def test_group_zero_from_a_received_state_is_refused():
+def test_group_zero_from_a_received_state_copies_the_params():
+    """The exporter frees a received state's memory, bf16 params included, so a Group-ZeRO switch from
+    it cannot leave them in place: its plan copies them into the new state's own granules."""
     spec = small_llama2()
     src, dst = PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
     mgr = ElasticMegatronManager([src, dst], spec, device="meta")
-    mgr.attach_training_state(_fake_shared(mgr.virtual_param_space.layout(src), 1 << 16))
-    with pytest.raises(NotImplementedError):
-        mgr.reshard(dst)
+    state = _fake_shared(mgr.virtual_param_space.layout(src), 1 << 16)
+    mgr.attach_training_state(state)
+    assert mgr.reshard(dst, is_meta_device=True) is None
+    plans = [(k, p) for k, p in mgr.transfer_manager._plans.items() if k[0] == "granules"]
+    assert len(plans) == 1 and plans[0][0][5] == "backup_up_bf16"
+    table = plans[0][1].segments
+    param = set(state.buffers.granules_of(3))
+    bf16 = table[np.isin(table["src_buf"], list(param))]
+    assert len(bf16) and (bf16["elem_bytes"] == 2).all()
+    stored = sum(h.hi - h.lo for vp in mgr.virtual_param_space.all_virtual_params
+                 for h in state.layout.bf16_holders(vp))
+    assert int((bf16["len"].astype(np.int64) * bf16["rows"]).sum()) == stored
 
 
 def test_low_memory_refuses_shared_states():
