@@ -385,18 +385,8 @@ def main():
     if tplan is not None:
         # The arena plan on the same allocations in this process, alternating with the per-tensor
         # plan, so that the two compare without the spread of placements between processes.
-        rounds = {"tensors": [], "arenas": []}
-        for _ in range(3):
-            for name, run in (("tensors", lambda: step(a, b)), ("arenas", lambda: tm.execute(plan, a, b, stream))):
-                run()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                for _ in range(5):
-                    run()
-                e1.record(stream)
-                torch.cuda.synchronize()
-                rounds[name].append(round(e0.elapsed_time(e1) / 5, 4))
-        out["config"]["same_process_ms"] = rounds
+        out["config"]["same_process_ms"] = alternate_rounds(
+            {"tensors": lambda: step(a, b), "arenas": lambda: tm.execute(plan, a, b, stream)}, stream)
     if args.placement_trials:
         import gc
 
@@ -678,6 +668,9 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
                       f"{report.lines()[:3]}", file=sys.stderr)
                 return 3
         n_granules = len(state.buffers)
+        owned = mapped_vs_owned(args, tm, plan, ls, state, b, dev, stream)
+        if owned.get("verified_bit_exact") is False:
+            return 3
     finally:
         if state is not None:
             state.close()
@@ -704,13 +697,43 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
         "config": {"workload": desc + f", from another process's state in {args.ipc_granule_bytes}-byte granules",
                    "params": spec.num_params(), "payload_bytes": plan.payload_bytes, "granules": n_granules,
                    "segments": int(plan.segments.shape[0]), "verified_bit_exact": verified,
-                   "exporter_exit_status": child.returncode,
+                   "exporter_exit_status": child.returncode, "mapped_vs_owned": owned,
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def mapped_vs_owned(args, tm, plan, ls, mapped, b, dev, stream):
+    """The granule plan from the mapped source and from a source of the same granules allocated in
+    this process, taking turns on the same destination: what reading another process's memory
+    costs, without the spread of placements between processes.  Skipped when the second source
+    does not fit beside the first."""
+    import gc
+
+    import torch
+
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+
+    need = sum(mapped.buffers.nbytes())
+    free = torch.cuda.mem_get_info(dev)[0]
+    if free < need + (4 << 30):
+        return {"skipped": f"a second source of {need} bytes does not fit in {free} free bytes"}
+    owned = SharedTrainingState.allocate(ls, dev, args.ipc_granule_bytes)
+    try:
+        owned.fill_synthetic(SEED)
+        rounds = alternate_rounds({"mapped": lambda: tm.execute_states(plan, mapped, b, stream),
+                                   "owned": lambda: tm.execute_states(plan, owned, b, stream)}, stream)
+        rounds["verified_bit_exact"] = None if args.no_verify else b.verify_synthetic(SEED)[0] == 0
+    finally:
+        del owned
+        gc.collect()
+        torch.cuda.empty_cache()
+    if rounds["verified_bit_exact"] is False:
+        print("[bench] the switch from the owned source differs from the generator", file=sys.stderr)
+    return rounds
 
 
 def shape_sweep(args, desc, tm, plan, a, b, backup, vocab_rows, stream):
@@ -867,6 +890,26 @@ def launch_shape():
             "piece_bytes": 16 * t.lanes * t.units, "chunk_index": t.chunk_index, "warm_tables": t.warm_tables,
             "xcd_remap": t.xcd_remap,
             "buffer_ops": t.buffer_ops, "nontemporal": t.nontemporal}
+
+
+def alternate_rounds(runs, stream, rounds=3, reps=5):
+    """{name: [ms per launch of each round]}: each run's ``reps`` launches after one untimed one,
+    the runs taking turns for ``rounds`` rounds, so that they compare on the same allocations in
+    one process, without the spread of placements between processes."""
+    import torch
+
+    out = {name: [] for name in runs}
+    for _ in range(rounds):
+        for name, run in runs.items():
+            run()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                run()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            out[name].append(round(e0.elapsed_time(e1) / reps, 4))
+    return out
 
 
 def read_ceiling(a, b, with_param, stream):
