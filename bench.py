@@ -259,6 +259,8 @@ def main():
         return copy_calibration(args, dev, stream)
 
     desc, spec_fn, src, dst, *opt = workloads()[args.workload]
+    if args.low_memory and args.ipc:
+        return bench_ipc_staged(args, desc, spec_fn, src, dst, dev)
     if args.low_memory:
         return bench_low_memory(args, desc, spec_fn, src, dst, dev)
     if args.megatron_buffers:
@@ -607,10 +609,6 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
     ipc_manager.py:54-155): a child process allocates the source in granules, fills it and sends
     the payload; this process maps the granules and times the switch from them into its own
     arenas.  The mappings are closed before the child is told to exit."""
-    import dataclasses
-    import select
-    import subprocess
-
     import torch
 
     from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
@@ -627,23 +625,15 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
     spec = spec_fn()
     space = build_virtual_model(spec)
     ls, ld = space.layout(src), space.layout(dst)
-    child = subprocess.Popen(
-        [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_export", "--model-spec",
-         json.dumps(dataclasses.asdict(spec)), "--strategy", json.dumps(ipc.strategy_to_dict(src)), "--seed",
-         str(SEED), "--granule-bytes", str(args.ipc_granule_bytes)],
-        cwd=ROOT, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
+    child = spawn_exporter(spec, src, args.ipc_granule_bytes)
     state = None
     try:
         tm = TransferManager(bf16_source=args.bf16_source)
         plan = tm.compile_granules(ls, ld, args.ipc_granule_bytes, None, kind)
         arena_plan = tm.compile(ls, ld, kind)
         b = TrainingState.allocate(ld, dev)
-        if not select.select([child.stdout], [], [], 600)[0]:
-            print("bench.py --ipc: the exporting process sent nothing in 600 s", file=sys.stderr)
-            return 1
-        line = child.stdout.readline()
-        if not line:
-            print(f"bench.py --ipc: the exporting process exited with {child.wait()}", file=sys.stderr)
+        line = exporter_payload(child)
+        if line is None:
             return 1
         state, _ = ipc.receive_training_state(line, dev, space=space)
         print(f"[bench] {args.workload}: {len(state.buffers)} granules mapped, {plan.segments.shape[0]} segments",
@@ -672,19 +662,7 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
         if owned.get("verified_bit_exact") is False:
             return 3
     finally:
-        if state is not None:
-            state.close()
-        if child.poll() is None:
-            try:
-                ipc.notify_release(child.stdin)
-                child.stdin.close()
-            except BrokenPipeError:
-                pass
-            try:
-                child.wait(timeout=120)
-            except subprocess.TimeoutExpired:
-                child.kill()
-                child.wait()
+        end_exporter(child, state)
     step_ms = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = sum(step_ms) / len(step_ms)
     traffic_gbps = arena_plan.traffic_bytes / (ms / 1e3) / 1e9
@@ -701,6 +679,146 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def spawn_exporter(spec, strategy, granule_bytes):
+    """The exporting process of a hand-off: a child that allocates the state of ``strategy`` in
+    granules, fills it with the seeded values and sends the payload on its stdout."""
+    import dataclasses
+    import subprocess
+
+    from elasticmegatron_amd.transfer import ipc_manager as ipc
+
+    return subprocess.Popen(
+        [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_export", "--model-spec",
+         json.dumps(dataclasses.asdict(spec)), "--strategy", json.dumps(ipc.strategy_to_dict(strategy)), "--seed",
+         str(SEED), "--granule-bytes", str(granule_bytes)],
+        cwd=ROOT, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
+
+
+def exporter_payload(child, timeout_s=600):
+    """The payload line the exporter sends, or None (reported) when it sends nothing."""
+    import select
+
+    if not select.select([child.stdout], [], [], timeout_s)[0]:
+        print(f"bench.py --ipc: the exporting process sent nothing in {timeout_s} s", file=sys.stderr)
+        return None
+    line = child.stdout.readline()
+    if not line:
+        print(f"bench.py --ipc: the exporting process exited with {child.wait()}", file=sys.stderr)
+        return None
+    return line
+
+
+def end_exporter(child, state):
+    """Close what is still mapped, then tell the exporter to free its memory and wait for it."""
+    import subprocess
+
+    from elasticmegatron_amd.transfer import ipc_manager as ipc
+
+    if state is not None:
+        state.close()
+    if child.poll() is None:
+        try:
+            ipc.notify_release(child.stdin)
+            child.stdin.close()
+        except BrokenPipeError:
+            pass
+        try:
+            child.wait(timeout=120)
+        except subprocess.TimeoutExpired:
+            child.kill()
+            child.wait()
+
+
+def bench_ipc_staged(args, desc, spec_fn, src, dst, dev):
+    """A staged switch (ElasticMegatronManager(low_memory=True)) from another process's state: after
+    each optimizer kind's launch the source arena's mappings are closed and the exporter frees it
+    before the next kind's destination arena is allocated, so the device holds the source, the
+    destination's bf16 params and one fp32 arena at most.  The switch consumes its source, so one
+    switch is timed per run, its plans prepared on the meta-device pass beforehand."""
+    import logging
+
+    import torch
+
+    from elasticmegatron_amd import ElasticMegatronManager
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
+    from elasticmegatron_amd.transfer import ipc_manager as ipc
+    from elasticmegatron_amd.transfer.transfer import backup_kind
+
+    quiet = logging.getLogger("bench.reshard")
+    quiet.addHandler(logging.NullHandler())
+    quiet.propagate = False
+    spec = spec_fn()
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta", low_memory=True)
+    child = spawn_exporter(spec, src, args.ipc_granule_bytes)
+    state, free_before_release = None, []
+    try:
+        line = exporter_payload(child)
+        if line is None:
+            return 1
+        state, _ = ipc.receive_training_state(line, dev, space=mgr.virtual_param_space)
+        hook = ipc.release_hook(child.stdin, child.stdout)
+
+        def on_release(kind):
+            free_before_release.append(torch.cuda.mem_get_info(dev)[0])
+            hook(kind)
+
+        state.on_release = on_release
+        n_granules = len(state.buffers)
+        mgr.attach_training_state(state)
+        mgr.reshard(dst, is_meta_device=True)
+        # A received state cannot keep its bf16 params: a Group-ZeRO switch copies them.
+        backup = ParallelStrategy.is_redundant_backup(src, dst)
+        kind = "transfer" if backup is None else backup_kind(backup, copy_bf16=True)
+        plans = mgr.transfer_manager.staged_for_states(state.layout, mgr.space_for(dst).layout(dst),
+                                                       state.granule_bytes, None, kind)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        new = mgr.reshard(dst, logger=quiet)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t) * 1e3
+        state = None
+        stages = mgr.last_stage_ms
+        bad = None
+        if not args.no_verify:
+            bad, first = new.verify_synthetic(SEED)
+            if bad:
+                print(f"[bench] verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+                return 3
+        peak_here = torch.cuda.max_memory_allocated(dev)
+    finally:
+        end_exporter(child, state)
+    total = torch.cuda.get_device_properties(dev).total_memory
+    payload = sum(p.payload_bytes for p in plans)
+    traffic = sum(p.payload_bytes + p.read_bytes for p in plans)
+    launch_ms = sum(s["execute"] for s in stages)
+    kern = traffic / (launch_ms / 1e3) / 1e9
+    ls = mgr.space_for(src).layout(src)
+    src_bytes = 3 * ls.fp32_numel * 4 + ls.bf16_numel * 2
+    out = {
+        "metric": metric_for(args.workload, desc), "value": round(payload / (wall / 1e3) / 1e9, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": 1, "warmup": 0, "ms_per_step": round(wall, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
+        "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
+        "config": {"workload": desc + f", from another process's state in {args.ipc_granule_bytes}-byte granules, "
+                               "staged: one optimizer kind per launch, each source arena freed by the exporter "
+                               "after its launch",
+                   "params": spec.num_params(), "payload_bytes": payload, "granules": n_granules,
+                   "launch_ms": round(launch_ms, 4), "stages_ms": stages,
+                   "source_state_bytes": src_bytes, "peak_allocated_here_bytes": int(peak_here),
+                   "device_used_before_each_release_bytes": [int(total - f) for f in free_before_release],
+                   "device_bytes": int(total), "verified_bit_exact": None if bad is None else bad == 0,
+                   "exporter_exit_status": child.returncode,
+                   "step": "one whole switch through ElasticMegatronManager.reshard: per optimizer kind, the "
+                           "destination arena's allocation, its launch, the close of the source arena's "
+                           "mappings and the exporter's free of it"},
+        "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(kern / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "note": "algorithmic bytes over the launches' time, allocation and release excluded"},
     }
     print(json.dumps(out), flush=True)
     return 0

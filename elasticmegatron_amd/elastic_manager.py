@@ -66,6 +66,10 @@ class ElasticMegatronManager:
         then allocated in 1 GiB granules, so that the memory a released source arena leaves serves
         the next destination arena without a call to the driver (a state passed in
         ``training_state`` should be allocated with ``granule_bytes=ARENA_GRANULE_BYTES`` too).
+        The source may be a state received from another process: each of its fp32 arenas is
+        unmapped after its stage, and the state's ``on_release`` hook
+        (:func:`~.transfer.ipc_manager.release_hook`) has the exporting process free that arena
+        before the next stage allocates.
 
         ``share_granule_bytes``: the states this manager allocates are
         :class:`~.transfer.ipc_manager.SharedTrainingState` objects with granules of that size, so that the
@@ -99,8 +103,8 @@ class ElasticMegatronManager:
         self.release_source = release_source
         self.low_memory = low_memory
         self.share_granule_bytes = share_granule_bytes
-        if low_memory and (share_granule_bytes is not None or isinstance(training_state, SharedTrainingState)):
-            raise NotImplementedError("staged switches run on TrainingState arenas, not on shared granules")
+        if low_memory and share_granule_bytes is not None:
+            raise NotImplementedError("staged switches write TrainingState arenas, not shared granules")
         self.last_stage_ms: List[Dict[str, float]] = []   # staged switches: per stage, allocate / execute ms
         self.last_transfer_ms = 0.0
         self.last_verification = None
@@ -126,8 +130,6 @@ class ElasticMegatronManager:
         spec = state.layout.space.spec
         if spec != self._spec_for(state.parallel_strategy):
             raise ValueError("the state was laid out for another model")
-        if self.low_memory and isinstance(state, SharedTrainingState):
-            raise NotImplementedError("staged switches run on TrainingState arenas, not on shared granules")
         space = state.layout.space
         if space is not self._spaces.get(spec.padded_vocab_size):
             # Adopt the state's virtual model, built for every strategy of the list it serves.
@@ -208,19 +210,21 @@ class ElasticMegatronManager:
 
         ``dst`` may start without fp32 arenas; each is allocated just before its stage.  With
         ``release_source`` the source arena of each kind is released right after its stage, once
-        it has been checked when ``verify`` is set.  Returns (executor ms summed over the stages,
-        verification records or None).
+        it has been checked when ``verify`` is set.  ``src`` may be held in granules (a shared or
+        received state).  Returns (ms of the stages' allocation, launch and release, summed;
+        verification records or None); ``last_stage_ms`` has each stage's three times.
         """
         if kind == "transfer" and src.layout.space is dst.layout.space:
             src.layout.space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
-        stages = self.transfer_manager.compile_staged(src.layout, dst.layout, kind)
+        stages = self.transfer_manager.staged_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst),
+                                                         kind)
         elapsed, stats, names = 0.0, None, None
         self.last_stage_ms = []
         for k, plan in enumerate(stages):
             with Timer() as ta:
                 dst.allocate_kind(k)
             with Timer() as te:
-                self.transfer_manager.execute(plan, src, dst)
+                self.transfer_manager.execute_states(plan, src, dst)
             elapsed += ta.elapsed + te.elapsed
             self.last_stage_ms.append({"allocate": ta.elapsed, "execute": te.elapsed})
             if verify:
@@ -231,8 +235,11 @@ class ElasticMegatronManager:
                     raise RuntimeError(f"reshard verification failed in stage {k} "
                                        f"({('main', 'exp_avg', 'exp_avg_sq')[k]}): "
                                        + "\n".join(report_from_stats(stats, names).lines()[:20]))
-            if self.release_source:
-                src.release_kind(k)
+            with Timer() as tr:
+                if self.release_source:
+                    src.release_kind(k)
+            elapsed += tr.elapsed
+            self.last_stage_ms[-1]["release"] = tr.elapsed
         return elapsed, (stats, names) if verify else None
 
     def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool,
@@ -333,7 +340,8 @@ class ElasticMegatronManager:
         param = self._carried_params(src_state, gd) if backup is not None else None
         kind = "transfer" if backup is None else backup_kind(backup, param is None)
         plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind)
-        stages = self.transfer_manager.compile_staged(src_state.layout, dst_layout, kind) if self.low_memory else ()
+        stages = self.transfer_manager.staged_for_states(src_state.layout, dst_layout, gs, gd, kind) \
+            if self.low_memory else ()
         if is_meta_device:
             self._prepare(stages or plan, src_state)
             return None

@@ -7,7 +7,10 @@ Stands in for the old training process of a hand-off (the reference's
 send_training_state, elastic_megatron/transfer/ipc_manager.py:54-132): it
 allocates a :class:`~.ipc_manager.SharedTrainingState`, fills it with the
 seeded synthetic values, writes the payload as one line on stdout, and keeps
-the memory until a release notice arrives on stdin (or stdin closes).
+the memory until a release notice arrives on stdin (or stdin closes).  An
+arena's own release notice (a staged switch releases the source arena by
+arena) frees that arena's granules and is answered on stdout once the memory
+is back with the driver.
 """
 
 import json
@@ -18,9 +21,10 @@ import torch
 
 from ..megatron_manager.parallel_strategy import ParallelStrategy
 from ..resharding.granules import DEFAULT_GRANULE_BYTES
+from ..resharding.layout import ARENA_NAMES
 from ..resharding.model_spec import ModelSpec
 from ..resharding.virtual_param import build_virtual_model
-from .ipc_manager import SharedTrainingState, send_training_state, wait_for_release
+from .ipc_manager import SharedTrainingState, notify_freed, send_training_state, wait_for_release
 
 
 def main(argv: Sequence[str]) -> int:
@@ -44,7 +48,15 @@ def main(argv: Sequence[str]) -> int:
     state.fill_synthetic(args.seed)
     print(f"[exporter] {len(state.buffers)} granules of {layout.strategy} filled", file=sys.stderr, flush=True)
     send_training_state(state, sys.stdout, misc=json.loads(args.misc))
-    released = wait_for_release(sys.stdin)
+
+    def free_arena(name: str) -> None:
+        state.release_kind(ARENA_NAMES.index(name))
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        print(f"[exporter] {name} freed", file=sys.stderr, flush=True)
+        notify_freed(sys.stdout, name)
+
+    released = wait_for_release(sys.stdin, on_arena=free_arena)
     print(f"[exporter] {'released' if released else 'channel closed'}; exiting", file=sys.stderr, flush=True)
     return 0
 

@@ -30,7 +30,7 @@ from __future__ import annotations
 
 import dataclasses
 import json
-from typing import IO, Dict, List, Optional, Sequence, Tuple, Union
+from typing import IO, Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
@@ -43,6 +43,7 @@ from ..resharding.model_spec import ModelSpec
 
 PAYLOAD_FORMAT = "emrs-shared-state/1"
 RELEASED = "released"
+FREED = "freed"
 _STRATEGY_FIELDS = ("world_size", "tensor_model_parallel_size", "pipeline_model_parallel_size",
                     "context_parallel_size", "num_distributed_optimizer_instances", "expert_model_parallel_size",
                     "expert_tensor_parallel_size", "sequence_parallel")
@@ -70,7 +71,10 @@ class SharedTrainingState:
         self._device = torch.device(device)
         self.tensors = tensors          # owned granules; None when imported
         self._open = tensors is None    # imported mappings not yet closed
-        self._released = [False] * 4    # per arena
+        self._released = [False] * 4    # per arena: freed (owned) or unmapped (imported)
+        # Imported states: called with an arena's index once its mappings are closed, so that the
+        # exporting process can free that arena (see :func:`release_hook`).
+        self.on_release: Optional[Callable[[int], None]] = None
 
     # ----- construction -----
     @classmethod
@@ -111,9 +115,10 @@ class SharedTrainingState:
         return self.tensors is None
 
     def buffer_ptrs(self) -> List[int]:
+        """Base pointer of every granule; 0 for the granules of a released arena."""
         if self.imported and not self._open:
             raise RuntimeError("the shared state's mappings are closed")
-        return list(self._ptrs)
+        return [0 if self._released[a] else p for a, p in zip(self.buffers.arena, self._ptrs)]
 
     def buffer_bytes(self) -> List[int]:
         """Bytes of every granule; 0 for the granules of a released arena."""
@@ -121,6 +126,28 @@ class SharedTrainingState:
         return [0 if self._released[a] else n for a, n in zip(self.buffers.arena, nb)]
 
     # ----- lifetime -----
+    def release_kind(self, kind: int) -> None:
+        """Release fp32 arena ``kind`` (0 main, 1 exp_avg, 2 exp_avg_sq), as a staged switch does
+        once that arena is copied (the reference releases each optimizer tensor once it is sent,
+        resharding_metadata.py:58-65).  Owned granules are freed.  An imported state's granules of
+        that arena are unmapped (after the device has finished with them), then ``on_release`` is
+        called so that the exporting process can free them."""
+        if kind not in (0, 1, 2):
+            raise ValueError("release_kind takes an fp32 arena: 0 main, 1 exp_avg, 2 exp_avg_sq")
+        if self._released[kind]:
+            return
+        if not self.imported:
+            for b in self.buffers.granules_of(kind):
+                self.tensors[b].untyped_storage().resize_(0)
+            self._released[kind] = True
+            return
+        if not self._open:
+            return
+        self._unmap(self.buffers.granules_of(kind))
+        self._released[kind] = True
+        if self.on_release is not None:
+            self.on_release(kind)
+
     def release_optimizer(self) -> None:
         """Drop the fp32 state (training_state.py:313-315): owned granules are freed, and an
         imported state is unmapped whole (its bf16 params went to the new state with the switch)."""
@@ -128,19 +155,20 @@ class SharedTrainingState:
             self.close()
             return
         for a in range(3):
-            for b in self.buffers.granules_of(a):
-                self.tensors[b].untyped_storage().resize_(0)
-            self._released[a] = True
+            self.release_kind(a)
 
-    def close(self) -> None:
-        """Unmap every granule of an imported state (emrs_ipc_close).  Waits for the device first,
-        so work that still reads the mappings has finished."""
-        if not self.imported or not self._open:
-            return
+    def _unmap(self, granules) -> None:
         with torch.cuda.device(self._device):
             torch.cuda.synchronize(self._device)
-            for p in self._ptrs:
-                _native.ipc_close(p)
+            for b in granules:
+                _native.ipc_close(self._ptrs[b])
+
+    def close(self) -> None:
+        """Unmap every granule of an imported state still mapped (emrs_ipc_close).  Waits for the
+        device first, so work that still reads the mappings has finished."""
+        if not self.imported or not self._open:
+            return
+        self._unmap([b for b, a in enumerate(self.buffers.arena) if not self._released[a]])
         self._open = False
         self._released = [True] * 4
 
@@ -288,17 +316,50 @@ def receive_training_state(source: Union[Dict, IO[str], str], device=None, space
     return SharedTrainingState(layout, bufs, ptrs, dev), payload.get("misc", {})
 
 
-def notify_release(wfile: IO[str]) -> None:
-    """Tell the exporting process that this process has closed its mappings."""
-    wfile.write(RELEASED + "\n")
+def notify_release(wfile: IO[str], arena: Optional[str] = None) -> None:
+    """Tell the exporting process that this process has closed its mappings: all of them, or with
+    ``arena`` those of that arena only (a staged switch releases the source arena by arena)."""
+    wfile.write((RELEASED if arena is None else f"{RELEASED} {arena}") + "\n")
     wfile.flush()
 
 
-def wait_for_release(rfile: IO[str]) -> bool:
-    """Block until the importer's release notice (True) or the end of the channel (False)."""
+def wait_for_release(rfile: IO[str], on_arena: Optional[Callable[[str], None]] = None) -> bool:
+    """Block until the importer's release notice (True) or the end of the channel (False).
+    ``on_arena(name)`` is called for each fp32 arena the importer releases before that."""
     while True:
         line = rfile.readline()
         if not line:
             return False
-        if line.strip() == RELEASED:
+        words = line.split()
+        if words == [RELEASED]:
             return True
+        if len(words) == 2 and words[0] == RELEASED and words[1] in ARENA_NAMES[:3] and on_arena is not None:
+            on_arena(words[1])
+
+
+def notify_freed(wfile: IO[str], arena: str) -> None:
+    """The exporter's answer to an arena's release notice: its memory is back with the driver."""
+    wfile.write(f"{FREED} {arena}\n")
+    wfile.flush()
+
+
+def wait_for_freed(rfile: IO[str], arena: str) -> bool:
+    """Block until the exporter has freed ``arena`` (True) or the channel ends (False)."""
+    while True:
+        line = rfile.readline()
+        if not line:
+            return False
+        if line.split() == [FREED, arena]:
+            return True
+
+
+def release_hook(wfile: IO[str], rfile: IO[str]) -> Callable[[int], None]:
+    """``SharedTrainingState.on_release`` for a received state: tells the exporter over ``wfile``
+    that an arena's mappings are closed and waits on ``rfile`` until it has freed that arena, so
+    that the next stage of a staged switch can allocate in its place."""
+    def release(arena: int) -> None:
+        name = ARENA_NAMES[arena]
+        notify_release(wfile, name)
+        if not wait_for_freed(rfile, name):
+            raise RuntimeError(f"the exporting process ended before it freed {name}")
+    return release

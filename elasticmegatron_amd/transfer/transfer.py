@@ -119,10 +119,14 @@ class CompiledTensorPlan:
     read_bytes: int
     buffer_nbytes: list = None   # bytes of every source, then every destination buffer
     reference_comm_bytes: int = 0
+    src_refs: Tuple[int, ...] = None   # buffers the plan reads
+    dst_refs: Tuple[int, ...] = None   # buffers the plan writes
 
     def __post_init__(self):
         if self.buffer_nbytes is None:
             self.buffer_nbytes = self.src.nbytes() + self.dst.nbytes()
+        if self.src_refs is None:
+            self.src_refs, self.dst_refs = _arena_refs(self.segments)
 
 
 class TransferManager:
@@ -324,6 +328,29 @@ class TransferManager:
         self._plans[key] = cp
         return cp
 
+    def staged_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
+                          dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True):
+        """The three plans of :meth:`compile_staged`, re-based onto granules when either side is held
+        in them (a staged switch from a received state)."""
+        stages = self.compile_staged(src_layout, dst_layout, kind, include_bf16)
+        if src_granule_bytes is None and dst_granule_bytes is None:
+            return stages
+        key = ("staged-granules", src_layout.space.spec, src_layout.strategy, dst_layout.space.spec,
+               dst_layout.strategy, kind, include_bf16, self.bf16_source, src_granule_bytes, dst_granule_bytes)
+        got = self._plans.get(key)
+        if got is not None:
+            return got
+        sb, db = GranuleBuffers(src_layout, src_granule_bytes), GranuleBuffers(dst_layout, dst_granule_bytes)
+        out = []
+        for st in stages:
+            table = rebase_on_tensors(st.segments, sb, db)
+            out.append(CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint),
+                                          sb, db, payload_bytes(table), read_bytes(table),
+                                          reference_comm_bytes=st.reference_comm_bytes))
+        got = tuple(out)
+        self._plans[key] = got
+        return got
+
     def plan_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
                         dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True):
         """The arena plan when both sides are whole arenas, else the granule plan."""
@@ -345,10 +372,13 @@ class TransferManager:
             raise RuntimeError("source and destination states must be on one GPU")
         sp, sn = _buffers_of(src)
         dp, dn = _buffers_of(dst)
-        for have, need, side in ((sn, plan.src.nbytes(), "source"), (dn, plan.dst.nbytes(), "destination")):
-            if len(have) != len(need) or any(h < n for h, n in zip(have, need)):
-                raise ValueError(f"the {side} state's buffers do not match the plan (released, or laid out "
-                                 "for another granule size)")
+        # Buffers the plan does not touch may be empty: a staged switch allocates the destination's
+        # arenas and releases the source's one at a time.
+        for have, need, refs, side in ((sn, plan.src.nbytes(), plan.src_refs, "source"),
+                                       (dn, plan.dst.nbytes(), plan.dst_refs, "destination")):
+            if len(have) != len(need) or any(have[i] < need[i] for i in refs):
+                raise ValueError(f"the {side} state's buffers do not match the plan (released, not yet "
+                                 "allocated, or laid out for another granule size)")
         st = stream if stream is not None else torch.cuda.current_stream(src.device)
         with torch.cuda.device(src.device):
             plan.native.execute(sp, dp, st.cuda_stream)

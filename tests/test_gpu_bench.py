@@ -59,3 +59,16 @@ def test_ipc_line(gpu_device):
     d = _bench("--ipc", "--ipc-granule-bytes", str(3 << 22), "--steps", "2", "--warmup", "1")
     assert d["config"]["verified_bit_exact"] is True and d["config"]["exporter_exit_status"] == 0
     assert d["config"]["granules"] > 4 and d["ms_per_step"] > 0
+    assert set(d["config"]["mapped_vs_owned"]) == {"mapped", "owned", "verified_bit_exact"}
+    assert d["config"]["mapped_vs_owned"]["verified_bit_exact"] is True
+
+
+@pytest.mark.gpu
+def test_ipc_staged_line(gpu_device):
+    """--ipc --low-memory: one staged switch from a child's granules, each source arena freed by the
+    child after its launch, the destination checked afterwards."""
+    d = _bench("--ipc", "--low-memory", "--ipc-granule-bytes", str(3 << 22))
+    c = d["config"]
+    assert c["verified_bit_exact"] is True and c["exporter_exit_status"] == 0
+    assert [sorted(s) for s in c["stages_ms"]] == [["allocate", "execute", "release"]] * 3
+    assert len(c["device_used_before_each_release_bytes"]) == 3 and d["steps"] == 1

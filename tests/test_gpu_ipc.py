@@ -191,3 +191,41 @@ def test_hand_off_group_zero_copies_the_params(gpu_device):
     want = oracle1.flatten(oracle1.redundant_backup(inv, spec, strat(src), strat(dst), world, True))
     got32, _ = extract(new.layout, _host_arenas(new))
     assert compare(got32, {}, want, {}) == []
+
+
+def test_staged_hand_off_frees_the_source_arena_by_arena(gpu_device):
+    """A staged switch (low_memory) from another process's granules, config 1's first switch: after
+    each stage the source arena's mappings are closed and the exporter frees that arena before the
+    next stage allocates (release_hook).  Each stage verified on the device before its release, the
+    whole bit-exact against Oracle-1."""
+    from oracle import model
+    from oracle import transfer as oracle1
+
+    spec, src, dst = tiny_llama2(), PS(8, 2, 1), PS(8, 1, 1)
+    print(f"case staged hand-off {spec.name} {src} -> {dst}", flush=True)
+    child = _spawn_exporter(spec, src, 3 * (1 << 22) + 256 * 7)
+    state = None
+    try:
+        mgr = ElasticMegatronManager([src, dst], spec, device="meta", low_memory=True)
+        line = _payload_line(child, 240)
+        state, _ = ipc.receive_training_state(line, gpu_device, space=mgr.virtual_param_space)
+        mapped = _native.ipc_open_count()
+        state.on_release = ipc.release_hook(child.stdin, child.stdout)
+        mgr.attach_training_state(state)
+        assert mgr.reshard(dst, is_meta_device=True) is None
+        new = mgr.reshard(dst, verify=True)
+        torch.cuda.synchronize()
+        assert mgr.last_verification.bit_exact
+        assert [sorted(s) for s in mgr.last_stage_ms] == [["allocate", "execute", "release"]] * 3
+        assert _native.ipc_open_count() == 0
+        print(f"  {len(state.buffers)} granules in {mapped} allocations; stages {mgr.last_stage_ms}", flush=True)
+        state = None
+    finally:
+        rc = _finish(child, state)
+        print(f"  exporter exit status {rc}", flush=True)
+    assert rc == 0
+    inv = model.inventory(spec)
+    world = oracle1.build_src_world(inv, spec, strat(src), SEED)
+    dw, dbf, _ = oracle1.transfer(inv, spec, strat(src), strat(dst), world)
+    got32, gotbf = extract(new.layout, _host_arenas(new))
+    assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []

@@ -178,3 +178,37 @@ def test_random_granules_write_what_the_arena_plan_writes(sw):
     space = build_virtual_model(spec)
     la, lb, table = _lowered(space, a, b)
     _run(la, lb, table, gs, gd)
+
+
+@pytest.mark.parametrize("kind,src,dst", [
+    ("transfer", PS(8, 2, 1), PS(8, 1, 1)),
+    ("backup_up_bf16", PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
+], ids=["transfer", "groupzero-bf16-copy"])
+def test_staged_granule_plans_split_the_granule_plan_by_kind(kind, src, dst):
+    """A staged switch from a received state: stage k reads only the source granules of fp32 arena k
+    (stage 0 also the bf16 params, when they are copied), writes only destination arena k (stage 0
+    also the bf16 params), and the three stages in turn write what the whole granule plan writes."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    gs = _granule_bytes(ls, 37)
+    whole = tm.compile_granules(ls, ld, gs, None, kind)
+    stages = tm.staged_for_states(ls, ld, gs, None, kind)
+    assert tm.staged_for_states(ls, ld, gs, None, kind) is stages
+    sb = whole.src
+    for k, p in enumerate(stages):
+        allowed = {k, 3} if k == 0 else {k}
+        assert {sb.arena[i] for i in p.src_refs} <= allowed
+        assert set(p.dst_refs) <= allowed and k in set(p.dst_refs)
+    assert sum(p.payload_bytes for p in stages) == whole.payload_bytes
+    assert sum(p.read_bytes for p in stages) == whole.read_bytes
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    want, got = new_arenas(ld, fill=0), new_arenas(ld, fill=0)
+    execute_numpy(whole.segments, _split(sb, a), want)
+    for p in stages:
+        execute_numpy(p.segments, _split(sb, a), got)
+    for x, y in zip(got, want):
+        assert np.array_equal(x, y)

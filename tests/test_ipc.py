@@ -188,7 +188,44 @@ def test_group_zero_from_a_received_state_copies_the_params():
     assert int((bf16["len"].astype(np.int64) * bf16["rows"]).sum()) == stored
 
 
-def test_low_memory_refuses_shared_states():
+def test_low_memory_refuses_to_allocate_shared_states():
     with pytest.raises(NotImplementedError):
         ElasticMegatronManager([PS(8, 1, 1)], small_llama2(), device="meta", low_memory=True,
                                share_granule_bytes=1 << 20)
+
+
+def test_arena_release_protocol():
+    """A staged switch from a received state releases the source arena by arena: the importer's
+    notice names the arena, the exporter frees it and answers, and the final notice ends the wait."""
+    import io
+
+    to_exporter, to_importer = io.StringIO(), io.StringIO()
+    to_importer.write("noise\n")
+    ipc.notify_freed(to_importer, "main")
+    ipc.notify_freed(to_importer, "exp_avg")
+    to_importer.seek(0)
+    hook = ipc.release_hook(to_exporter, to_importer)
+    hook(0)
+    hook(1)
+    with pytest.raises(RuntimeError):
+        hook(2)                      # the exporter never answered: the channel ended
+    ipc.notify_release(to_exporter)
+    freed = []
+    assert ipc.wait_for_release(io.StringIO(to_exporter.getvalue()), on_arena=freed.append) is True
+    assert freed == ["main", "exp_avg", "exp_avg_sq"]
+    # Only fp32 arenas are released one at a time.
+    assert ipc.wait_for_release(io.StringIO("released param\nreleased\n"), on_arena=freed.append) is True
+    assert freed == ["main", "exp_avg", "exp_avg_sq"]
+
+
+def test_staged_manager_accepts_a_received_state():
+    """low_memory with a received source: the staged plans are re-based onto its granules."""
+    spec = small_llama2()
+    src, dst = PS(8, 2, 1), PS(8, 4, 1)
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta", low_memory=True)
+    state = _fake_shared(mgr.virtual_param_space.layout(src), 1 << 16)
+    mgr.attach_training_state(state)
+    assert mgr.reshard(dst, is_meta_device=True) is None
+    staged = [p for k, p in mgr.transfer_manager._plans.items() if k[0] == "staged-granules"]
+    assert len(staged) == 1 and len(staged[0]) == 3
+    assert all(isinstance(p, CompiledTensorPlan) and len(p.src) == len(state.buffers) for p in staged[0])
