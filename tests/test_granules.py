@@ -177,6 +177,12 @@ def test_random_granules_write_what_the_arena_plan_writes(sw):
     spec, a, b, gs, gd = sw
     space = build_virtual_model(spec)
     la, lb, table = _lowered(space, a, b)
+    if max(len(GranuleBuffers(la, gs)), len(GranuleBuffers(lb, gd))) > _native.EMRS_MAX_BUFFERS:
+        # More granules on a side than a plan can address: refused when the plan is made.
+        with pytest.raises(_native.EmrsError) as e:
+            _run(la, lb, table, gs, gd)
+        assert e.value.code == -7    # EMRS_ERR_TOO_MANY_BUFFERS
+        return
     _run(la, lb, table, gs, gd)
 
 
