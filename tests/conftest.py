@@ -7,6 +7,14 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# The property tests draw the same examples on every run, so that a run of the suite is
+# repeatable; broader searches run the same strategies with more examples outside the suite.
+# Loaded before the test modules are imported: their @settings inherit it.
+from hypothesis import settings as _hypothesis_settings  # noqa: E402
+
+_hypothesis_settings.register_profile("repeatable", derandomize=True, database=None)
+_hypothesis_settings.load_profile("repeatable")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X)")
