@@ -193,15 +193,26 @@ def test_hand_off_group_zero_copies_the_params(gpu_device):
     assert compare(got32, {}, want, {}) == []
 
 
-def test_staged_hand_off_frees_the_source_arena_by_arena(gpu_device):
-    """A staged switch (low_memory) from another process's granules, config 1's first switch: after
-    each stage the source arena's mappings are closed and the exporter frees that arena before the
-    next stage allocates (release_hook).  Each stage verified on the device before its release, the
-    whole bit-exact against Oracle-1."""
+def _staged_cases():
+    from tests.helpers import small_llama2
+
+    return [pytest.param(tiny_llama2, PS(8, 2, 1), PS(8, 1, 1), id="tiny-tp2dp4-tp1dp8"),
+            pytest.param(small_llama2, PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2),
+                         id="small-groupzero-1-2")]
+
+
+@pytest.mark.parametrize("factory,src,dst", _staged_cases())
+def test_staged_hand_off_frees_the_source_arena_by_arena(gpu_device, factory, src, dst):
+    """A staged switch (low_memory) from another process's granules: config 1's first switch, and a
+    Group-ZeRO scale-up, whose bf16 params are copied in the first stage.  After each stage the
+    source arena's mappings are closed and the exporter frees that arena before the next stage
+    allocates (release_hook).  Each stage verified on the device before its release; the fp32 state
+    (and for the switch the bf16 params) bit-exact against Oracle-1, the Group-ZeRO bf16 params
+    against the generator."""
     from oracle import model
     from oracle import transfer as oracle1
 
-    spec, src, dst = tiny_llama2(), PS(8, 2, 1), PS(8, 1, 1)
+    spec = factory()
     print(f"case staged hand-off {spec.name} {src} -> {dst}", flush=True)
     child = _spawn_exporter(spec, src, 3 * (1 << 22) + 256 * 7)
     state = None
@@ -226,6 +237,11 @@ def test_staged_hand_off_frees_the_source_arena_by_arena(gpu_device):
     assert rc == 0
     inv = model.inventory(spec)
     world = oracle1.build_src_world(inv, spec, strat(src), SEED)
-    dw, dbf, _ = oracle1.transfer(inv, spec, strat(src), strat(dst), world)
     got32, gotbf = extract(new.layout, _host_arenas(new))
-    assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []
+    if dst.num_distributed_optimizer_instances == 1:
+        dw, dbf, _ = oracle1.transfer(inv, spec, strat(src), strat(dst), world)
+        assert compare(got32, gotbf, oracle1.flatten(dw), dbf) == []
+    else:
+        want = oracle1.flatten(oracle1.redundant_backup(inv, spec, strat(src), strat(dst), world, True))
+        assert compare(got32, {}, want, {}) == []
+        assert new.verify_synthetic(SEED, fp32=False)[0] == 0
