@@ -19,7 +19,7 @@ from tests.helpers import SEED
 from tests.test_random_switches import _random_strategy
 
 pytestmark = pytest.mark.gpu
-N_CASES = 12
+N_CASES = 40
 
 
 def _medium_spec(rng, k):
