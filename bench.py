@@ -1055,9 +1055,11 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
 
     - a plain contiguous copy of the source main arena into the destination one, by copy_plan_kernel;
     - write-only: the same kernel zero-filling the destination main arena (no reads), with one
-      workgroup per 4 KB chunk whatever the launch shape: a workgroup that only stores 1 KB is so
-      short that the rate of launching workgroups, not the memory, would bound the figure;
+      workgroup per 4 KB chunk whatever the launch shape (a workgroup that only stores 1 KB is so
+      short that the rate of launching workgroups, not the memory, would bound the figure), in the
+      faster of two shapes: 64 lanes of four units or 256 lanes of one;
     - read-only: emrs_xor_checksum over the source main arena (no writes);
+    - both main arenas read together, as a comparison reads them: the plan check of that copy;
     - the workload's own read and write bytes moved one direction after the other at those two
       rates, a figure a kernel that overlaps reads with writes can beat.
     """
@@ -1090,13 +1092,29 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
     shape = dict(blocks_per_cu=tu.blocks_per_cu, nontemporal=bool(tu.nontemporal), xcd_remap=tu.xcd_remap,
                  run=tu.run, persistent=bool(tu.persistent), lanes=tu.lanes, buffer_ops=bool(tu.buffer_ops),
                  chunk_index=bool(tu.chunk_index), warm_tables=bool(tu.warm_tables))
-    _native.set_tuning(**shape, units=0)  # one workgroup per chunk
+    w_shapes = {}
     try:
-        w_ms = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
+        for name, lanes, units in (("64x4", 64, 0), ("256x1", 256, 1)):   # one workgroup per chunk
+            _native.set_tuning(**dict(shape, lanes=lanes), units=units)
+            w_shapes[name] = timed(lambda: fill.execute([a.main.data_ptr()], [b.main.data_ptr()], stream.cuda_stream))
     finally:
         _native.set_tuning(**shape, units=tu.units)
+    w_ms = min(w_shapes.values())
     word = torch.zeros(1, dtype=torch.int32, device=a.main.device)
     r_ms = timed(lambda: _native.xor_checksum(a.main.data_ptr(), n * 4, word.data_ptr(), stream.cuda_stream))
+    # Reading both arenas together, as a comparison does: the plan's own check of the contiguous
+    # copy just made (the destination now equals the source, so only its bit-level pass runs).
+    both = [a.main.data_ptr()], [b.main.data_ptr()]
+    copy.execute(*both, stream.cuda_stream)     # the write-only pass zeroed the destination
+    if int(copy.compare(*both, stream=stream.cuda_stream)["mismatches"][0]):
+        raise RuntimeError("the contiguous copy differs from its source")
+    two = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        copy.compare(*both, stream=stream.cuda_stream)
+        two.append((time.perf_counter() - t0) * 1e3)
+    two_ms = sorted(two)[len(two) // 2]
     gbps = 2 * n * 4 / (ms / 1e3) / 1e9
     w_gbps, r_gbps = n * 4 / (w_ms / 1e3) / 1e9, n * 4 / (r_ms / 1e3) / 1e9
     serial = (read_bytes + write_bytes) / (read_bytes / r_gbps + write_bytes / w_gbps)
@@ -1104,6 +1122,10 @@ def copy_ceiling(a, b, stream, traffic_gbps, read_bytes, write_bytes, reps=5):
             "what": "one contiguous copy of the main arena by copy_plan_kernel, same allocations",
             "reshard_frac_of_copy": round(traffic_gbps / gbps, 4),
             "read_only_gbps": round(r_gbps, 1), "write_only_gbps": round(w_gbps, 1),
+            "write_only_gbps_by_shape": {k: round(n * 4 / (v / 1e3) / 1e9, 1) for k, v in w_shapes.items()},
+            "two_arena_read_gbps": round(2 * n * 4 / (two_ms / 1e3) / 1e9, 1),
+            "two_arena_read_what": "emrs_plan_compare of the contiguous copy (source and destination main arenas "
+                                   "read together; wall time, median of the repetitions)",
             "serial_read_then_write_gbps": round(serial, 1),
             "reshard_frac_of_serial": round(traffic_gbps / serial, 4)}
 

@@ -247,28 +247,35 @@ int launch(bool verify, const emrs_piece *pieces, uint64_t n, void *const *bases
 
 namespace {
 
-// XOR of every 32-bit word of a buffer, read as the copy kernel reads: eight
-// 16-byte non-temporal loads in flight per lane, chunks of 256 lanes x 8
-// units dealt out grid-stride.  One atomic per wavefront at the end.
+// XOR of every 32-bit word of a buffer: the plain read rate of the device.
+// One-wavefront workgroups, eight per CU, each with four 16-byte non-temporal
+// loads in flight per lane over 4 KB pieces dealt out grid-stride; one atomic
+// per workgroup at the end.  Timed on 32-72 GiB buffers, this shape read at
+// 7.1-7.3 TB/s where 256-lane workgroups with eight loads per lane, five per
+// CU, read at 6.7-6.8 TB/s; 16 or 32 workgroups per CU read slower
+// (6.3-6.4 TB/s), as did 128 or 256 lanes with four loads each (6.7-6.8).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kXorUnroll = 8;
-constexpr uint64_t kXorChunk = (uint64_t)kThreads * kXorUnroll;
+constexpr int kXorLanes = 64;
+constexpr int kXorUnroll = 4;
+constexpr int kXorBlocksPerCu = 8;
+constexpr uint64_t kXorPiece = (uint64_t)kXorLanes * kXorUnroll;   // units per workgroup step
 
-__global__ __launch_bounds__(kThreads) void xor_checksum_kernel(const u32x4 *__restrict__ p, uint64_t n_units,
+__global__ __launch_bounds__(kXorLanes) void xor_checksum_kernel(const u32x4 *__restrict__ p, uint64_t n_units,
                                                                  uint32_t *__restrict__ out) {
   uint32_t acc = 0;
-  for (uint64_t base = (uint64_t)blockIdx.x * kXorChunk; base < n_units; base += (uint64_t)gridDim.x * kXorChunk) {
+  const uint64_t step = (uint64_t)gridDim.x * kXorPiece;
+  for (uint64_t base = (uint64_t)blockIdx.x * kXorPiece; base < n_units; base += step) {
     u32x4 v[kXorUnroll];
 #pragma unroll
     for (int j = 0; j < kXorUnroll; ++j) {
-      const uint64_t i = base + (uint64_t)j * kThreads + threadIdx.x;
+      const uint64_t i = base + (uint64_t)j * kXorLanes + threadIdx.x;
       v[j] = i < n_units ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int j = 0; j < kXorUnroll; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   for (int off = 32; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off, 64);
-  if (threadIdx.x % 64 == 0 && acc) atomicXor(out, acc);
+  if (threadIdx.x == 0 && acc) atomicXor(out, acc);
 }
 
 }  // namespace
@@ -290,9 +297,9 @@ extern "C" int emrs_xor_checksum(const void *p, uint64_t bytes, uint32_t *out, v
   if (e != hipSuccess) return sfail(EMRS_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
   const uint64_t n_units = bytes / 16;
   if (n_units == 0) return EMRS_OK;
-  // Five resident workgroups per CU, as the copy kernel runs.
-  const uint64_t blocks = std::min<uint64_t>((n_units + kXorChunk - 1) / kXorChunk, (uint64_t)std::max(cus, 1) * 5);
-  hipLaunchKernelGGL(xor_checksum_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, st,
+  const uint64_t blocks =
+      std::min<uint64_t>((n_units + kXorPiece - 1) / kXorPiece, (uint64_t)std::max(cus, 1) * kXorBlocksPerCu);
+  hipLaunchKernelGGL(xor_checksum_kernel, dim3((uint32_t)blocks), dim3(kXorLanes), 0, st,
                      static_cast<const u32x4 *>(p), n_units, out);
   e = hipGetLastError();
   if (e != hipSuccess) return sfail(EMRS_ERR_HIP, std::string("xor_checksum_kernel launch: ") + hipGetErrorString(e));

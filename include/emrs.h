@@ -363,9 +363,9 @@ int emrs_synth_verify(const emrs_piece *pieces, uint64_t n_pieces,
 /*
  * XOR of every 32-bit word of the device buffer [p, p + bytes) into the
  * device word *out (zeroed first), enqueued on `stream`.  p and bytes must be
- * multiples of 16.  The buffer is read as the copy kernel reads its sources,
- * so the call also measures this device's read-only HBM bandwidth.  No
- * counterpart in the reference.
+ * multiples of 16.  The buffer is read with 16-byte non-temporal loads in
+ * the fastest read schedule found on MI355X, so the call also measures the
+ * device's read-only HBM bandwidth.  No counterpart in the reference.
  */
 int emrs_xor_checksum(const void *p, uint64_t bytes, uint32_t *out, void *stream);
 
