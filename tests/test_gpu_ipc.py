@@ -68,16 +68,21 @@ def _finish(child, state):
 
 
 def _host_arenas(state):
-    return [t.view(torch.int32).cpu().numpy().view("uint32") for t in (state.main, state.exp_avg, state.exp_avg_sq)] \
-        + [state.param.view(torch.int16).cpu().numpy().view("uint16")]
+    if isinstance(state, ipc.SharedTrainingState):   # the granules of each arena, joined
+        arenas = [torch.cat([state.tensors[b] for b in state.buffers.granules_of(a)]) for a in range(4)]
+    else:
+        arenas = [state.main, state.exp_avg, state.exp_avg_sq, state.param]
+    return [t.view(torch.int32).cpu().numpy().view("uint32") for t in arenas[:3]] \
+        + [arenas[3].view(torch.int16).cpu().numpy().view("uint16")]
 
 
-def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s):
-    """Export in a child, receive, attach and reshard; returns (manager, new state, granules, mapped)."""
+def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s, share=None):
+    """Export in a child, receive, attach and reshard; returns (manager, new state, granules, mapped).
+    ``share``: the new state is held in granules of that size too."""
     child = _spawn_exporter(spec, src, granule_bytes)
     state = None
     try:
-        mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+        mgr = ElasticMegatronManager([src, dst], spec, device="meta", share_granule_bytes=share)
         assert mgr.reshard(dst, is_meta_device=True) is None
         line = _payload_line(child, timeout_s)
         print(f"  payload received ({len(line)} bytes)", flush=True)
@@ -172,18 +177,21 @@ def test_manager_keeps_shareable_states_through_a_chain(gpu_device):
         assert new.verify_synthetic(SEED, bf16=True)[0] == 0
 
 
-def test_hand_off_group_zero_copies_the_params(gpu_device):
+@pytest.mark.parametrize("share", [None, (1 << 20) + 256 * 5], ids=["into-arenas", "into-granules"])
+def test_hand_off_group_zero_copies_the_params(gpu_device, share):
     """A Group-ZeRO scale-up (one optimizer instance -> two, config 5b's switch on the small model)
-    from another process's granules.  The exporter frees its memory, so the new state gets its own
-    copy of the bf16 params.  fp32 state bit-exact against Oracle-1's redundant backup, bf16 params
-    against the generator, and the switch checked on the device against the mapped source."""
+    from another process's granules, into arenas or into granules of another size.  The exporter
+    frees its memory, so the new state gets its own copy of the bf16 params.  fp32 state bit-exact
+    against Oracle-1's redundant backup, bf16 params against the generator, and the switch checked
+    on the device against the mapped source."""
     from oracle import model
     from oracle import transfer as oracle1
     from tests.helpers import small_llama2
 
     spec, src, dst = small_llama2(), PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
-    print(f"case hand-off {spec.name} {src} -> {dst}", flush=True)
-    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, spec, src, dst, (1 << 20) + 256 * 3, 240)
+    print(f"case hand-off {spec.name} {src} -> {dst}, new state in granules of {share}", flush=True)
+    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, spec, src, dst, (1 << 20) + 256 * 3, 240, share)
+    assert isinstance(new, ipc.SharedTrainingState) == (share is not None)
     print(f"  {n_granules} granules in {n_mapped} allocations; switch {mgr.last_transfer_ms:.3f} ms", flush=True)
     assert new.verify_synthetic(SEED, fp32=False)[0] == 0
     inv = model.inventory(spec)
