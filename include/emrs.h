@@ -35,8 +35,11 @@
  *     of the last failure on the calling thread.
  *   - Work is enqueued on the caller's stream (a hipStream_t passed as
  *     void*; NULL is the null stream).  Execution is asynchronous.
- *   - A plan may be executed concurrently on several streams; it holds no
- *     mutable state after its first upload to a device.
+ *   - A plan may be executed and compared from several threads and on
+ *     several streams at once: its per-device tables are made, and the
+ *     launch records emrs_plan_destroy waits on are kept, under the plan's
+ *     own lock.  emrs_plan_destroy must not overlap other calls on the same
+ *     plan.
  */
 #ifndef EMRS_H
 #define EMRS_H
