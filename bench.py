@@ -65,6 +65,9 @@ def workloads():
         # 182 GB per state: only a staged switch (--low-memory) fits it on one GPU.
         "llama2-13b-tp1dp8-tp4dp2": ("Llama-2-13B TP1PP1DP8 -> TP4PP1DP2, world 8, 40M buckets",
                                      ms.llama2_13b, PS(8, 1, 1), PS(8, 4, 1)),
+        # 966 GB per state: one destination rank's share (--share-rank) is what one GPU runs.
+        "llama2-70b-tp8pp4dp2-tp4pp4dp4": ("Llama-2-70B TP8PP4DP2 -> TP4PP4DP4, world 64, 40M buckets",
+                                           ms.llama2_70b, PS(64, 8, 4), PS(64, 4, 4)),
     }
 
 
@@ -125,6 +128,9 @@ def parse():
     ap.add_argument("--rank-shares", action="store_true",
                     help="time each destination rank's share of the plan on its own (the part one GPU "
                          "would run with one rank per GPU) beside the whole plan, on the same allocations")
+    ap.add_argument("--share-rank", type=int, default=None,
+                    help="run only this destination rank's share of the switch, on the tensors it touches "
+                         "alone (allocated one per stored tensor): the part one GPU runs with one rank per GPU")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
@@ -259,6 +265,12 @@ def main():
         return copy_calibration(args, dev, stream)
 
     desc, spec_fn, src, dst, *opt = workloads()[args.workload]
+    if args.share_rank is not None:
+        return bench_share(args, desc, spec_fn, src, dst, dev, stream)
+    if not args.low_memory and not args.ipc and not fits_twice(spec_fn(), dev):
+        print(f"bench.py: two whole states of {args.workload} do not fit on this GPU; time one destination rank's "
+              "share (--share-rank G) or a staged switch (--low-memory)", file=sys.stderr)
+        return 2
     if args.low_memory and args.ipc:
         return bench_ipc_staged(args, desc, spec_fn, src, dst, dev)
     if args.low_memory:
@@ -819,6 +831,131 @@ def bench_ipc_staged(args, desc, spec_fn, src, dst, dev):
         "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kern / HBM_PEAK_GBPS, 4), "traffic": None,
                      "note": "algorithmic bytes over the launches' time, allocation and release excluded"},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def fits_twice(spec, dev) -> bool:
+    """Whether two whole states of the model (14 bytes per parameter each) fit in the device's memory."""
+    import torch
+
+    return 2 * 14 * spec.num_params() < torch.cuda.get_device_properties(dev).total_memory * 0.97
+
+
+def bench_share(args, desc, spec_fn, src, dst, dev, stream):
+    """One destination rank's share of the switch (``TransferManager.compile_share_tensors``) on the
+    tensors it touches alone, each allocated on its own as a Megatron job holds them: the rank's own
+    optimizer tensors and its model shard's bf16 params, and the source tensors it reads.  With one
+    rank per GPU this is GPU g's part of the switch at its real size; its reads of other ranks' tensors
+    would come over xGMI.  Checked against the generator on every fp32 element the rank holds and, bit
+    for bit, by the share's own comparison."""
+    import numpy as np
+    import torch
+
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.resharding.layout import ARENA_PARAM
+    from elasticmegatron_amd.resharding.shares import pull_bytes
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    g = args.share_rank
+    spec = spec_fn()
+    space = build_virtual_model(spec)
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(bf16_source=args.bf16_source)
+    t0 = time.time()
+    plan = tm.compile_share_tensors(ls, ld, g)
+    planning_s = time.time() - t0
+    sb, db = plan.src, plan.dst
+    sizes = sum(sb.nbytes()[i] for i in plan.src_refs), sum(db.nbytes()[i] for i in plan.dst_refs)
+    free = torch.cuda.mem_get_info(dev)[0]
+    print(f"[bench] {args.workload} rank {g}: {len(plan.segments)} segments over {len(plan.src_refs)} source and "
+          f"{len(plan.dst_refs)} destination tensors ({sizes[0] / 1e9:.1f} + {sizes[1] / 1e9:.1f} GB; "
+          f"{free / 1e9:.1f} GB free); planning {planning_s:.1f} s", file=sys.stderr, flush=True)
+    if sum(sizes) > free - (8 << 30):
+        print("bench.py --share-rank: the share's tensors do not fit", file=sys.stderr)
+        return 2
+
+    def alloc(bufs, refs):
+        out = [None] * len(bufs)
+        for i in refs:
+            out[i] = torch.empty(bufs.numel[i], device=dev,
+                                 dtype=torch.bfloat16 if bufs.arena[i] == ARENA_PARAM else torch.float32)
+        return out
+
+    src_t, dst_t = alloc(sb, plan.src_refs), alloc(db, plan.dst_refs)
+
+    def by_tensor(pieces, bufs, tensors):
+        """The generator pieces of the allocated tensors, re-addressed by tensor, in batches of at most
+        128 tensors: (pieces, pointers, bytes)."""
+        ids = {}
+        for p in pieces:
+            b, loc = bufs.locate(int(p["buf"]), int(p["buf_off"]))
+            if tensors[b] is not None:
+                q = p.copy()
+                q["buf_off"] = loc
+                ids.setdefault(b, []).append(q)
+        keys = sorted(ids)
+        for lo in range(0, len(keys), 128):
+            batch = keys[lo:lo + 128]
+            rows = []
+            for j, b in enumerate(batch):
+                for q in ids[b]:
+                    q["buf"] = j
+                    rows.append(q)
+            yield (np.array(rows, dtype=pieces.dtype), [tensors[b].data_ptr() for b in batch],
+                   [tensors[b].numel() * tensors[b].element_size() for b in batch])
+
+    for pcs, ptrs, nb in by_tensor(ls.pieces(), sb, src_t):
+        _native.synth_fill(pcs, ptrs, nb, SEED, stream.cuda_stream)
+    for _ in range(args.warmup):
+        tm.execute_tensors(plan, src_t, dst_t, stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        tm.execute_tensors(plan, src_t, dst_t, stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    verified = None
+    if not args.no_verify:
+        bad = 0
+        own = [t if t is not None and db.arena[i] != ARENA_PARAM else None for i, t in enumerate(dst_t)]
+        for pcs, ptrs, nb in by_tensor(ld.pieces(include_bf16=False), db, own):
+            n, _ = _native.synth_verify(pcs, ptrs, nb, SEED, stream.cuda_stream)
+            bad += n
+        stats = plan.native.compare([0 if t is None else t.data_ptr() for t in src_t],
+                                    [0 if t is None else t.data_ptr() for t in dst_t], stream=stream.cuda_stream)
+        verified = bad == 0 and int(stats["mismatches"].sum()) == 0
+        if not verified:
+            print(f"[bench] share verification FAILED: {bad} generator mismatches, "
+                  f"{int(stats['mismatches'].sum())} plan mismatches", file=sys.stderr)
+            return 3
+    per_rank, _ = tm.compile_shares(ls, ld)
+    fp32, param = pull_bytes(per_rank[g].segments, ls)
+    local = int(fp32[g]) if g < len(fp32) else 0
+    remote = int(fp32.sum()) - local + param
+    traffic = plan.payload_bytes + plan.read_bytes
+    gbps = traffic / (ms / 1e3) / 1e9
+    out = {
+        "metric": metric_for(args.workload, desc) + f", destination rank {g}'s share",
+        "value": round(plan.payload_bytes / (ms / 1e3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
+        "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
+        "config": {"workload": desc + f", destination rank {g}'s share on the tensors it touches",
+                   "params": spec.num_params(), "rank": g, "segments": int(len(plan.segments)),
+                   "payload_bytes": plan.payload_bytes, "read_bytes": plan.read_bytes,
+                   "source_tensors": len(plan.src_refs), "destination_tensors": len(plan.dst_refs),
+                   "source_tensor_bytes": sizes[0], "destination_tensor_bytes": sizes[1],
+                   "read_local_bytes": local, "read_remote_bytes": remote,
+                   "remote_at_xgmi_ingress_ms": round(remote / (XGMI_INGRESS_GBPS * 1e9) * 1e3, 3),
+                   "planning_s": round(planning_s, 2), "verified_bit_exact": verified, "launch": launch_shape()},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
     return 0

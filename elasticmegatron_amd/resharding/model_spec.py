@@ -188,6 +188,15 @@ def llama2_13b() -> ModelSpec:
                      overlap_grad_reduce=True)
 
 
+def llama2_70b() -> ModelSpec:
+    """80 layers, hidden 8192, 64 heads with 8 KV groups, SwiGLU FFN 28672, vocab 32000: 69.0e9
+    parameters, 966 GB of state, which no single GPU holds; one destination rank's share of a
+    switch fits."""
+    return ModelSpec(name="llama2-70b", num_layers=80, hidden_size=8192, num_attention_heads=64,
+                     num_query_groups=8, ffn_hidden_size=28672, padded_vocab_size=32000,
+                     ddp_bucket_size=40_000_000, overlap_grad_reduce=True)
+
+
 def llama3_8b() -> ModelSpec:
     return ModelSpec(name="llama3-8b", num_layers=32, hidden_size=4096, num_attention_heads=32,
                      num_query_groups=8, ffn_hidden_size=14336, vocab_size=128256,

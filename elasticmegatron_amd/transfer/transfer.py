@@ -278,14 +278,41 @@ class TransferManager:
         self._plans[key] = cp
         return cp
 
+    def compile_share_tensors(self, src: StrategyLayout, dst: StrategyLayout, rank: int, kind: str = "transfer",
+                              include_bf16: bool = True) -> CompiledTensorPlan:
+        """Destination rank ``rank``'s share of the switch (:meth:`compile_shares`) over one buffer
+        per stored tensor (:meth:`compile_tensors`).  It reads and writes only some of the tensors:
+        ``plan.src_refs`` / ``plan.dst_refs``, the rest may be passed as None to
+        :meth:`execute_tensors`.  With one rank per GPU, those are what GPU ``rank`` runs its part
+        of the switch on: its own optimizer tensors, its part of its model shard's bf16 params, and
+        the source tensors it pulls, which in a multi-GPU job other GPUs hold."""
+        key = ("share-tensors", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
+               self.bf16_source, rank)
+        cp = self._plans.get(key)
+        if cp is not None:
+            return cp
+        per_rank, _ = self.compile_shares(src, dst, kind, include_bf16)
+        if not 0 <= rank < len(per_rank):
+            raise ValueError(f"rank {rank} is not a destination rank (world {len(per_rank)})")
+        sb, db = TensorBuffers(src), TensorBuffers(dst)
+        table = rebase_on_tensors(per_rank[rank].segments, sb, db)
+        cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,
+                                payload_bytes(table), read_bytes(table))
+        self._plans[key] = cp
+        return cp
+
     def execute_tensors(self, plan: CompiledTensorPlan, src_tensors, dst_tensors,
                         stream: Optional[torch.cuda.Stream] = None) -> None:
-        """Run a per-tensor plan; ``src_tensors`` / ``dst_tensors`` follow ``plan.src.keys`` / ``plan.dst.keys``."""
+        """Run a per-tensor plan; ``src_tensors`` / ``dst_tensors`` follow ``plan.src.keys`` / ``plan.dst.keys``.
+        A tensor the plan neither reads nor writes may be None (a share of the switch)."""
         if self.fake_transfer:
             return
         if len(src_tensors) != len(plan.src) or len(dst_tensors) != len(plan.dst):
             raise ValueError("tensor lists do not match the plan's buffers")
         ts = list(src_tensors) + list(dst_tensors)
+        if any(t is None for t in ts):
+            self._execute_some_tensors(plan, ts, stream)
+            return
         # One pass per property in list comprehensions: a per-tensor plan passes thousands of
         # tensors, and this check runs before every launch.  The pointers and sizes are read on
         # every call; the layout and device checks are skipped when both equal those of the last
@@ -304,6 +331,30 @@ class TransferManager:
             self._checked_tensors[id(plan)] = (plan, ptrs, dev)
         st = stream if stream is not None else torch.cuda.current_stream(dev)
         ns = len(plan.src)
+        with torch.cuda.device(dev):
+            plan.native.execute(ptrs[:ns], ptrs[ns:], st.cuda_stream)
+        self._payload_bytes += plan.payload_bytes
+
+    def _execute_some_tensors(self, plan: CompiledTensorPlan, ts, stream) -> None:
+        """execute_tensors with None for the tensors the plan does not touch: every tensor it reads or
+        writes is checked on every call (such a plan is one rank's share, run once per switch)."""
+        ns = len(plan.src)
+        refs = set(plan.src_refs) | {ns + i for i in plan.dst_refs}
+        need = plan.buffer_nbytes
+        dev = None
+        for i in sorted(refs):
+            t = ts[i]
+            if t is None:
+                raise ValueError(f"the plan reads or writes {(plan.src.keys + plan.dst.keys)[i]}, which is None")
+            if t.nbytes != need[i] or not t.is_contiguous():
+                raise ValueError("a tensor does not match its buffer (bytes or layout)")
+            dev = t.device if dev is None else dev
+            if t.device != dev or dev.type != "cuda":
+                raise RuntimeError("tensors must live in GPU memory, on one device: the reshard has no CPU path")
+        if dev is None:
+            return   # nothing to move
+        ptrs = [0 if t is None or i not in refs else t.data_ptr() for i, t in enumerate(ts)]
+        st = stream if stream is not None else torch.cuda.current_stream(dev)
         with torch.cuda.device(dev):
             plan.native.execute(ptrs[:ns], ptrs[ns:], st.cuda_stream)
         self._payload_bytes += plan.payload_bytes

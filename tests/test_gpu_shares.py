@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from elasticmegatron_amd import ParallelStrategy as PS
 from elasticmegatron_amd.megatron_manager.training_state import TrainingState
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.transfer import TransferManager
@@ -95,3 +96,47 @@ def test_shares_of_a_group_zero_switch(gpu_device, name, small, big, scale_up):
     space = build_virtual_model(small_llama2())
     _run(gpu_device, space.layout(src), space.layout(dst), "backup_up" if scale_up else "backup_down",
          TransferManager(), group_zero=True)
+
+
+@pytest.mark.parametrize("factory,src,dst", [
+    pytest.param(small_llama2, PS(8, 2, 1), PS(8, 1, 2), id="llama2-tp2-pp2"),
+])
+def test_share_on_its_own_tensors(gpu_device, factory, src, dst):
+    """Each destination rank's share over per-tensor buffers (compile_share_tensors), run with only
+    the tensors it touches allocated (None for the rest), each as its own allocation: the rank's
+    optimizer tensors equal the whole plan's, every bf16 element the share writes equals the whole
+    plan's, and the share's own comparison finds no difference."""
+    from elasticmegatron_amd.resharding.layout import ARENA_PARAM
+
+    space = build_virtual_model(factory())
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    whole = TrainingState.allocate(ld, gpu_device)
+    tm.execute(tm.compile(ls, ld), a, whole)
+    want = _host(whole)
+    for g in range(dst.world_size):
+        print(f"case share of rank {g} on its own tensors: {src} -> {dst}", flush=True)
+        plan = tm.compile_share_tensors(ls, ld, g)
+        sb, db = plan.src, plan.dst
+        src_t = [a.arenas()[sb.arena[i]][sb.offset[i]:sb.offset[i] + sb.numel[i]].clone() if i in plan.src_refs
+                 else None for i in range(len(sb))]
+        dst_t = [torch.full((db.numel[i],), -1, device=gpu_device,
+                            dtype=torch.int16 if db.arena[i] == ARENA_PARAM else torch.int32)
+                 .view(torch.bfloat16 if db.arena[i] == ARENA_PARAM else torch.float32)
+                 if i in plan.dst_refs else None for i in range(len(db))]
+        tm.execute_tensors(plan, src_t, dst_t)
+        torch.cuda.synchronize()
+        stats = plan.native.compare([0 if t is None else t.data_ptr() for t in src_t],
+                                    [0 if t is None else t.data_ptr() for t in dst_t])
+        assert int(stats["mismatches"].sum()) == 0
+        for i in plan.dst_refs:
+            got = dst_t[i].cpu().view(torch.int16 if db.arena[i] == ARENA_PARAM else torch.int32).numpy()
+            ref = want[db.arena[i]][db.offset[i]:db.offset[i] + db.numel[i]]
+            if db.arena[i] == ARENA_PARAM:
+                written = got != -1          # a DP rank writes its part of the model shard's params
+                assert written.any() and np.array_equal(got[written], ref[written])
+            else:
+                assert db.keys[i][1] == g and np.array_equal(got, ref)

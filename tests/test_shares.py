@@ -17,7 +17,8 @@ from elasticmegatron_amd.resharding.layout import ARENA_PARAM, SEG_DUP, SEG_ZERO
 from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from elasticmegatron_amd.resharding.shares import destination_rank_shares, fp32_rank_of
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
-from tests.helpers import REPAD_CASES, SEED, SMALL_CASES, execute_numpy, new_arenas, piece_fill_numpy, repad_spaces
+from tests.helpers import (REPAD_CASES, SEED, SMALL_CASES, execute_numpy, new_arenas, piece_fill_numpy, repad_spaces,
+                           small_llama2, small_llama3)
 from tests.test_group_zero import CASES as GZ_CASES
 
 
@@ -177,3 +178,50 @@ def test_pull_bytes_splits_a_read_across_source_ranks():
     strided["rows"], strided["len"], strided["src_stride"] = 2, 4, 8
     with pytest.raises(ValueError, match="strided"):
         pull_bytes(strided, ls)
+
+
+@pytest.mark.parametrize("factory,src,dst", [
+    pytest.param(small_llama2, PS(8, 2, 1), PS(8, 1, 2), id="llama2-tp2-pp2"),
+    pytest.param(small_llama3, PS(8, 4, 1), PS(8, 1, 2), id="llama3-tp4-pp2"),
+])
+def test_share_over_tensors_touches_only_its_rank(factory, src, dst):
+    """Rank g's share over per-tensor buffers (compile_share_tensors) writes only rank g's optimizer
+    tensors and bf16 params of its model shard, and reads only source tensors.  Run with None for
+    every tensor it does not touch (numpy model, each share on its own copy of the referenced
+    source tensors), the shares together write what the whole plan writes."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(factory())
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    whole = new_arenas(ld)
+    execute_numpy(lower_transfer(ls, ld), a, whole)
+    got = new_arenas(ld)
+    for g in range(dst.world_size):
+        plan = tm.compile_share_tensors(ls, ld, g)
+        sb, db = plan.src, plan.dst
+        for i in plan.dst_refs:
+            key = db.keys[i]
+            if db.arena[i] == ARENA_PARAM:
+                assert key[0] == "param"
+            else:
+                assert key[1] == g, key   # (kind, rank, name): only rank g's own optimizer tensors
+        src_bufs = [a[sb.arena[i]][sb.offset[i]:sb.offset[i] + sb.numel[i]].copy() if i in plan.src_refs else None
+                    for i in range(len(sb))]
+        unset = {4: 0xFFFFFFFF, 2: 0xFFFF}   # values the generator never gives
+        dst_bufs = [np.full(db.numel[i], unset[whole[db.arena[i]].itemsize], dtype=whole[db.arena[i]].dtype)
+                    if i in plan.dst_refs else None for i in range(len(db))]
+        execute_numpy(plan.segments, src_bufs, dst_bufs)
+        for i in plan.dst_refs:
+            view = got[db.arena[i]][db.offset[i]:db.offset[i] + db.numel[i]]
+            written = dst_bufs[i] != unset[dst_bufs[i].itemsize]
+            assert np.all(view[written] == unset[view.itemsize])    # no element written by two shares
+            view[written] = dst_bufs[i][written]
+    for k in range(3):   # every stored fp32 element, from exactly the shares
+        stored = whole[k] != 0xFFFFFFFF
+        assert np.array_equal(got[k][stored], whole[k][stored])
+    stored = whole[3] != 0xFFFF
+    assert np.array_equal(got[3][stored], whole[3][stored])
