@@ -72,3 +72,13 @@ def test_ipc_staged_line(gpu_device):
     assert c["verified_bit_exact"] is True and c["exporter_exit_status"] == 0
     assert [sorted(s) for s in c["stages_ms"]] == [["allocate", "execute", "release"]] * 3
     assert len(c["device_used_before_each_release_bytes"]) == 3 and d["steps"] == 1
+
+
+@pytest.mark.gpu
+def test_share_rank_line(gpu_device):
+    """--share-rank: one destination rank's share on the tensors it touches alone, checked."""
+    d = _bench("--share-rank", "3", "--steps", "2", "--warmup", "1")
+    c = d["config"]
+    assert c["verified_bit_exact"] is True and c["rank"] == 3
+    assert 0 < c["destination_tensors"] and 0 < c["source_tensors"] and d["ms_per_step"] > 0
+    assert c["read_local_bytes"] + c["read_remote_bytes"] == c["read_bytes"]
