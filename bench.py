@@ -1324,6 +1324,8 @@ def copy_calibration(args, dev, stream):
     t = np.zeros(1, dtype=SEGMENT_DTYPE)
     t[0] = (0, 0, 4, 0, 0, 0, n, 1, 0, 0, 0, 0, 0, 0)
     plan = _native.Plan(t, [n * 4], [n * 4])
+    if args.shape_sweep:
+        return copy_shapes(args, plan, a, b, stream)
     for _ in range(args.warmup):
         plan.execute([a.data_ptr()], [b.data_ptr()], stream.cuda_stream)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -1336,6 +1338,44 @@ def copy_calibration(args, dev, stream):
     ms = e0.elapsed_time(e1) / args.steps
     print(json.dumps({"copy_bytes": n * 4, "ms": round(ms, 4),
                       "traffic_GBps": round(2 * n * 4 / (ms / 1e3) / 1e9, 1)}), flush=True)
+    return 0
+
+
+def copy_shapes(args, plan, a, b, stream):
+    """--copy-calibration-gib with --shape-sweep: the contiguous copy in each launch shape of the
+    copy kernel, on the same two buffers, round after round; the fastest plain copy this kernel makes."""
+    import torch
+
+    from elasticmegatron_amd import _native
+
+    rows = [{"shape": shp or "default", "ms": []} for shp in args.shape_sweep]
+    try:
+        for _ in range(args.rounds):
+            for shp, row in zip(args.shape_sweep, rows):
+                _native.set_tuning(**shp)
+                b.zero_()
+                for _ in range(args.warmup):
+                    plan.execute([a.data_ptr()], [b.data_ptr()], stream.cuda_stream)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record(stream)
+                for _ in range(args.steps):
+                    plan.execute([a.data_ptr()], [b.data_ptr()], stream.cuda_stream)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                if not torch.equal(a, b):
+                    print(f"[bench] copy shape {shp}: the copy differs from its source", file=sys.stderr)
+                    return 3
+                row["ms"].append(round(e0.elapsed_time(e1) / args.steps, 4))
+                row["launch"] = launch_shape()
+    finally:
+        _native.set_tuning()
+    nbytes = 2 * a.numel() * a.element_size()
+    for row in rows:
+        row["best_TBps"] = round(nbytes / (min(row["ms"]) / 1e3) / 1e12, 3)
+    print(json.dumps({"what": "one contiguous copy in each launch shape of the copy kernel, same buffers, "
+                               "rounds alternating", "copy_bytes": nbytes // 2, "rounds": args.rounds,
+                      "shapes": rows}), flush=True)
     return 0
 
 
