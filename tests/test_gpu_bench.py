@@ -82,3 +82,12 @@ def test_share_rank_line(gpu_device):
     assert c["verified_bit_exact"] is True and c["rank"] == 3
     assert 0 < c["destination_tensors"] and 0 < c["source_tensors"] and d["ms_per_step"] > 0
     assert c["read_local_bytes"] + c["read_remote_bytes"] == c["read_bytes"]
+
+
+@pytest.mark.gpu
+def test_copy_shapes_line(gpu_device):
+    """--copy-calibration-gib with --shape-sweep: a contiguous copy in each launch shape, checked."""
+    d = _bench("--copy-calibration-gib", "0.25", "--shape-sweep", "default;units=2;persistent=1", "--rounds", "2",
+               "--steps", "1", "--warmup", "1")
+    assert [r["shape"] for r in d["shapes"]] == ["default", {"units": 2}, {"persistent": 1}]
+    assert all(len(r["ms"]) == 2 and r["best_TBps"] > 0 for r in d["shapes"])
