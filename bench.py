@@ -130,7 +130,8 @@ def parse():
                          "would run with one rank per GPU) beside the whole plan, on the same allocations")
     ap.add_argument("--share-rank", type=int, default=None,
                     help="run only this destination rank's share of the switch, on the tensors it touches "
-                         "alone (allocated one per stored tensor): the part one GPU runs with one rank per GPU")
+                         "alone (allocated one per stored tensor): the part one GPU runs with one rank per GPU; "
+                         "-1: every rank's share in turn")
     ap.add_argument("--bf16-source", choices=("cast", "copy"), default="cast",
                     help="cast: bf16 params = bf16(new main), fused into the main copy; copy: from source bf16")
     ap.add_argument("--lanes", type=int, default=0, choices=(0, 64, 128, 256),
@@ -849,22 +850,79 @@ def bench_share(args, desc, spec_fn, src, dst, dev, stream):
     optimizer tensors and its model shard's bf16 params, and the source tensors it reads.  With one
     rank per GPU this is GPU g's part of the switch at its real size; its reads of other ranks' tensors
     would come over xGMI.  Checked against the generator on every fp32 element the rank holds and, bit
-    for bit, by the share's own comparison."""
+    for bit, by the share's own comparison.  ``--share-rank -1`` runs every rank's share in turn and
+    gives the switch's time with one rank per GPU as the slowest rank's, each rank taking the longer
+    of its HBM time and its remote reads at the xGMI ingress rate."""
+    import gc
+
+    import torch
+
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    spec = spec_fn()
+    space = build_virtual_model(spec)
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(bf16_source=args.bf16_source)
+    common = {"steps": args.steps, "warmup": args.warmup, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
+              "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), "
+                      "exp_avg_sq = |N(0,1e-6)|)"}
+    if args.share_rank >= 0:
+        row = share_run(args, tm, ls, ld, args.share_rank, dev, stream)
+        if isinstance(row, int):
+            return row
+        g = args.share_rank
+        out = {"metric": metric_for(args.workload, desc) + f", destination rank {g}'s share",
+               "value": round(row["payload_bytes"] / (row["ms"] / 1e3) / 1e9, 2), "unit": "GB/s",
+               "ms_per_step": row["ms"], **common,
+               "config": {"workload": desc + f", destination rank {g}'s share on the tensors it touches",
+                          "params": spec.num_params(), **row, "launch": launch_shape()},
+               "roofline": {"bound": "hbm", "achieved": row["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                            "frac": round(row["traffic_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None}}
+        print(json.dumps(out), flush=True)
+        return 0
+    rows = []
+    for g in range(dst.world_size):
+        row = share_run(args, tm, ls, ld, g, dev, stream)
+        if isinstance(row, int):
+            return row
+        rows.append(row)
+        gc.collect()
+        torch.cuda.empty_cache()
+    per_gpu = [max(r["ms"], r["remote_at_xgmi_ingress_ms"]) for r in rows]
+    slowest = max(range(len(rows)), key=lambda i: per_gpu[i])
+    payload = sum(r["payload_bytes"] for r in rows)
+    out = {"metric": metric_for(args.workload, desc) + ", every destination rank's share",
+           "value": round(payload / (per_gpu[slowest] / 1e3) / 1e9, 2), "unit": "GB/s",
+           "ms_per_step": per_gpu[slowest], **common,
+           "config": {"workload": desc + ", every destination rank's share on the tensors it touches, one after "
+                                         "another on one GPU",
+                      "params": spec.num_params(), "ranks": len(rows),
+                      "what": "value and ms_per_step: the switch with one rank per GPU, bound by the slowest rank, "
+                              "each rank taking the longer of its measured HBM time and its remote reads at "
+                              f"{XGMI_INGRESS_GBPS:.0f} GB/s of xGMI ingress (projected, not measured on several GPUs)",
+                      "slowest_rank": slowest, "max_hbm_ms": max(r["ms"] for r in rows),
+                      "max_remote_xgmi_ms": max(r["remote_at_xgmi_ingress_ms"] for r in rows),
+                      "min_traffic_gbps": min(r["traffic_gbps"] for r in rows),
+                      "max_traffic_gbps": max(r["traffic_gbps"] for r in rows),
+                      "verified_bit_exact": all(r["verified_bit_exact"] is not False for r in rows),
+                      "launch": launch_shape(), "shares": rows}}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def share_run(args, tm, ls, ld, g, dev, stream):
+    """Rank g's share on its own tensors: allocate, fill, time, check.  Returns its figures, or an
+    exit code."""
     import numpy as np
     import torch
 
     from elasticmegatron_amd import _native
     from elasticmegatron_amd.resharding.layout import ARENA_PARAM
     from elasticmegatron_amd.resharding.shares import pull_bytes
-    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
-    from elasticmegatron_amd.transfer.transfer import TransferManager
 
-    g = args.share_rank
-    spec = spec_fn()
-    space = build_virtual_model(spec)
-    space.register_reshard(src, dst)
-    ls, ld = space.layout(src), space.layout(dst)
-    tm = TransferManager(bf16_source=args.bf16_source)
     t0 = time.time()
     plan = tm.compile_share_tensors(ls, ld, g)
     planning_s = time.time() - t0
@@ -931,7 +989,7 @@ def bench_share(args, desc, spec_fn, src, dst, dev, stream):
                                     [0 if t is None else t.data_ptr() for t in dst_t], stream=stream.cuda_stream)
         verified = bad == 0 and int(stats["mismatches"].sum()) == 0
         if not verified:
-            print(f"[bench] share verification FAILED: {bad} generator mismatches, "
+            print(f"[bench] share of rank {g}: verification FAILED: {bad} generator mismatches, "
                   f"{int(stats['mismatches'].sum())} plan mismatches", file=sys.stderr)
             return 3
     per_rank, _ = tm.compile_shares(ls, ld)
@@ -939,26 +997,14 @@ def bench_share(args, desc, spec_fn, src, dst, dev, stream):
     local = int(fp32[g]) if g < len(fp32) else 0
     remote = int(fp32.sum()) - local + param
     traffic = plan.payload_bytes + plan.read_bytes
-    gbps = traffic / (ms / 1e3) / 1e9
-    out = {
-        "metric": metric_for(args.workload, desc) + f", destination rank {g}'s share",
-        "value": round(plan.payload_bytes / (ms / 1e3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
-        "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
-        "config": {"workload": desc + f", destination rank {g}'s share on the tensors it touches",
-                   "params": spec.num_params(), "rank": g, "segments": int(len(plan.segments)),
-                   "payload_bytes": plan.payload_bytes, "read_bytes": plan.read_bytes,
-                   "source_tensors": len(plan.src_refs), "destination_tensors": len(plan.dst_refs),
-                   "source_tensor_bytes": sizes[0], "destination_tensor_bytes": sizes[1],
-                   "read_local_bytes": local, "read_remote_bytes": remote,
-                   "remote_at_xgmi_ingress_ms": round(remote / (XGMI_INGRESS_GBPS * 1e9) * 1e3, 3),
-                   "planning_s": round(planning_s, 2), "verified_bit_exact": verified, "launch": launch_shape()},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
-    }
-    print(json.dumps(out), flush=True)
-    return 0
+    return {"rank": g, "ms": round(ms, 4), "segments": int(len(plan.segments)),
+            "payload_bytes": plan.payload_bytes, "read_bytes": plan.read_bytes,
+            "traffic_gbps": round(traffic / (ms / 1e3) / 1e9, 1),
+            "source_tensors": len(plan.src_refs), "destination_tensors": len(plan.dst_refs),
+            "source_tensor_bytes": sizes[0], "destination_tensor_bytes": sizes[1],
+            "read_local_bytes": local, "read_remote_bytes": remote,
+            "remote_at_xgmi_ingress_ms": round(remote / (XGMI_INGRESS_GBPS * 1e9) * 1e3, 3),
+            "planning_s": round(planning_s, 2), "verified_bit_exact": verified}
 
 
 def mapped_vs_owned(args, tm, plan, ls, mapped, b, dev, stream):
