@@ -47,3 +47,36 @@ def test_full_size_chain_through_the_manager(gpu_device, low_memory):
         mgr = None
         gc.collect()
         torch.cuda.empty_cache()
+
+
+def test_many_switches_keep_memory_steady(gpu_device):
+    """Two hundred switches of a small model through the manager, cycling through five strategies
+    (a Group-ZeRO hop included): after the first cycle has built and cached every plan, device
+    memory in use does not grow, and the final state holds the generator's values."""
+    from tests.helpers import small_llama2
+
+    seq = [dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1),
+           dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=2),
+           dict(world_size=4, tensor_model_parallel_size=1, pipeline_model_parallel_size=1),
+           dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1,
+                num_distributed_optimizer_instances=2),
+           dict(world_size=4, tensor_model_parallel_size=1, pipeline_model_parallel_size=1)]
+    mgr = ElasticMegatronManager(seq, small_llama2(), device=gpu_device)
+    mgr.training_state.fill_synthetic(SEED)
+    quiet = __import__("logging").getLogger("test.quiet")
+    quiet.addHandler(__import__("logging").NullHandler())
+    quiet.propagate = False
+    used, other = [], []     # torch's allocations; device memory outside torch's pool (plan tables)
+    for i in range(200):
+        mgr.reshard(seq[(i + 1) % len(seq)], logger=quiet)
+        if i % len(seq) == len(seq) - 1:
+            torch.cuda.synchronize()
+            gc.collect()
+            free, total = torch.cuda.mem_get_info(gpu_device)
+            used.append(torch.cuda.memory_allocated(gpu_device))
+            other.append(total - free - torch.cuda.memory_reserved(gpu_device))
+    print(f"case 200 switches: allocated after each cycle {used[0]} .. {max(used)} bytes; outside torch's pool "
+          f"{other[0]} .. {max(other)} bytes", flush=True)
+    assert max(used[1:]) <= used[1]
+    assert max(other[1:]) <= other[1] + (64 << 20)
+    assert mgr.training_state.verify_synthetic(SEED)[0] == 0
