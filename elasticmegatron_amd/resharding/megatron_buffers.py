@@ -80,20 +80,34 @@ class MegatronBuffers:
             raise ValueError(f"elements [{offset}, {offset + numel}) of arena {arena} leave buffer {key}")
         return key, local
 
-    def tensor_views(self, tb: TensorBuffers, buffers: Dict[Tuple, "torch.Tensor"]) -> list:
+    def rank_keys(self, rank: int) -> List[Tuple]:
+        """The buffers global rank ``rank`` holds in a job with one rank per GPU: its fp32 DP shards
+        and the bf16 ``param_data`` of the model shards it belongs to (dense, and expert with MoE)."""
+        st = self.layout.strategy
+        pp, _, tp = st.dense_rank_coords(rank)
+        epp, _, ep, etp = st.expert_rank_coords(rank)
+        wanted = [(kind, rank, part) for kind in FP32_KINDS for part in ("dense", "expert")]
+        wanted += [("param", ("dense", pp, tp)), ("param", ("expert", epp, ep, etp))]
+        return [key for key in wanted if key in self.numel]
+
+    def tensor_views(self, tb: TensorBuffers, buffers: Dict[Tuple, "torch.Tensor"], partial: bool = False) -> list:
         """The tensors of ``tb`` (one side of a per-tensor plan of this layout), in buffer order, as
-        views of the caller's flat ``buffers``."""
+        views of the caller's flat ``buffers``.  With ``partial`` only the buffers given are needed
+        (one rank's own, :meth:`rank_keys`), and the tensors of any other buffer come back as None."""
         if tb.layout is not self.layout and (tb.layout.space.spec, tb.layout.strategy) != \
                 (self.layout.space.spec, self.layout.strategy):
             raise ValueError("the per-tensor buffers belong to another layout")
         for key, _, n in self.specs:
             t = buffers.get(key)
+            if t is None and partial:
+                continue
             if t is None or t.numel() != n or not t.is_contiguous():
                 raise ValueError(f"buffer {key} is missing or is not a contiguous tensor of {n} elements")
         out = []
         for a, off, n in zip(tb.arena, tb.offset, tb.numel):
             key, local = self.locate(a, off, n)
-            out.append(buffers[key][local:local + n])
+            t = buffers.get(key)
+            out.append(None if t is None else t[local:local + n])
         return out
 
     def remap_pieces(self, pieces: np.ndarray) -> np.ndarray:

@@ -145,3 +145,44 @@ def test_full_size_switch_on_megatron_buffers(gpu_device, src, dst):
     finally:
         sbuf = dbuf = src_views = dst_views = None  # noqa: F841
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("factory,src,dst", CASES[:3])
+def test_each_rank_writes_its_share_into_its_own_buffers(gpu_device, factory, src, dst):
+    """With one rank per GPU each rank holds only its own flat buffers (MegatronBuffers.rank_keys: its
+    fp32 DP shards and its model shard's param_data).  Each destination rank's share
+    (compile_share_tensors) runs with views of those buffers as its only destination tensors, the
+    job's source buffers as sources.  Rank g's fp32 buffers then equal the whole switch's, padding
+    included (the canary), and every bf16 element it writes equals the whole switch's."""
+    spec = factory()
+    space = build_virtual_model(spec)
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(check_disjoint=True)
+    ms_, md = MegatronBuffers(ls), MegatronBuffers(ld)
+    sbuf, whole = ms_.allocate(gpu_device), md.allocate(gpu_device)
+    _canary(sbuf)
+    _canary(whole)
+    full = tm.compile_tensors(ls, ld)
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    for v, w in zip(ms_.tensor_views(full.src, sbuf), full.src.views(a)):
+        v.copy_(w)
+    del a
+    tm.execute_tensors(full, ms_.tensor_views(full.src, sbuf), md.tensor_views(full.dst, whole))
+    for g in range(dst.world_size):
+        print(f"case rank {g}'s share into its own buffers, {spec.name}: {src} -> {dst}", flush=True)
+        plan = tm.compile_share_tensors(ls, ld, g)
+        own = {k: torch.empty_like(whole[k]) for k in md.rank_keys(g)}
+        _canary(own)
+        dst_views = md.tensor_views(plan.dst, own, partial=True)
+        assert all(dst_views[i] is not None for i in plan.dst_refs)
+        tm.execute_tensors(plan, ms_.tensor_views(plan.src, sbuf), dst_views)
+        torch.cuda.synchronize()
+        for k, t in own.items():
+            if k[0] == "param":
+                bits, want = t.view(torch.int16), whole[k].view(torch.int16)
+                written = bits != CANARY16
+                assert bool(written.any()) and torch.equal(bits[written], want[written])
+            else:
+                assert torch.equal(t.view(torch.int32), whole[k].view(torch.int32)), k

@@ -109,3 +109,30 @@ def test_remapped_pieces_fill_the_same_values(factory, ps):
         want = arenas[a][off:off + n]
         assert np.array_equal(v.numpy().view(want.dtype), want)
     assert mb.byte_sizes() == [x.nbytes for x in flat]
+
+
+@pytest.mark.parametrize("factory,src,dst", [
+    (small_llama2, PS(8, 2, 1), PS(8, 1, 2)),
+    (small_mixtral, PS(8, 1, 1, expert_model_parallel_size=4), PS(8, 1, 1, expert_model_parallel_size=8)),
+], ids=["llama2-tp2-pp2", "mixtral-ep4-ep8"])
+def test_each_share_writes_only_its_ranks_own_buffers(factory, src, dst):
+    """Every destination tensor of rank g's share lies in one of the buffers rank g holds with one
+    rank per GPU (rank_keys: its fp32 DP shards and its model shard's param_data), and the partial
+    views give None for every other buffer."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(factory())
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    md, tm = MegatronBuffers(ld), TransferManager()
+    for g in range(dst.world_size):
+        plan = tm.compile_share_tensors(ls, ld, g)
+        keys = set(md.rank_keys(g))
+        assert keys and all(k[1] == g for k in keys if k[0] != "param")
+        for i in plan.dst_refs:
+            assert md.locate(plan.dst.arena[i], plan.dst.offset[i], plan.dst.numel[i])[0] in keys
+        own = {k: torch.empty(md.numel[k], dtype=torch.bfloat16 if k[0] == "param" else torch.float32)
+               for k in keys}
+        views = md.tensor_views(plan.dst, own, partial=True)
+        assert all(views[i] is not None for i in plan.dst_refs)
+        assert sum(v is not None for v in views) < len(views)
