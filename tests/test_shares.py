@@ -225,3 +225,14 @@ def test_share_over_tensors_touches_only_its_rank(factory, src, dst):
         assert np.array_equal(got[k][stored], whole[k][stored])
     stored = whole[3] != 0xFFFF
     assert np.array_equal(got[3][stored], whole[3][stored])
+
+
+def test_share_of_a_rank_outside_the_world_is_refused():
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 2))
+    tm = TransferManager()
+    for bad in (-1, 8):
+        with pytest.raises(ValueError):
+            tm.compile_share_tensors(ls, ld, bad)
