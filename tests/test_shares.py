@@ -236,3 +236,30 @@ def test_share_of_a_rank_outside_the_world_is_refused():
     for bad in (-1, 8):
         with pytest.raises(ValueError):
             tm.compile_share_tensors(ls, ld, bad)
+
+
+def test_partial_execution_checks_the_tensors_it_touches():
+    """execute_tensors with None for untouched tensors: a touched tensor that is None, of the wrong
+    size, or not in GPU memory is refused before anything runs."""
+    import torch
+
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 2))
+    tm = TransferManager()
+    plan = tm.compile_share_tensors(ls, ld, 5)
+    src = [None] * len(plan.src)
+    dst = [None] * len(plan.dst)
+    with pytest.raises(ValueError, match="which is None"):
+        tm.execute_tensors(plan, src, dst)
+    for i in plan.src_refs:
+        src[i] = torch.empty(plan.src.numel[i], dtype=torch.float32 if plan.src.arena[i] < 3 else torch.bfloat16)
+    for i in plan.dst_refs:
+        dst[i] = torch.empty(plan.dst.numel[i], dtype=torch.float32 if plan.dst.arena[i] < 3 else torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU memory"):
+        tm.execute_tensors(plan, src, dst)
+    i = plan.src_refs[0]          # the first tensor checked
+    src[i] = torch.empty(plan.src.numel[i] + 1, dtype=src[i].dtype)
+    with pytest.raises(ValueError, match="does not match"):
+        tm.execute_tensors(plan, src, dst)
