@@ -1054,7 +1054,10 @@ struct ResolvedBases {
   std::vector<uint64_t> ptrs;
 };
 
-int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *dst_bases, ResolvedBases *rb) {
+// out_of_place: a destination buffer may overlap no other referenced buffer
+// (an execution); a comparison only reads, so there any buffers may overlap.
+int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *dst_bases, ResolvedBases *rb,
+                  bool out_of_place = true) {
   const uint32_t ns = plan->stats.n_src_bufs, nd = plan->stats.n_dst_bufs;
   if ((ns && !src_bases) || (nd && !dst_bases))
     return fail(EMRS_ERR_INVALID_ARGUMENT, "base pointer array is NULL");
@@ -1083,13 +1086,15 @@ int resolve_bases(const emrs_plan *plan, void *const *src_bases, void *const *ds
   // Out of place: no destination range may overlap another referenced range.
   // Sweep in address order; an earlier range overlaps the current one exactly
   // when its end lies past the current start.
-  std::sort(iv.begin(), iv.end(), [](const Iv &x, const Iv &y) { return x.b < y.b; });
-  uintptr_t end_src = 0, end_dst = 0;
-  for (const Iv &x : iv) {
-    if (x.b < end_dst)
-      return fail(EMRS_ERR_ALIAS, x.dst ? "two destination buffers overlap" : "a source buffer overlaps a destination buffer");
-    if (x.dst && x.b < end_src) return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
-    (x.dst ? end_dst : end_src) = std::max(x.dst ? end_dst : end_src, x.e);
+  if (out_of_place) {
+    std::sort(iv.begin(), iv.end(), [](const Iv &x, const Iv &y) { return x.b < y.b; });
+    uintptr_t end_src = 0, end_dst = 0;
+    for (const Iv &x : iv) {
+      if (x.b < end_dst)
+        return fail(EMRS_ERR_ALIAS, x.dst ? "two destination buffers overlap" : "a source buffer overlaps a destination buffer");
+      if (x.dst && x.b < end_src) return fail(EMRS_ERR_ALIAS, "a source buffer overlaps a destination buffer");
+      (x.dst ? end_dst : end_src) = std::max(x.dst ? end_dst : end_src, x.e);
+    }
   }
   rb->table = ns > kArgBuffers || nd > kArgBuffers;
   if (rb->table) {
@@ -1752,7 +1757,7 @@ int compare_setup(emrs_plan *plan, void *const *src_bases, void *const *dst_base
   for (uint64_t i = 0; i < n_in; ++i)
     if ((groups && groups[i] >= n_groups) || (aux_groups && aux_groups[i] >= n_groups))
       return fail(EMRS_ERR_INVALID_ARGUMENT, "group id >= n_groups");
-  int rc = resolve_bases(plan, src_bases, dst_bases, &job->rb);
+  int rc = resolve_bases(plan, src_bases, dst_bases, &job->rb, /*out_of_place=*/false);
   if (rc) return rc;
   const size_t nd = plan->segs.size();
   job->g_host.resize(2 * nd);

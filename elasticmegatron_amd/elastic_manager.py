@@ -36,7 +36,8 @@ from .resharding.model_spec import ModelSpec
 from .resharding.util import Timer
 from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
 from .transfer.ipc_manager import SharedTrainingState
-from .transfer.transfer import TransferManager, _granule_of, backup_kind, shares_params
+from .transfer.transfer import (BACKUP_KINDS, TransferManager, _granule_of, adoptable_granules, backup_kind,
+                                held_granules, shares_params)
 from .transfer.verify import merge_stats, report_from_stats
 
 StrategyLike = Union[ParallelStrategy, Dict[str, int]]
@@ -78,6 +79,11 @@ class ElasticMegatronManager:
         process that held it (``receive_training_state``).  ``device="meta"`` allocates nothing: the
         manager plans (``reshard(..., is_meta_device=True)``) until :meth:`attach_training_state`
         hands it the real state, as the reference builds its new process on the meta device first.
+        A Group-ZeRO switch from such a state that this process owns and releases
+        (``release_source``) leaves instance 0 where it is: the new state takes over the old one's
+        leading granules of every fp32 arena (all of instance 0 with PP = 1) instead of copying
+        them, so a scale-up to two instances moves two thirds of the bytes, a scale-down almost
+        none, and the peak memory drops by the granules taken over.
         """
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
@@ -112,11 +118,15 @@ class ElasticMegatronManager:
             training_state = self._allocate(self.space_for(cur).layout(cur), device)
         self.training_state = training_state
 
-    def _allocate(self, layout, device, param=None):
-        """A new state of ``layout`` of the kind this manager keeps (nothing on the meta device)."""
+    def _allocate(self, layout, device, param=None, adopted=None):
+        """A new state of ``layout`` of the kind this manager keeps (nothing on the meta device);
+        ``adopted``: leading fp32 granules of the old state it takes over (shared states only)."""
         meta = device is not None and torch.device(device).type == "meta"
         if self.share_granule_bytes is not None and not meta:
-            return SharedTrainingState.allocate(layout, device, self.share_granule_bytes, param_granules=param)
+            return SharedTrainingState.allocate(layout, device, self.share_granule_bytes, param_granules=param,
+                                                adopted=adopted)
+        if adopted is not None:
+            raise AssertionError("only a shared state takes over granules")
         return TrainingState.allocate(layout, device, param=param,
                                       granule_bytes=ARENA_GRANULE_BYTES if self.low_memory else 0)
 
@@ -246,16 +256,29 @@ class ElasticMegatronManager:
                          is_meta_device: bool = False) -> float:
         """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
         ``is_meta_device`` plans, caches and uploads the plan's tables without moving data.  The
-        bf16 params stay where they are when ``dst`` shares ``src``'s, and are copied otherwise.
+        bf16 params stay where they are when ``dst`` shares ``src``'s, and are copied otherwise;
+        the leading fp32 granules that ``dst`` holds in ``src``'s memory are left in place.
         Returns the executor's ms."""
         kind = backup_kind(is_scale_up, not shares_params(src, dst))
-        plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst), kind)
+        plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst), kind,
+                                                     adopt_granules=held_granules(src, dst))
         if is_meta_device:
             self._prepare(plan, src)
         with Timer() as t:
             if not is_meta_device:
                 self.transfer_manager.execute_states(plan, src, dst)
         return t.elapsed
+
+    def _adoptable(self, src_state, dst_layout, kind: str, dst_granule_bytes, param) -> int:
+        """Leading fp32 granules that the new state of a Group-ZeRO switch takes over from the old
+        one: only from a shared state this process owns and the switch releases, into granules of
+        the same size, with the bf16 params shared too."""
+        if kind not in BACKUP_KINDS or param is None or not self.release_source:
+            return 0
+        if not isinstance(src_state, SharedTrainingState) or src_state.imported \
+                or src_state.granule_bytes != dst_granule_bytes:
+            return 0
+        return adoptable_granules(src_state.layout, dst_layout, dst_granule_bytes, kind)
 
     @staticmethod
     def _carried_params(src_state, dst_granule_bytes):
@@ -339,7 +362,9 @@ class ElasticMegatronManager:
         # (or are copied, when the new state cannot share them).
         param = self._carried_params(src_state, gd) if backup is not None else None
         kind = "transfer" if backup is None else backup_kind(backup, param is None)
-        plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind)
+        # ... and instance 0's fp32 granules stay where they are when the new state can take them over.
+        adopt = self._adoptable(src_state, dst_layout, kind, gd, param)
+        plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind, adopt_granules=adopt)
         stages = self.transfer_manager.staged_for_states(src_state.layout, dst_layout, gs, gd, kind) \
             if self.low_memory else ()
         if is_meta_device:
@@ -353,7 +378,8 @@ class ElasticMegatronManager:
             if verify:
                 report = report_from_stats(*checked)
         else:
-            dst_state = self._allocate(dst_layout, src_state.device, param=param)
+            adopted = src_state.leading_fp32_granules(adopt) if adopt else None
+            dst_state = self._allocate(dst_layout, src_state.device, param=param, adopted=adopted)
             if backup is None:
                 elapsed = self.transfer_params(src_state, dst_state)
             else:
@@ -368,6 +394,8 @@ class ElasticMegatronManager:
                 raise RuntimeError(f"reshard verification failed: {report.mismatches} elements differ\n"
                                    + "\n".join(lines[:20]))
         if self.release_source:
+            if adopt:
+                src_state.hand_over(adopt)
             src_state.release_optimizer()
         self.training_state = dst_state
         msg = self.log_communication_info(elapsed, logger=logger)

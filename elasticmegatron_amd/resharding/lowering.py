@@ -278,8 +278,38 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
     return _assemble(fp32.table(), bf16.table(), fp32.group_array(), bf16.group_array(), with_groups)
 
 
+def _backup_sources(src: StrategyLayout, dst: StrategyLayout, vp, scale_up: bool):
+    """(source holder, destination holder) of every fp32 run of ``vp`` in a Group-ZeRO switch: a
+    new instance's shard comes from instance 0 on a scale-up and from the same instance on a
+    scale-down (transfer.py:343-388)."""
+    src_by = {(h.instance, h.tp_rank, h.lo): h for h in src.fp32_holders(vp)}
+    out = []
+    for h in dst.fp32_holders(vp):
+        s = src_by.get((0 if scale_up else h.instance, h.tp_rank, h.lo))
+        if s is None or s.hi != h.hi:
+            raise AssertionError(f"{vp.name}: no matching source shard for a Group-ZeRO copy")
+        out.append((s, h))
+    return out
+
+
+def in_place_prefix(src: StrategyLayout, dst: StrategyLayout, scale_up: bool) -> int:
+    """Length of the head of a Group-ZeRO switch's fp32 arenas that the new state could take over
+    from the old one unchanged: every destination run that starts below it sits at its source's
+    offset, and it does not pass the end of either arena.  With PP = 1 it covers instance 0 (the
+    leading ranks of both worlds); with PP > 1, instance 0 of the first stage."""
+    if src.strategy.optimizer_data_parallel_size != dst.strategy.optimizer_data_parallel_size:
+        raise AssertionError("Group-ZeRO switch must keep the optimizer DP size")
+    end = min(src.fp32_numel, dst.fp32_numel)
+    for vp in src.space.all_virtual_params:
+        if src.has_param(vp) and dst.has_param(vp):
+            for s, h in _backup_sources(src, dst, vp, scale_up):
+                if s.offset != h.offset:
+                    end = min(end, h.offset)
+    return end
+
+
 def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False,
-                           copy_bf16: bool = False):
+                           copy_bf16: bool = False, in_place_below: int = 0):
     """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
 
     On a scale-up every new instance of a shard is filled from instance 0's
@@ -294,6 +324,13 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     bf16 params are then copied shard by shard, the same bits the shared
     arena would hold (4 bytes of traffic per parameter).
 
+    ``in_place_below``: fp32 elements of the new arenas below this offset are
+    not written, because the new state holds the old one's memory there (it
+    took over the old state's leading granules; at most
+    :func:`in_place_prefix`, checked run by run).  A run that crosses the
+    offset is copied from it on.  A scale-up to two instances then moves one
+    read and one write per element instead of one read and two writes.
+
     ``with_groups``: as for :func:`lower_transfer`.
     """
     space = src.space
@@ -305,14 +342,16 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
         if not (src.has_param(vp) and dst.has_param(vp)):
             continue
         g = vp.global_index if with_groups else 0
-        src_by = {(h.instance, h.tp_rank, h.lo): h for h in src.fp32_holders(vp)}
         # Destinations per source shard, in destination order.
         fills: Dict[int, Tuple[Holder, List[Holder]]] = {}
-        for h in dst.fp32_holders(vp):
-            inst = 0 if scale_up else h.instance
-            s = src_by.get((inst, h.tp_rank, h.lo))
-            if s is None or s.hi != h.hi:
-                raise AssertionError(f"{vp.name}: no matching source shard for a Group-ZeRO copy")
+        for s, h in _backup_sources(src, dst, vp, scale_up):
+            if h.offset < in_place_below:
+                if s.offset != h.offset:
+                    raise AssertionError(f"{vp.name}: a run below the in-place bound is not at its source's offset")
+                cut = in_place_below - h.offset
+                if cut < h.hi - h.lo:
+                    b.add(0, 0, 4, s.offset + cut, in_place_below, h.hi - h.lo - cut, 1, 0, 0, group=g)
+                continue
             fills.setdefault(id(s), (s, []))[1].append(h)
         for s, hs in fills.values():
             n = s.hi - s.lo

@@ -72,6 +72,7 @@ class SharedTrainingState:
         self.tensors = tensors          # owned granules; None when imported
         self._open = tensors is None    # imported mappings not yet closed
         self._released = [False] * 4    # per arena: freed (owned) or unmapped (imported)
+        self._handed_over = set()       # owned granules now held by another state (hand_over)
         # Imported states: called with an arena's index once its mappings are closed, so that the
         # exporting process can free that arena (see :func:`release_hook`).
         self.on_release: Optional[Callable[[int], None]] = None
@@ -79,9 +80,14 @@ class SharedTrainingState:
     # ----- construction -----
     @classmethod
     def allocate(cls, layout: StrategyLayout, device=None, granule_bytes: int = DEFAULT_GRANULE_BYTES,
-                 param_granules: Optional[List[torch.Tensor]] = None) -> "SharedTrainingState":
+                 param_granules: Optional[List[torch.Tensor]] = None,
+                 adopted: Optional[Sequence[Sequence[torch.Tensor]]] = None) -> "SharedTrainingState":
         """Uninitialised granules for ``layout``, one allocation each; ``param_granules`` may be the
-        bf16 granules of another state of the same model-parallel layout, shared instead."""
+        bf16 granules of another state of the same model-parallel layout, shared instead.
+        ``adopted``: per fp32 arena (main, exp_avg, exp_avg_sq), the same number of granules of
+        another state to hold as this state's leading granules of that arena instead of allocating
+        them (a Group-ZeRO switch that leaves instance 0 in place; the other state then hands them
+        over, see :meth:`hand_over`)."""
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         if dev.type != "cuda":
             raise RuntimeError("a shared state lives in GPU memory")
@@ -89,13 +95,57 @@ class SharedTrainingState:
         keep = list(bufs.granules_of(ARENA_PARAM))
         if param_granules is not None and [t.numel() for t in param_granules] != [bufs.numel[b] for b in keep]:
             raise ValueError("the shared param granules do not match the layout")
+        held = {}
+        if adopted is not None:
+            if len(adopted) != 3 or len({len(ts) for ts in adopted}) != 1:
+                raise ValueError("adopted takes the same number of granules for each fp32 arena")
+            for a, ts in enumerate(adopted):
+                ids = bufs.granules_of(a)
+                if len(ts) > len(ids):
+                    raise ValueError("more adopted granules than the arena has")
+                for j, t in enumerate(ts):
+                    b = ids[j]
+                    if t.dtype != torch.float32 or t.numel() != bufs.numel[b] or t.device != dev \
+                            or not t.is_contiguous():
+                        raise ValueError(f"adopted granule {j} of {ARENA_NAMES[a]} does not match the layout")
+                    held[b] = t
         tensors = []
         for b, (a, n) in enumerate(zip(bufs.arena, bufs.numel)):
             if a == ARENA_PARAM and param_granules is not None:
                 tensors.append(param_granules[b - keep[0]])
+            elif b in held:
+                tensors.append(held[b])
             else:
                 tensors.append(torch.empty(n, dtype=_DTYPES[a], device=dev))
         return cls(layout, bufs, [t.data_ptr() for t in tensors], dev, tensors)
+
+    def leading_fp32_granules(self, n: int) -> List[List[torch.Tensor]]:
+        """The first ``n`` granules of every fp32 arena of an owned state, for another state to
+        adopt (``allocate(..., adopted=...)``)."""
+        if self.imported:
+            raise RuntimeError("an imported state's granules belong to the exporting process")
+        out = []
+        for a in range(3):
+            ids = self.buffers.granules_of(a)
+            if n > len(ids) or self._released[a] or any(b in self._handed_over for b in ids[:n]):
+                raise ValueError(f"{ARENA_NAMES[a]} has no {n} leading granules to give")
+            out.append([self.tensors[b] for b in ids[:n]])
+        return out
+
+    def hand_over(self, n: int) -> None:
+        """Forget the first ``n`` granules of every fp32 arena: another state adopted them and
+        owns them from now on.  Releasing this state then leaves them alone, and its pointers to
+        them read 0."""
+        if self.imported:
+            raise RuntimeError("an imported state's granules belong to the exporting process")
+        for a in range(3):
+            ids = self.buffers.granules_of(a)
+            if n > len(ids):
+                raise ValueError(f"{ARENA_NAMES[a]} has only {len(ids)} granules")
+            for b in ids[:n]:
+                self._handed_over.add(b)
+                self.tensors[b] = None
+                self._ptrs[b] = 0
 
     # ----- what the transfer manager reads -----
     @property
@@ -115,15 +165,18 @@ class SharedTrainingState:
         return self.tensors is None
 
     def buffer_ptrs(self) -> List[int]:
-        """Base pointer of every granule; 0 for the granules of a released arena."""
+        """Base pointer of every granule; 0 for the granules of a released arena and for those
+        handed over to another state."""
         if self.imported and not self._open:
             raise RuntimeError("the shared state's mappings are closed")
         return [0 if self._released[a] else p for a, p in zip(self.buffers.arena, self._ptrs)]
 
     def buffer_bytes(self) -> List[int]:
-        """Bytes of every granule; 0 for the granules of a released arena."""
+        """Bytes of every granule; 0 for the granules of a released arena and for those handed
+        over to another state."""
         nb = self.buffers.nbytes()
-        return [0 if self._released[a] else n for a, n in zip(self.buffers.arena, nb)]
+        return [0 if self._released[a] or b in self._handed_over else n
+                for b, (a, n) in enumerate(zip(self.buffers.arena, nb))]
 
     # ----- lifetime -----
     def release_kind(self, kind: int) -> None:
@@ -138,7 +191,8 @@ class SharedTrainingState:
             return
         if not self.imported:
             for b in self.buffers.granules_of(kind):
-                self.tensors[b].untyped_storage().resize_(0)
+                if b not in self._handed_over:
+                    self.tensors[b].untyped_storage().resize_(0)
             self._released[kind] = True
             return
         if not self._open:

@@ -24,7 +24,7 @@ from .. import _native
 from ..megatron_manager.parallel_strategy import ParallelStrategy
 from ..megatron_manager.training_state import TrainingState
 from ..resharding.comm_stats import FP32_TENSORS_BYTES, reference_comm_bytes
-from ..resharding.lowering import lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
+from ..resharding.lowering import in_place_prefix, lower_redundant_backup, lower_transfer, payload_bytes, read_bytes
 from ..resharding.layout import ARENA_PARAM, SEG_CAST_BF16, SEG_DUP, SEG_ZERO_FILL, StrategyLayout
 from ..resharding.shares import destination_rank_shares
 from ..resharding.granules import GranuleBuffers
@@ -64,14 +64,28 @@ def backup_kind(scale_up: bool, copy_bf16: bool = False) -> str:
 
 
 def _lower(src: StrategyLayout, dst: StrategyLayout, kind: str, include_bf16: bool, bf16_source: str,
-           with_groups: bool = False):
+           with_groups: bool = False, in_place_below: int = 0):
     """The segment table of a plan kind (with groups for verification)."""
     if kind == "transfer":
+        if in_place_below:
+            raise ValueError("only a Group-ZeRO switch can leave part of the new state in place")
         return lower_transfer(src, dst, include_bf16=include_bf16, bf16_source=bf16_source, with_groups=with_groups)
     if kind in BACKUP_KINDS:
         up, copy = BACKUP_KINDS[kind]
-        return lower_redundant_backup(src, dst, scale_up=up, with_groups=with_groups, copy_bf16=copy)
+        return lower_redundant_backup(src, dst, scale_up=up, with_groups=with_groups, copy_bf16=copy,
+                                      in_place_below=in_place_below)
     raise ValueError(kind)
+
+
+def adoptable_granules(src: StrategyLayout, dst: StrategyLayout, granule_bytes: int, kind: str) -> int:
+    """Leading granules of each fp32 arena that the new state of a Group-ZeRO switch can take over
+    from the old one instead of copying them, both held in granules of ``granule_bytes``: whole
+    granules of the same size on both sides inside :func:`in_place_prefix`.  With PP = 1 that is
+    all of instance 0, a third of a scale-up to two instances' traffic and nearly all of a
+    scale-down's.  0 for any other switch."""
+    if kind not in BACKUP_KINDS or granule_bytes is None:
+        return 0
+    return in_place_prefix(src, dst, BACKUP_KINDS[kind][0]) * 4 // granule_bytes
 
 
 def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
@@ -172,12 +186,15 @@ class TransferManager:
         return n
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                include_bf16: bool = True) -> CompiledPlan:
+                include_bf16: bool = True, in_place_below: int = 0) -> CompiledPlan:
+        """The arena plan of a switch; ``in_place_below``: see :func:`lower_redundant_backup`."""
         key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16, self.bf16_source)
+        if in_place_below:
+            key += (("in-place", in_place_below),)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        table = _lower(src, dst, kind, include_bf16, self.bf16_source)
+        table = _lower(src, dst, kind, include_bf16, self.bf16_source, in_place_below=in_place_below)
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
         if kind == "transfer":
@@ -361,16 +378,26 @@ class TransferManager:
 
     def compile_granules(self, src: StrategyLayout, dst: StrategyLayout, src_granule_bytes: Optional[int],
                          dst_granule_bytes: Optional[int], kind: str = "transfer",
-                         include_bf16: bool = True) -> CompiledTensorPlan:
+                         include_bf16: bool = True, adopt_granules: int = 0) -> CompiledTensorPlan:
         """The switch between states whose arenas are cut into granules (``SharedTrainingState``,
         handed between processes; ``None``: whole arenas, a ``TrainingState``).  ``plan.src`` /
-        ``plan.dst`` are the :class:`~..resharding.granules.GranuleBuffers` of each side."""
+        ``plan.dst`` are the :class:`~..resharding.granules.GranuleBuffers` of each side.
+
+        ``adopt_granules``: a Group-ZeRO switch whose new state holds the old one's first
+        ``adopt_granules`` granules of every fp32 arena (at most :func:`adoptable_granules`); the
+        plan writes nothing there."""
+        if adopt_granules:
+            if src_granule_bytes is None or src_granule_bytes != dst_granule_bytes:
+                raise ValueError("adopting granules needs both states in granules of one size")
+            if not 0 < adopt_granules <= adoptable_granules(src, dst, src_granule_bytes, kind):
+                raise ValueError(f"the new state cannot take over {adopt_granules} granules of the old one")
         key = ("granules", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source, src_granule_bytes, dst_granule_bytes)
+               self.bf16_source, src_granule_bytes, dst_granule_bytes, adopt_granules)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        arena_plan = self.compile(src, dst, kind, include_bf16)
+        below = adopt_granules * src_granule_bytes // 4 if adopt_granules else 0
+        arena_plan = self.compile(src, dst, kind, include_bf16, in_place_below=below)
         sb, db = GranuleBuffers(src, src_granule_bytes), GranuleBuffers(dst, dst_granule_bytes)
         table = rebase_on_tensors(arena_plan.segments, sb, db)
         cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,
@@ -403,12 +430,13 @@ class TransferManager:
         return got
 
     def plan_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
-                        dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True):
+                        dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True,
+                        adopt_granules: int = 0):
         """The arena plan when both sides are whole arenas, else the granule plan."""
-        if src_granule_bytes is None and dst_granule_bytes is None:
+        if src_granule_bytes is None and dst_granule_bytes is None and not adopt_granules:
             return self.compile(src_layout, dst_layout, kind, include_bf16)
         return self.compile_granules(src_layout, dst_layout, src_granule_bytes, dst_granule_bytes, kind,
-                                     include_bf16)
+                                     include_bf16, adopt_granules)
 
     def execute_states(self, plan, src, dst, stream: Optional[torch.cuda.Stream] = None) -> None:
         """Run ``plan`` (from :meth:`plan_for_states`) between two states of either kind."""
@@ -562,6 +590,24 @@ class TransferManager:
 def _granule_of(state) -> Optional[int]:
     """Granule size of a shared state's arenas; None for a TrainingState's whole arenas."""
     return None if isinstance(state, TrainingState) else state.granule_bytes
+
+
+def held_granules(src, dst) -> int:
+    """Leading granules of every fp32 arena (the same count in each) that ``dst`` holds in
+    ``src``'s memory, both states held in granules of one size: what a Group-ZeRO switch from
+    ``src`` into ``dst`` leaves in place (:func:`adoptable_granules`).  0 for whole arenas."""
+    gs, gd = _granule_of(src), _granule_of(dst)
+    if gs is None or gs != gd:
+        return 0
+    sp, dp = src.buffer_ptrs(), dst.buffer_ptrs()
+    n = None
+    for a in range(3):
+        si, di = src.buffers.granules_of(a), dst.buffers.granules_of(a)
+        k = 0
+        while k < min(len(si), len(di)) and sp[si[k]] and sp[si[k]] == dp[di[k]]:
+            k += 1
+        n = k if n is None else min(n, k)
+    return n
 
 
 def shares_params(src, dst) -> bool:

@@ -235,12 +235,14 @@ typedef struct emrs_compare_stats {
  *   groups[i]:     group of input segment i's elements (NULL: all group 0)
  *   aux_groups[i]: group of input segment i's bf16 image (NULL: groups[i])
  *   stats:         n_groups host records, filled when the call returns
- * Base pointers follow emrs_plan_execute's rules.  The call runs on `stream`
+ * Base pointers follow emrs_plan_execute's rules, except that buffers may
+ * overlap: a comparison only reads (a state that took over part of its
+ * source's memory compares equal there).  The call runs on `stream`
  * and waits for it.  It allocates and frees a small device buffer (the
  * group tables and accumulators), so it is not for capture into a graph:
  * while `stream` is capturing it returns EMRS_ERR_CAPTURE.
  * Errors: INVALID_ARGUMENT (n_groups == 0, a group id >= n_groups), the
- * base-pointer errors of emrs_plan_execute, CAPTURE, NO_DEVICE, HIP.
+ * base-pointer errors of emrs_plan_execute but ALIAS, CAPTURE, NO_DEVICE, HIP.
  */
 int emrs_plan_compare(emrs_plan *plan, void *const *src_bases, void *const *dst_bases,
                       const uint32_t *groups, const uint32_t *aux_groups, uint32_t n_groups,

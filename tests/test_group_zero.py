@@ -13,7 +13,7 @@ import pytest
 
 from elasticmegatron_amd import ParallelStrategy as PS
 from elasticmegatron_amd.resharding.layout import SEG_DUP
-from elasticmegatron_amd.resharding.lowering import lower_redundant_backup, payload_bytes, read_bytes
+from elasticmegatron_amd.resharding.lowering import in_place_prefix, lower_redundant_backup, payload_bytes, read_bytes
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from oracle import model
 from oracle import transfer as oracle1
@@ -113,3 +113,71 @@ def test_bf16_copy_writes_the_generator_params(name, small, big, up):
     b[3][h.offset + 5] ^= 1
     stats = compare_numpy(tg, groups, aux_groups, n_groups, a, b)
     assert np.flatnonzero(stats["mismatches"]).tolist() == [4 * 3]
+
+
+def _in_place_run(src, dst, scale_up, below):
+    """The switch with the new arenas' head below ``below`` taken over from the old arenas (their
+    bits copied in before the plan runs, as adopted memory would hold them)."""
+    spec = small_llama2()
+    inv = model.inventory(spec)
+    S, D = strat(src), strat(dst)
+    world = oracle1.build_src_world(inv, spec, S, SEED)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, world, scale_up))
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    table = lower_redundant_backup(ls, ld, scale_up, in_place_below=below)
+    a, b = new_arenas(ls), new_arenas(ld)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    for k in range(3):
+        b[k][:below] = a[k][:below]
+    execute_numpy(table, a, b)
+    got, _ = extract(ld, b)
+    return table, got, want
+
+
+def _writes_below(table, below):
+    """Destination elements below ``below`` that the table writes (first copy and duplicate)."""
+    first = (table["dst_off"] < below).any()
+    dup = (table["flags"] & SEG_DUP) != 0
+    return bool(first or (table["aux_off"][dup] < below).any())
+
+
+@pytest.mark.parametrize("name,small,big", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("scale_up", [True, False], ids=["up", "down"])
+def test_in_place_head_matches_oracle(name, small, big, scale_up):
+    """A new state holding the old one's head: the plan writes nothing there, and the state it
+    completes is the oracle's, at the full in-place prefix and at a bound that cuts runs."""
+    src, dst = (small, big) if scale_up else (big, small)
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(src), space.layout(dst)
+    prefix = in_place_prefix(ls, ld, scale_up)
+    if small.pipeline_model_parallel_size == 1:
+        # PP = 1: instance 0 is the head of both worlds, and it is all of the smaller one.
+        assert prefix == min(ls.fp32_numel, ld.fp32_numel)
+    else:
+        assert 0 < prefix < min(ls.fp32_numel, ld.fp32_numel)
+    full = lower_redundant_backup(ls, ld, scale_up)
+    for below in (prefix, prefix // 3 + 17):
+        table, got, want = _in_place_run(src, dst, scale_up, below)
+        assert compare(got, {}, want, {}) == []
+        assert not _writes_below(table, below)
+        assert payload_bytes(table) < payload_bytes(full)
+    inst = big.num_distributed_optimizer_instances
+    table, _, _ = _in_place_run(src, dst, scale_up, prefix)
+    if small.pipeline_model_parallel_size == 1 and scale_up:
+        # Instance 0 stays: inst - 1 copies written, read once per pair of them.
+        assert payload_bytes(table) * inst == payload_bytes(full) * (inst - 1)
+        assert read_bytes(table) * inst == payload_bytes(full) * (inst // 2)
+    elif small.pipeline_model_parallel_size == 1:
+        assert payload_bytes(table) == 0 and read_bytes(table) == 0
+
+
+def test_in_place_bound_past_the_prefix_is_refused():
+    """A bound past the in-place prefix would leave a run that is not at its source's offset
+    unwritten: the lowering refuses it."""
+    small, big = CASES[2][1], CASES[2][2]          # PP 2: the prefix ends inside the arenas
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(small), space.layout(big)
+    prefix = in_place_prefix(ls, ld, True)
+    with pytest.raises(AssertionError, match="not at its source's offset"):
+        lower_redundant_backup(ls, ld, True, in_place_below=prefix + 1)

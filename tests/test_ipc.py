@@ -21,7 +21,8 @@ from elasticmegatron_amd.resharding.granules import GranuleBuffers
 from elasticmegatron_amd.resharding.model_spec import ModelSpec, llama2_7b, tiny_llama2
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer import ipc_manager as ipc
-from elasticmegatron_amd.transfer.transfer import CompiledTensorPlan
+from elasticmegatron_amd.transfer.transfer import (CompiledTensorPlan, TransferManager, adoptable_granules, held_granules,
+                                                   shares_params)
 from tests.helpers import small_llama2
 
 
@@ -186,6 +187,82 @@ def test_group_zero_from_a_received_state_copies_the_params():
     stored = sum(h.hi - h.lo for vp in mgr.virtual_param_space.all_virtual_params
                  for h in state.layout.bf16_holders(vp))
     assert int((bf16["len"].astype(np.int64) * bf16["rows"]).sum()) == stored
+
+
+def _owned_cpu(layout, granule, adopted=None, param=None):
+    """An owned state's bookkeeping over host tensors (the ownership rules need no device)."""
+    bufs = GranuleBuffers(layout, granule)
+    held = {}
+    for a, ts in enumerate(adopted or ()):
+        held.update(zip(bufs.granules_of(a), ts))
+    pg = list(bufs.granules_of(3))
+    ts = [held[b] if b in held else param[b - pg[0]] if (param is not None and b in pg) else
+          torch.zeros(n, dtype=torch.bfloat16 if a == 3 else torch.float32)
+          for b, (a, n) in enumerate(zip(bufs.arena, bufs.numel))]
+    return ipc.SharedTrainingState(layout, bufs, [t.data_ptr() for t in ts], torch.device("cpu"), ts)
+
+
+def test_group_zero_new_state_takes_over_instance_0_granules():
+    """A state built for a Group-ZeRO scale-up holds the old state's leading fp32 granules; once the
+    old state hands them over, releasing it frees everything else and leaves them to the new one."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(4, 1, 1)), space.layout(PS(8, 1, 1, num_distributed_optimizer_instances=2))
+    g = 1 << 14
+    n = adoptable_granules(ls, ld, g, "backup_up")
+    assert n == ls.fp32_numel * 4 // g and n > 1
+    assert adoptable_granules(ls, ld, g, "transfer") == 0
+    old = _owned_cpu(ls, g)
+    new = _owned_cpu(ld, g, old.leading_fp32_granules(n), [old.tensors[b] for b in old.buffers.granules_of(3)])
+    assert held_granules(old, new) == n and shares_params(old, new)
+    kept = [new.tensors[b] for a in range(3) for b in new.buffers.granules_of(a)[:n]]
+    for i, t in enumerate(kept):
+        t.fill_(float(i + 1))
+    others = [old.tensors[b] for a in range(3) for b in old.buffers.granules_of(a)[n:]]
+    old.hand_over(n)
+    old.release_optimizer()
+    assert all(t.untyped_storage().nbytes() == 0 for t in others)
+    assert all(t.untyped_storage().nbytes() == t.numel() * 4 and bool((t == i + 1).all()) for i, t in enumerate(kept))
+    ptrs, nbytes = old.buffer_ptrs(), old.buffer_bytes()
+    assert all(ptrs[b] == 0 and nbytes[b] == 0 for a in range(3) for b in old.buffers.granules_of(a))
+    with pytest.raises(ValueError):
+        old.leading_fp32_granules(1)
+    assert held_granules(old, new) == 0
+
+
+def test_adoption_is_refused_where_it_cannot_hold():
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(4, 1, 1)), space.layout(PS(8, 1, 1, num_distributed_optimizer_instances=2))
+    tm = TransferManager()
+    g = 1 << 14
+    n = ls.fp32_numel * 4 // g
+    with pytest.raises(ValueError):
+        tm.compile_granules(ls, ld, g, g, "backup_up", adopt_granules=n + 1)   # past instance 0
+    with pytest.raises(ValueError):
+        tm.compile_granules(ls, ld, g, 2 * g, "backup_up", adopt_granules=1)   # two granule sizes
+    with pytest.raises(ValueError):
+        tm.compile_granules(ls, ld, g, g, "transfer", adopt_granules=1)       # not Group ZeRO
+    with pytest.raises(RuntimeError):
+        _fake_shared(ls, g).hand_over(1)                                        # not this process's memory
+    plan = tm.compile_granules(ls, ld, g, g, "backup_up", adopt_granules=n)
+    head = {b for a in range(3) for b in plan.dst.granules_of(a)[:n]}
+    written = set(plan.dst_refs)
+    assert not head & written and set(range(3 * len(plan.dst.granules_of(0)))) - head <= written
+
+
+def test_manager_plans_the_adopting_switch_for_an_owned_shared_state():
+    """Group ZeRO from a shared state this process owns and releases: the plan leaves the adoptable
+    head in place.  Without release_source the old state must stay whole, so nothing is taken over."""
+    spec = small_llama2()
+    src, dst = PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
+    g = 1 << 14
+    for release, want in ((True, True), (False, False)):
+        mgr = ElasticMegatronManager([src, dst], spec, device="meta", share_granule_bytes=g, release_source=release)
+        state = _owned_cpu(mgr.virtual_param_space.layout(src), g)
+        mgr.attach_training_state(state)
+        assert mgr.reshard(dst, is_meta_device=True) is None
+        keys = [k for k in mgr.transfer_manager._plans if k[0] == "granules"]
+        assert len(keys) == 1 and keys[0][5] == "backup_up"
+        assert (keys[0][-1] == state.layout.fp32_numel * 4 // g) is want and (keys[0][-1] == 0) is not want
 
 
 def test_low_memory_refuses_to_allocate_shared_states():

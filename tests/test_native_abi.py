@@ -220,6 +220,29 @@ def test_alias_checks_before_any_device_work(n_bufs):
     assert e.value.code == -3
 
 
+@pytest.mark.parametrize("n_bufs", [2, 300])
+def test_compare_accepts_overlapping_buffers(n_bufs):
+    """A comparison only reads: a destination overlapping a source (a state that took over part of
+    its source's memory) passes its base checks, where an execution refuses it."""
+    plan = _two_seg_plan(n_bufs)
+    base = 1 << 40
+    src = [base + i * 4096 for i in range(n_bufs)]
+    dst = list(src)                      # every destination is its source's memory
+    with pytest.raises(_native.EmrsError) as e:
+        plan.execute(src, dst, 0)
+    assert e.value.code == -8
+    if torch.cuda.is_available():
+        return
+    with pytest.raises(_native.EmrsError) as e:
+        plan.compare(src, dst)
+    assert e.value.code == -6            # got as far as looking for a device
+    bad = list(dst)
+    bad[0] += 8
+    with pytest.raises(_native.EmrsError) as e:
+        plan.compare(src, bad)
+    assert e.value.code == -3            # alignment is still checked
+
+
 def test_xor_checksum_rejects_bad_arguments_before_touching_a_device():
     with pytest.raises(_native.EmrsError) as e:
         _native.xor_checksum(0x1000, 16, 0)               # no output word
