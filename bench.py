@@ -24,6 +24,7 @@ parameter costs 12 bytes read and 14 written).
 
 import argparse
 import json
+import logging
 import os
 import sys
 import time
@@ -62,6 +63,11 @@ def workloads():
         "llama2-7b-groupzero-1-2": ("Llama-2-7B Group ZeRO instances 1 -> 2 (world 6 -> 12), fp32 only",
                                     ms.llama2_7b, PS(6, 1, 1),
                                     PS(12, 1, 1, num_distributed_optimizer_instances=2)),
+        "llama2-7b-groupzero-2-1": ("Llama-2-7B Group ZeRO instances 2 -> 1 (world 12 -> 6), fp32 only",
+                                    ms.llama2_7b, PS(12, 1, 1, num_distributed_optimizer_instances=2),
+                                    PS(6, 1, 1)),
+        "tiny-llama2-groupzero-1-2": ("tiny LLaMA-2 (2L h512) Group ZeRO instances 1 -> 2 (world 4 -> 8), fp32 only",
+                                      ms.tiny_llama2, PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
         # 182 GB per state: only a staged switch (--low-memory) fits it on one GPU.
         "llama2-13b-tp1dp8-tp4dp2": ("Llama-2-13B TP1PP1DP8 -> TP4PP1DP2, world 8, 40M buckets",
                                      ms.llama2_13b, PS(8, 1, 1), PS(8, 4, 1)),
@@ -158,6 +164,10 @@ def parse():
                     help="the switch from another process's state: a child exports the source in granules "
                          "(--ipc-granule-bytes), this process maps them and reshards into its own arenas")
     ap.add_argument("--ipc-granule-bytes", type=int, default=1 << 30)
+    ap.add_argument("--adopt", action="store_true",
+                    help="Group-ZeRO workloads: time the switch between shared states (granules of "
+                         "--ipc-granule-bytes) with instance 0 copied and with the new state taking it over, launch "
+                         "and ElasticMegatronManager.reshard end to end")
     ap.add_argument("--low-memory", action="store_true",
                     help="time staged switches through ElasticMegatronManager(low_memory=True), alternating "
                          "directions: one optimizer kind per launch, arenas allocated and released as it goes")
@@ -280,6 +290,8 @@ def main():
         return bench_megatron_buffers(args, desc, spec_fn, src, dst, dev, stream)
     if args.ipc:
         return bench_ipc(args, desc, spec_fn, src, dst, dev, stream)
+    if args.adopt:
+        return bench_adopt(args, desc, spec_fn, src, dst, dev, stream)
     repad = bool(opt and opt[0])
     backup = ParallelStrategy.is_redundant_backup(src, dst)
     spec = spec_fn()
@@ -692,6 +704,116 @@ def bench_ipc(args, desc, spec_fn, src, dst, dev, stream):
                    "min_ms": round(min(step_ms), 4), "max_ms": round(max(step_ms), 4), "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": round(traffic_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(traffic_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def timed_launches(run, steps, warmup, stream):
+    """ms of each of ``steps`` launches of ``run`` after ``warmup`` untimed ones (events on
+    ``stream``, the launches' own stream)."""
+    import torch
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    events[0].record(stream)
+    for i in range(steps):
+        run()
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+
+
+def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
+    """A Group-ZeRO switch between shared states this process owns: the new state either gets
+    instance 0 copied into granules of its own, or takes over the old state's leading granules
+    (all of instance 0) and the plan writes only the other instances.  Both launches are timed on
+    the same source, one after the other (two new states do not fit beside the source), each
+    checked against the generator; then ElasticMegatronManager.reshard runs end to end both ways
+    (without release_source the old state is kept whole, so nothing is taken over).  Every new
+    state's granules come from torch's cache, as in a running job: memory handed back to the driver
+    is cleared before it is handed out again, at tens of GB/s, which would swamp the comparison."""
+    import gc
+
+    import torch
+
+    from elasticmegatron_amd import ElasticMegatronManager
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+    from elasticmegatron_amd.transfer.transfer import TransferManager, adoptable_granules, backup_kind
+
+    backup = ParallelStrategy.is_redundant_backup(src, dst)
+    if backup is None:
+        print("--adopt times a Group-ZeRO workload", file=sys.stderr)
+        return 2
+    g, kind = args.ipc_granule_bytes, backup_kind(backup)
+    spec = spec_fn()
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    n = adoptable_granules(ls, ld, g, kind)
+    tm = TransferManager(bf16_source=args.bf16_source)
+    plans = {"copied": tm.compile_granules(ls, ld, g, g, kind), "taken_over": tm.compile_granules(ls, ld, g, g, kind,
+                                                                                                  adopt_granules=n)}
+    a = SharedTrainingState.allocate(ls, dev, g)
+    a.fill_synthetic(SEED)
+    param = [a.tensors[x] for x in a.buffers.granules_of(3)]
+    res = {}
+    for name, plan in plans.items():
+        torch.cuda.reset_peak_memory_stats(dev)
+        before = torch.cuda.memory_allocated(dev)
+        b = SharedTrainingState.allocate(ld, dev, g, param_granules=param,
+                                         adopted=a.leading_fp32_granules(n) if name == "taken_over" else None)
+        new_bytes = torch.cuda.memory_allocated(dev) - before
+        tm.prepare(plan, dev)
+        step_ms = timed_launches(lambda: tm.execute_states(plan, a, b, stream), args.steps, args.warmup, stream)
+        bad, first = b.verify_synthetic(SEED)
+        exact = bad == 0 and tm.verify(a, b, kind).bit_exact
+        if not exact:
+            print(f"[bench] {name}: verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+            return 3
+        ms = sum(step_ms) / len(step_ms)
+        res[name] = {"ms": round(ms, 3), "min_ms": round(min(step_ms), 3), "payload_bytes": plan.payload_bytes,
+                     "traffic_bytes": plan.payload_bytes + plan.read_bytes, "new_state_allocated_bytes": new_bytes,
+                     "traffic_gbps": round((plan.payload_bytes + plan.read_bytes) / ms / 1e6, 1),
+                     "verified_bit_exact": exact}
+        print(f"[bench] {name}: {ms:.2f} ms, {res[name]['traffic_gbps']} GB/s", file=sys.stderr, flush=True)
+        del b
+        gc.collect()      # the granules stay in torch's cache for the next state
+
+    def manager_switch(release):
+        mgr = ElasticMegatronManager([src, dst], spec, device=dev, training_state=a, share_granule_bytes=g,
+                                     release_source=release)
+        mgr.reshard(dst, is_meta_device=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        new = mgr.reshard(dst, logger=logging.getLogger("bench"))     # keeps stdout to the JSON line
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        bad, _ = new.verify_synthetic(SEED)
+        return new, {"wall_ms": round(wall, 2), "launch_ms": round(mgr.last_transfer_ms, 2), "verified_bit_exact": bad == 0}
+
+    kept, e2e_copy = manager_switch(False)
+    del kept
+    gc.collect()
+    _, e2e_adopt = manager_switch(True)         # releases the source: last
+    if not (e2e_copy["verified_bit_exact"] and e2e_adopt["verified_bit_exact"]):
+        print("[bench] a manager switch FAILED verification", file=sys.stderr)
+        return 3
+    res["copied"]["reshard_end_to_end"], res["taken_over"]["reshard_end_to_end"] = e2e_copy, e2e_adopt
+    t = res["taken_over"]
+    out = {
+        "metric": f"Group-ZeRO switch between shared states, instance 0 taken over: ms per launch, {desc}, 1 GPU",
+        "value": t["ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t["ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (bitwise copy)", "data": "synthetic (seeded)",
+        "config": {"workload": desc + f", both states in {g}-byte granules", "params": spec.num_params(),
+                   "granules_taken_over_per_fp32_arena": n, "speedup_vs_copied": round(res["copied"]["ms"] / t["ms"], 3),
+                   **res, "launch": launch_shape()},
+        "roofline": {"bound": "hbm", "achieved": t["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -91,3 +91,17 @@ def test_copy_shapes_line(gpu_device):
                "--steps", "1", "--warmup", "1")
     assert [r["shape"] for r in d["shapes"]] == ["default", {"units": 2}, {"persistent": 1}]
     assert all(len(r["ms"]) == 2 and r["best_TBps"] > 0 for r in d["shapes"])
+
+
+@pytest.mark.gpu
+def test_adopt_line(gpu_device):
+    """--adopt: a Group-ZeRO switch between shared states with instance 0 copied and taken over, each
+    checked, and the taken-over launch moving a third less (instance 0's last partial granule aside)."""
+    d = _bench("--workload", "tiny-llama2-groupzero-1-2", "--adopt", "--ipc-granule-bytes", str(1 << 16),
+               "--steps", "2", "--warmup", "1")
+    c = d["config"]
+    assert c["granules_taken_over_per_fp32_arena"] > 0
+    for k in ("copied", "taken_over"):
+        assert c[k]["verified_bit_exact"] is True and c[k]["reshard_end_to_end"]["verified_bit_exact"] is True
+    assert abs(c["taken_over"]["traffic_bytes"] / c["copied"]["traffic_bytes"] - 2 / 3) < 0.01
+    assert c["taken_over"]["new_state_allocated_bytes"] < c["copied"]["new_state_allocated_bytes"]
