@@ -10,6 +10,8 @@ odd instance counts.
 
 import numpy as np
 import pytest
+from hypothesis import HealthCheck, assume, given, settings
+from hypothesis import strategies as st
 
 from elasticmegatron_amd import ParallelStrategy as PS
 from elasticmegatron_amd.resharding.layout import SEG_DUP
@@ -18,6 +20,7 @@ from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from oracle import model
 from oracle import transfer as oracle1
 from tests.helpers import SEED, compare, compare_numpy, execute_numpy, extract, new_arenas, piece_fill_numpy, small_llama2, strat
+from tests.test_plan_properties import switches
 
 CASES = [
     ("1to2", PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
@@ -181,3 +184,48 @@ def test_in_place_bound_past_the_prefix_is_refused():
     prefix = in_place_prefix(ls, ld, True)
     with pytest.raises(AssertionError, match="not at its source's offset"):
         lower_redundant_backup(ls, ld, True, in_place_below=prefix + 1)
+
+
+@st.composite
+def _group_zero_switches(draw):
+    spec, a, _ = draw(switches())
+    assume(not spec.num_experts)          # Group ZeRO with experts is refused
+    k, cp, up = draw(st.sampled_from([2, 3, 4])), draw(st.sampled_from([1, 2])), draw(st.booleans())
+    tp, pp = a.tensor_model_parallel_size, a.pipeline_model_parallel_size
+    try:
+        small = PS(a.world_size * cp, tp, pp, context_parallel_size=cp)
+        big = PS(a.world_size * cp * k, tp, pp, context_parallel_size=cp, num_distributed_optimizer_instances=k)
+        for s in (small, big):
+            s.validate_for(spec.num_layers, spec.num_experts)
+    except (AssertionError, ValueError, RuntimeError):
+        assume(False)
+    return spec, small, big, up, draw(st.integers(1, 400).map(lambda x: 256 * x))
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.filter_too_much, HealthCheck.too_slow])
+@given(_group_zero_switches())
+def test_random_in_place_head_leaves_what_the_full_plan_leaves(sw):
+    """Random models, instance counts, PP and CP sizes, directions and granule sizes: a new state
+    holding the old one's whole granules inside the in-place prefix, completed by the plan that
+    leaves them alone, holds what the full plan writes, and nothing below the bound is written."""
+    spec, small, big, up, g = sw
+    src, dst = (small, big) if up else (big, small)
+    space = build_virtual_model(spec)
+    try:
+        ls, ld = space.layout(src), space.layout(dst)
+    except (AssertionError, RuntimeError, ValueError):
+        assume(False)
+    below = in_place_prefix(ls, ld, up) * 4 // g * (g // 4)
+    full = lower_redundant_backup(ls, ld, up)
+    head = lower_redundant_backup(ls, ld, up, in_place_below=below)
+    assert not _writes_below(head, below)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    want, got = new_arenas(ld), new_arenas(ld)
+    execute_numpy(full, a, want)
+    for k in range(3):
+        got[k][:below] = a[k][:below]
+    execute_numpy(head, a, got)
+    w, _ = extract(ld, want)
+    h, _ = extract(ld, got)
+    assert compare(h, {}, w, {}) == []
