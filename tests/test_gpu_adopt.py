@@ -124,3 +124,19 @@ def test_random_adopting_switch(gpu_device, spec, small, big, up, m):
     bad, first = b.verify_synthetic(SEED)
     assert bad == 0, first
     del junk
+
+
+def test_hand_off_of_a_state_holding_taken_over_granules(gpu_device):
+    """The old process reached its strategy by a Group-ZeRO scale-up that took over instance 0, so
+    the state it exports holds granules adopted from the state before.  Mapped in this process and
+    switched back down (the bf16 params copied, since the exporter frees its memory), every element
+    holds the generator's value."""
+    from tests.test_gpu_ipc import _hand_off
+
+    src, dst = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1)
+    print(f"case hand-off of a taken-over state: child {dst} -> {src}, then here -> {dst}", flush=True)
+    mgr, new, n_granules, n_mapped = _hand_off(gpu_device, small_llama2(), src, dst, (1 << 20) + 256 * 3, 240,
+                                               start_from=dst)
+    print(f"  {n_granules} granules in {n_mapped} allocations", flush=True)
+    bad, first = new.verify_synthetic(SEED)
+    assert bad == 0, first

@@ -31,11 +31,13 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _spawn_exporter(spec, strategy, granule_bytes):
+def _spawn_exporter(spec, strategy, granule_bytes, start_from=None):
     cmd = [sys.executable, "-m", "elasticmegatron_amd.transfer.ipc_export",
            "--model-spec", json.dumps(dataclasses.asdict(spec)),
            "--strategy", json.dumps(ipc.strategy_to_dict(strategy)),
            "--seed", str(SEED), "--granule-bytes", str(granule_bytes), "--misc", json.dumps({"iteration": 42})]
+    if start_from is not None:
+        cmd += ["--start-from", json.dumps(ipc.strategy_to_dict(start_from))]
     return subprocess.Popen(cmd, cwd=ROOT, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
 
 
@@ -76,10 +78,11 @@ def _host_arenas(state):
         + [arenas[3].view(torch.int16).cpu().numpy().view("uint16")]
 
 
-def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s, share=None):
+def _hand_off(gpu_device, spec, src, dst, granule_bytes, timeout_s, share=None, start_from=None):
     """Export in a child, receive, attach and reshard; returns (manager, new state, granules, mapped).
-    ``share``: the new state is held in granules of that size too."""
-    child = _spawn_exporter(spec, src, granule_bytes)
+    ``share``: the new state is held in granules of that size too.  ``start_from``: the child
+    reaches ``src`` by a reshard from that strategy before it exports."""
+    child = _spawn_exporter(spec, src, granule_bytes, start_from)
     state = None
     try:
         mgr = ElasticMegatronManager([src, dst], spec, device="meta", share_granule_bytes=share)
