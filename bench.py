@@ -776,8 +776,8 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
             return 3
         ms = sum(step_ms) / len(step_ms)
         res[name] = {"ms": round(ms, 3), "min_ms": round(min(step_ms), 3), "payload_bytes": plan.payload_bytes,
-                     "traffic_bytes": plan.payload_bytes + plan.read_bytes, "new_state_allocated_bytes": new_bytes,
-                     "traffic_gbps": round((plan.payload_bytes + plan.read_bytes) / ms / 1e6, 1),
+                     "traffic_bytes": plan.traffic_bytes, "new_state_allocated_bytes": new_bytes,
+                     "traffic_gbps": round(plan.traffic_bytes / ms / 1e6, 1),
                      "verified_bit_exact": exact}
         print(f"[bench] {name}: {ms:.2f} ms, {res[name]['traffic_gbps']} GB/s", file=sys.stderr, flush=True)
         del b
@@ -813,7 +813,8 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
                    "granules_taken_over_per_fp32_arena": n, "speedup_vs_copied": round(res["copied"]["ms"] / t["ms"], 3),
                    **res, "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": t["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": committed_traffic(f"{args.workload}.taken_over", None, t["traffic_bytes"])},
     }
     print(json.dumps(out), flush=True)
     return 0

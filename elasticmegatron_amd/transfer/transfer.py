@@ -136,6 +136,11 @@ class CompiledTensorPlan:
     src_refs: Tuple[int, ...] = None   # buffers the plan reads
     dst_refs: Tuple[int, ...] = None   # buffers the plan writes
 
+    @property
+    def traffic_bytes(self) -> int:
+        """Algorithmic HBM traffic per execution: every byte read once and written once."""
+        return self.payload_bytes + self.read_bytes
+
     def __post_init__(self):
         if self.buffer_nbytes is None:
             self.buffer_nbytes = self.src.nbytes() + self.dst.nbytes()

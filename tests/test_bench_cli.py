@@ -13,7 +13,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402
 from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy  # noqa: E402
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model  # noqa: E402
-from elasticmegatron_amd.transfer.transfer import TransferManager  # noqa: E402
+from elasticmegatron_amd.transfer.transfer import TransferManager, adoptable_granules  # noqa: E402
 
 
 def _run(*args):
@@ -74,7 +74,8 @@ def test_committed_traffic_describes_the_current_plan(traffic_file):
     """Each committed PMC summary was measured on the plan its workload lowers to today (same
     algorithmic bytes), so bench.py quotes it; a stale one would be ignored, and this fails first."""
     name = traffic_file[:-len(".traffic.json")]
-    desc, spec_fn, src, dst, *opt = bench.workloads()[name]
+    workload, _, variant = name.partition(".")
+    desc, spec_fn, src, dst, *opt = bench.workloads()[workload]
     spec = spec_fn()
     backup = ParallelStrategy.is_redundant_backup(src, dst)
     if opt and opt[0]:
@@ -84,7 +85,12 @@ def test_committed_traffic_describes_the_current_plan(traffic_file):
         space = build_virtual_model(spec)
         ls, ld = space.layout(src), space.layout(dst)
     kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
-    plan = TransferManager().compile(ls, ld, kind)
+    if variant == "taken_over":   # bench.py --adopt: 1 GiB granules, instance 0 taken over
+        g = 1 << 30
+        plan = TransferManager().compile_granules(ls, ld, g, g, kind, adopt_granules=adoptable_granules(ls, ld, g, kind))
+    else:
+        assert variant == ""
+        plan = TransferManager().compile(ls, ld, kind)
     with open(os.path.join(ROOT, "profiles", traffic_file)) as f:
         rec = json.load(f)
     assert bench.committed_traffic(name, "cast" if backup is None else None, plan.traffic_bytes) == \
