@@ -36,8 +36,7 @@ from .resharding.model_spec import ModelSpec
 from .resharding.util import Timer
 from .resharding.virtual_param import VirtualParamSpace, build_virtual_model
 from .transfer.ipc_manager import SharedTrainingState
-from .transfer.transfer import (BACKUP_KINDS, TransferManager, _granule_of, adoptable_granules, backup_kind,
-                                held_granules, shares_params)
+from .transfer.transfer import BACKUP_KINDS, TransferManager, _granule_of, backup_kind, held_granules, shares_params
 from .transfer.verify import merge_stats, report_from_stats
 
 StrategyLike = Union[ParallelStrategy, Dict[str, int]]
@@ -278,7 +277,7 @@ class ElasticMegatronManager:
         if not isinstance(src_state, SharedTrainingState) or src_state.imported \
                 or src_state.granule_bytes != dst_granule_bytes:
             return 0
-        return adoptable_granules(src_state.layout, dst_layout, dst_granule_bytes, kind)
+        return self.transfer_manager.adoptable(src_state.layout, dst_layout, dst_granule_bytes, kind)
 
     @staticmethod
     def _carried_params(src_state, dst_granule_bytes):

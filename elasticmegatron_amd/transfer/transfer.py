@@ -170,6 +170,7 @@ class TransferManager:
         self.fake_transfer = False
         self._verify_plans: Dict[Tuple, Tuple] = {}
         self._checked_tensors: Dict[int, Tuple] = {}   # per plan: the pointers last checked
+        self._adoptable: Dict[Tuple, int] = {}
         self._payload_bytes = 0
         self._comm_bytes = 0
 
@@ -188,6 +189,16 @@ class TransferManager:
                 n += 1
         live = {id(p) for p in self._plans.values()}
         self._checked_tensors = {k: v for k, v in self._checked_tensors.items() if k in live}
+        self._adoptable = {k: v for k, v in self._adoptable.items()
+                           if not (strategy is None or any(x == strategy for x in k))}
+        return n
+
+    def adoptable(self, src: StrategyLayout, dst: StrategyLayout, granule_bytes: Optional[int], kind: str) -> int:
+        """:func:`adoptable_granules`, kept per switch (it walks every parameter's runs)."""
+        key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, granule_bytes, kind)
+        n = self._adoptable.get(key)
+        if n is None:
+            n = self._adoptable[key] = adoptable_granules(src, dst, granule_bytes, kind)
         return n
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
@@ -391,16 +402,16 @@ class TransferManager:
         ``adopt_granules``: a Group-ZeRO switch whose new state holds the old one's first
         ``adopt_granules`` granules of every fp32 arena (at most :func:`adoptable_granules`); the
         plan writes nothing there."""
-        if adopt_granules:
-            if src_granule_bytes is None or src_granule_bytes != dst_granule_bytes:
-                raise ValueError("adopting granules needs both states in granules of one size")
-            if not 0 < adopt_granules <= adoptable_granules(src, dst, src_granule_bytes, kind):
-                raise ValueError(f"the new state cannot take over {adopt_granules} granules of the old one")
         key = ("granules", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
                self.bf16_source, src_granule_bytes, dst_granule_bytes, adopt_granules)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
+        if adopt_granules:
+            if src_granule_bytes is None or src_granule_bytes != dst_granule_bytes:
+                raise ValueError("adopting granules needs both states in granules of one size")
+            if not 0 < adopt_granules <= self.adoptable(src, dst, src_granule_bytes, kind):
+                raise ValueError(f"the new state cannot take over {adopt_granules} granules of the old one")
         below = adopt_granules * src_granule_bytes // 4 if adopt_granules else 0
         arena_plan = self.compile(src, dst, kind, include_bf16, in_place_below=below)
         sb, db = GranuleBuffers(src, src_granule_bytes), GranuleBuffers(dst, dst_granule_bytes)
