@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy as PS
+from elasticmegatron_amd.resharding.granules import GranuleBuffers
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
 from elasticmegatron_amd.transfer.transfer import TransferManager, adoptable_granules, backup_kind
@@ -140,3 +141,43 @@ def test_hand_off_of_a_state_holding_taken_over_granules(gpu_device):
     print(f"  {n_granules} granules in {n_mapped} allocations", flush=True)
     bad, first = new.verify_synthetic(SEED)
     assert bad == 0, first
+
+
+def test_failed_switch_leaves_the_old_state_whole(gpu_device, monkeypatch):
+    """A switch whose verification fails raises, and the old state stays the live state with every
+    granule it lent to the new one: nothing is handed over before the check passes.  The new
+    state's own memory, freed with it, is handed out again and filled with NaN first; then the
+    same switch runs clean."""
+    import gc
+
+    g = 1 << 16
+    small, big = PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)
+    mgr = ElasticMegatronManager([small, big], small_llama2(), device=gpu_device, share_granule_bytes=g)
+    old = mgr.training_state
+    old.fill_synthetic(SEED)
+    ld = mgr.space_for(big).layout(big)
+    vp = next(v for v in ld.space.all_virtual_params if ld.has_param(v))
+    h = next(x for x in ld.fp32_holders(vp) if x.instance == 1)
+    real = mgr.transfer_manager.execute_states
+
+    def corrupting(plan, src, dst, stream=None):
+        real(plan, src, dst, stream)
+        b, off = dst.buffers.locate(1, h.offset)     # an exp_avg element of instance 1: written, not taken over
+        dst.tensors[b].view(torch.int32)[off] ^= 1
+
+    monkeypatch.setattr(mgr.transfer_manager, "execute_states", corrupting)
+    print("case failed switch with instance 0 lent to the new state", flush=True)
+    with pytest.raises(RuntimeError, match="verification failed"):
+        mgr.reshard(big, verify=True)
+    assert mgr.training_state is old
+    gc.collect()
+    n, gb = adoptable_granules(old.layout, ld, g, "backup_up"), GranuleBuffers(ld, g)
+    junk = _reuse_freed([gb.numel[b] for a in range(3) for b in gb.granules_of(a)[n:]], gpu_device)
+    torch.cuda.synchronize()
+    bad, first = old.verify_synthetic(SEED)
+    assert bad == 0, first
+    del junk
+    monkeypatch.undo()
+    new = mgr.reshard(big, verify=True)
+    torch.cuda.synchronize()
+    assert mgr.last_verification.bit_exact and new.verify_synthetic(SEED)[0] == 0
