@@ -277,6 +277,9 @@ class SharedTrainingState:
         """One emrs_ipc_buffer record per granule (ipc_manager.py:23-51)."""
         if self.imported:
             raise RuntimeError("an imported state is exported by the process that owns it")
+        if any(self._released) or self._handed_over:
+            raise RuntimeError("part of this state is released or handed over to another state: only a whole "
+                               "state can be exported")
         with torch.cuda.device(self._device):
             return [_native.ipc_export(p, n) for p, n in zip(self._ptrs, self.buffers.nbytes())]
 

@@ -229,6 +229,18 @@ def test_group_zero_new_state_takes_over_instance_0_granules():
     assert held_granules(old, new) == 0
 
 
+def test_export_refuses_a_state_that_is_not_whole():
+    """A released arena's granules are freed and handed-over ones belong to another state: exporting
+    either would hand out memory this state no longer owns, so export refuses before any handle."""
+    space = build_virtual_model(small_llama2())
+    ls = space.layout(PS(4, 1, 1))
+    for cut in ("release", "hand_over"):
+        st = _owned_cpu(ls, 1 << 14)
+        st.release_kind(1) if cut == "release" else st.hand_over(1)
+        with pytest.raises(RuntimeError, match="only a whole state"):
+            st.export()
+
+
 def test_adoption_is_refused_where_it_cannot_hold():
     space = build_virtual_model(small_llama2())
     ls, ld = space.layout(PS(4, 1, 1)), space.layout(PS(8, 1, 1, num_distributed_optimizer_instances=2))
