@@ -231,9 +231,10 @@ class SharedTrainingState:
 
     def _per_arena(self, pieces: np.ndarray):
         """The pieces of each arena in batches of at most 128 granules, addressed by granule within
-        the batch: (arena, pieces, granule pointers, granule bytes, first granule's buffer id)."""
+        the batch: (arena, pieces, granule pointers, granule bytes, first granule's buffer id).  A
+        released or handed-over granule has no bytes, so a piece there is refused before any launch."""
         pcs = self.buffers.split_pieces(pieces)
-        nbytes = self.buffers.nbytes()
+        ptrs, nbytes = self.buffer_ptrs(), self.buffer_bytes()
         for a in range(4):
             ids = self.buffers.granules_of(a)
             for lo in range(ids.start, ids.stop, self._SYNTH_MAX_BUFFERS):
@@ -242,7 +243,7 @@ class SharedTrainingState:
                 if len(sel) == 0:
                     continue
                 sel["buf"] -= lo
-                yield a, sel, self._ptrs[lo:hi], nbytes[lo:hi], lo
+                yield a, sel, ptrs[lo:hi], nbytes[lo:hi], lo
 
     def fill_synthetic(self, seed: int, params=None, fp32: bool = True, bf16: bool = True) -> None:
         """Write the seeded synthetic values of every stored element (see csrc/synth.hip)."""

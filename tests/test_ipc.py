@@ -241,6 +241,27 @@ def test_export_refuses_a_state_that_is_not_whole():
             st.export()
 
 
+def test_synthetic_fill_refuses_granules_the_state_no_longer_owns():
+    """The synthetic fill and check address a state's granules through its own pointers and sizes:
+    a released or handed-over granule has no bytes, so a piece there is refused on the host
+    (OUT_OF_BOUNDS), where a whole state gets as far as looking for a device."""
+    space = build_virtual_model(small_llama2())
+    ls = space.layout(PS(4, 1, 1))
+    for cut in (None, "release", "hand_over"):
+        st = _owned_cpu(ls, 1 << 14)
+        if cut == "release":
+            st.release_kind(1)
+        elif cut == "hand_over":
+            st.hand_over(2)
+        for a, pcs, ptrs, nb, _ in st._per_arena(ls.pieces()):
+            if a != 1:
+                continue
+            with pytest.raises(_native.EmrsError) as e:
+                _native.synth_fill(pcs, ptrs, nb, 1, 0)
+            assert e.value.code == (-6 if cut is None else -2)
+            break
+
+
 def test_adoption_is_refused_where_it_cannot_hold():
     space = build_virtual_model(small_llama2())
     ls, ld = space.layout(PS(4, 1, 1)), space.layout(PS(8, 1, 1, num_distributed_optimizer_instances=2))
