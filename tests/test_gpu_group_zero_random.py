@@ -4,7 +4,7 @@ Every fp32 element of the new state is checked against the generator's closed
 form (its value depends only on parameter, kind and full-tensor index, so an
 instance placed on the wrong rank reads wrong), and the plan's own
 verification must find no difference.  PP 1 only: with PP > 1 the instance rule
-is this build's extension, pinned elsewhere.
+is an extension past the reference, pinned elsewhere.
 """
 
 import numpy as np

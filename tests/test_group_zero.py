@@ -27,7 +27,7 @@ CASES = [
     ("1to3_tp2", PS(4, 2, 1), PS(12, 2, 1, num_distributed_optimizer_instances=3)),
     # Extension, not parity: with PP > 1 the reference's master of a stage >= 1 inter-instance group
     # is a rank the old world did not have, so it has no state to migrate (transfer.py:361-371,
-    # training_state.py:40-60).  This case pins the build's rule instead: a new rank reads the
+    # training_state.py:40-60).  This case pins the planner's rule instead: a new rank reads the
     # shard of the same stage and partial-DP rank.
     ("1to4_pp2", PS(4, 1, 2), PS(16, 1, 2, num_distributed_optimizer_instances=4)),
     # The reference's own precondition for Group-ZeRO is CP > 1 (parallel_strategy.py:99-106).

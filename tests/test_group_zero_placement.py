@@ -45,9 +45,9 @@ CASES = [
     ("w12_g2_w6", PS(12, 1, 1, num_distributed_optimizer_instances=2), PS(6, 1, 1), False, W12_G2_TO_W6),
 ]
 
-# This build's extension past the reference: with PP 2 the first rank of a stage-1 inter-instance
-# group (global rank 4 or 5 of W8) did not exist in the W4 world, so the reference's master has no
-# state to migrate.  The build reads the shard of the same stage and partial-DP rank instead:
+# An extension past the reference: with PP 2 the first rank of a stage-1 inter-instance group
+# (global rank 4 or 5 of W8) did not exist in the W4 world, so the reference's master has no state
+# to migrate.  The planner reads the shard of the same stage and partial-DP rank instead:
 # stage s, dp d of W8 (rank 4s+d) holds stage s, dp d mod 2 of W4 (rank 2s + d mod 2).
 PP2_EXTENSION = ("w4pp2_w8pp2_g2_extension", PS(4, 1, 2), PS(8, 1, 2, num_distributed_optimizer_instances=2),
                  True, {0: 0, 1: 1, 2: 0, 3: 1, 4: 2, 5: 3, 6: 2, 7: 3})
