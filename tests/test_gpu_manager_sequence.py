@@ -30,13 +30,17 @@ CHAIN = [dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_paralle
          dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1)]
 
 
-@pytest.mark.parametrize("low_memory", [False, True], ids=["whole", "staged"])
-def test_full_size_chain_through_the_manager(gpu_device, low_memory):
-    mgr = ElasticMegatronManager(CHAIN, ms.llama2_7b(), device=gpu_device, low_memory=low_memory)
+@pytest.mark.parametrize("low_memory,share", [(False, None), (True, None), (False, 1 << 30)],
+                         ids=["whole", "staged", "shared"])
+def test_full_size_chain_through_the_manager(gpu_device, low_memory, share):
+    """``shared``: every state held in 1 GiB granules, so the Group-ZeRO hops take instance 0 over
+    instead of copying it."""
+    mgr = ElasticMegatronManager(CHAIN, ms.llama2_7b(), device=gpu_device, low_memory=low_memory,
+                                 share_granule_bytes=share)
     try:
         mgr.training_state.fill_synthetic(SEED)
         for k, nxt in enumerate(CHAIN[1:], 1):
-            print(f"chain hop {k}: -> {nxt}, low_memory={low_memory}", flush=True)
+            print(f"chain hop {k}: -> {nxt}, low_memory={low_memory}, granules {share}", flush=True)
             assert mgr.reshard(nxt, is_meta_device=True) is None
             state = mgr.reshard(nxt, verify=True)
             assert mgr.last_verification.bit_exact, k
@@ -49,10 +53,12 @@ def test_full_size_chain_through_the_manager(gpu_device, low_memory):
         torch.cuda.empty_cache()
 
 
-def test_many_switches_keep_memory_steady(gpu_device):
+@pytest.mark.parametrize("share", [None, 1 << 20], ids=["arenas", "granules"])
+def test_many_switches_keep_memory_steady(gpu_device, share):
     """Two hundred switches of a small model through the manager, cycling through five strategies
     (a Group-ZeRO hop included): after the first cycle has built and cached every plan, device
-    memory in use does not grow, and the final state holds the generator's values."""
+    memory in use does not grow, and the final state holds the generator's values.  In granules,
+    the Group-ZeRO hops take instance 0 over, so ownership moves between states every cycle."""
     from tests.helpers import small_llama2
 
     seq = [dict(world_size=8, tensor_model_parallel_size=2, pipeline_model_parallel_size=1),
@@ -61,7 +67,7 @@ def test_many_switches_keep_memory_steady(gpu_device):
            dict(world_size=8, tensor_model_parallel_size=1, pipeline_model_parallel_size=1,
                 num_distributed_optimizer_instances=2),
            dict(world_size=4, tensor_model_parallel_size=1, pipeline_model_parallel_size=1)]
-    mgr = ElasticMegatronManager(seq, small_llama2(), device=gpu_device)
+    mgr = ElasticMegatronManager(seq, small_llama2(), device=gpu_device, share_granule_bytes=share)
     mgr.training_state.fill_synthetic(SEED)
     quiet = __import__("logging").getLogger("test.quiet")
     quiet.addHandler(__import__("logging").NullHandler())
