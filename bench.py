@@ -762,11 +762,11 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
     param = [a.tensors[x] for x in a.buffers.granules_of(3)]
     res = {}
     for name, plan in plans.items():
-        torch.cuda.reset_peak_memory_stats(dev)
         before = torch.cuda.memory_allocated(dev)
         b = SharedTrainingState.allocate(ld, dev, g, param_granules=param,
                                          adopted=a.leading_fp32_granules(n) if name == "taken_over" else None)
         new_bytes = torch.cuda.memory_allocated(dev) - before
+        both_states = torch.cuda.memory_allocated(dev)        # source and new state together
         tm.prepare(plan, dev)
         step_ms = timed_launches(lambda: tm.execute_states(plan, a, b, stream), args.steps, args.warmup, stream)
         bad, first = b.verify_synthetic(SEED)
@@ -777,6 +777,7 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
         ms = sum(step_ms) / len(step_ms)
         res[name] = {"ms": round(ms, 3), "min_ms": round(min(step_ms), 3), "payload_bytes": plan.payload_bytes,
                      "traffic_bytes": plan.traffic_bytes, "new_state_allocated_bytes": new_bytes,
+                     "both_states_allocated_bytes": both_states,
                      "traffic_gbps": round(plan.traffic_bytes / ms / 1e6, 1),
                      "verified_bit_exact": exact}
         print(f"[bench] {name}: {ms:.2f} ms, {res[name]['traffic_gbps']} GB/s", file=sys.stderr, flush=True)

@@ -105,3 +105,4 @@ def test_adopt_line(gpu_device):
         assert c[k]["verified_bit_exact"] is True and c[k]["reshard_end_to_end"]["verified_bit_exact"] is True
     assert abs(c["taken_over"]["traffic_bytes"] / c["copied"]["traffic_bytes"] - 2 / 3) < 0.01
     assert c["taken_over"]["new_state_allocated_bytes"] < c["copied"]["new_state_allocated_bytes"]
+    assert c["taken_over"]["both_states_allocated_bytes"] < c["copied"]["both_states_allocated_bytes"]
