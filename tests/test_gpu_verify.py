@@ -145,3 +145,43 @@ def test_manager_reshard_with_verification(gpu_device):
             rep = mgr.last_verification
             assert rep.bit_exact and rep.elements > 0
         assert mgr.training_state.verify_synthetic(SEED)[0] == 0
+
+
+@pytest.mark.parametrize("granule", [None, 1 << 16], ids=["arenas", "granules"])
+@pytest.mark.parametrize("no_alloc", [False, True], ids=["compare", "compare_static"])
+def test_compare_reads_a_state_against_itself(gpu_device, granule, no_alloc):
+    """A comparison only reads, so its source and destination may be the same memory (a state that
+    took over part of its source's).  The identity switch S -> S, compared between a state and
+    itself, finds every element equal: in arenas, and in granules of 64 KiB (hundreds of buffers
+    a side, the pointer-table path), with either entry point."""
+    from elasticmegatron_amd.resharding.granules import GranuleBuffers
+    from elasticmegatron_amd.resharding.tensors import rebase_on_tensors
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+
+    space = build_virtual_model(small_llama2())
+    s = PS(8, 2, 1)
+    space.register_reshard(s, s)
+    lay = space.layout(s)
+    table, groups, aux_groups = lower_transfer(lay, lay, with_groups=True)
+    if granule is None:
+        st = TrainingState.allocate(lay, gpu_device)
+        sizes = [lay.fp32_numel * 4] * 3 + [lay.bf16_numel * 2]
+        ptrs = st.arena_ptrs()
+    else:
+        gb = GranuleBuffers(lay, granule)
+        table, origin = rebase_on_tensors(table, gb, gb, return_origin=True)
+        groups, aux_groups = groups[origin], aux_groups[origin]
+        st = SharedTrainingState.allocate(lay, gpu_device, granule)
+        sizes, ptrs = gb.nbytes(), st.buffer_ptrs()
+        assert len(ptrs) > 128
+    st.fill_synthetic(SEED)
+    plan = _native.Plan(table, sizes, sizes)
+    n_groups = 4 * len(space.all_virtual_params)
+    print(f"case self-compare granule={granule} no_alloc={no_alloc}: {len(ptrs)} buffers a side", flush=True)
+    stats = plan.compare(ptrs, ptrs, groups, aux_groups, n_groups, torch.cuda.current_stream(gpu_device).cuda_stream,
+                         no_alloc=no_alloc)
+    assert int(stats["elements"].sum()) > 0
+    assert int(stats["mismatches"].sum()) == 0
+    with pytest.raises(_native.EmrsError) as e:       # an execution over the same memory is refused
+        plan.execute(ptrs, ptrs, torch.cuda.current_stream(gpu_device).cuda_stream)
+    assert e.value.code == -8
