@@ -84,3 +84,35 @@ def test_llama2_13b_switch_fits_in_one_gpu(gpu_device):
         gc.collect()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+
+
+def _random_chains(n=6):
+    import numpy as np
+
+    from tests.test_gpu_random_medium import _medium_spec
+    from tests.test_random_switches import _random_strategy
+
+    out = []
+    for k in range(7000, 7000 + n):
+        rng = np.random.default_rng(k)
+        spec = _medium_spec(rng, k)
+        seq = [_random_strategy(rng, spec) for _ in range(3)]
+        out.append(pytest.param(spec, seq, id=f"{k}-{'moe' if spec.num_experts else 'dense'}-" + "-".join(
+            f"tp{s.tensor_model_parallel_size}pp{s.pipeline_model_parallel_size}w{s.world_size}" for s in seq)))
+    return out
+
+
+@pytest.mark.parametrize("spec,seq", _random_chains())
+def test_random_staged_chain(gpu_device, spec, seq):
+    """Seeded medium models (dense and MoE) through a chain of three random strategies, every switch
+    staged and verified on the device stage by stage, each source arena released after its stage;
+    the last state holds the generator's values."""
+    mgr = ElasticMegatronManager(seq, spec, device=gpu_device, low_memory=True)
+    mgr.training_state.fill_synthetic(SEED)
+    for s in seq[1:]:
+        print(f"case staged {spec.name} {spec.num_params()} params -> {s}", flush=True)
+        mgr.reshard(s, verify=True)
+        assert mgr.last_verification.bit_exact
+    torch.cuda.synchronize()
+    bad, first = mgr.training_state.verify_synthetic(SEED)
+    assert bad == 0, first
