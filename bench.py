@@ -794,7 +794,8 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3
         bad, _ = new.verify_synthetic(SEED)
-        return new, {"wall_ms": round(wall, 2), "launch_ms": round(mgr.last_transfer_ms, 2), "verified_bit_exact": bad == 0}
+        return new, {"wall_ms": round(wall, 2), "launch_ms": round(mgr.last_transfer_ms, 2),
+                     "verified_bit_exact": bad == 0}
 
     kept, e2e_copy = manager_switch(False)
     del kept
@@ -811,7 +812,8 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
         "ms_per_step": t["ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32 (bitwise copy)", "data": "synthetic (seeded)",
         "config": {"workload": desc + f", both states in {g}-byte granules", "params": spec.num_params(),
-                   "granules_taken_over_per_fp32_arena": n, "speedup_vs_copied": round(res["copied"]["ms"] / t["ms"], 3),
+                   "granules_taken_over_per_fp32_arena": n,
+                   "speedup_vs_copied": round(res["copied"]["ms"] / t["ms"], 3),
                    **res, "launch": launch_shape()},
         "roofline": {"bound": "hbm", "achieved": t["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4),

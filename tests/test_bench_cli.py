@@ -87,7 +87,8 @@ def test_committed_traffic_describes_the_current_plan(traffic_file):
     kind = "transfer" if backup is None else ("backup_up" if backup else "backup_down")
     if variant == "taken_over":   # bench.py --adopt: 1 GiB granules, instance 0 taken over
         g = 1 << 30
-        plan = TransferManager().compile_granules(ls, ld, g, g, kind, adopt_granules=adoptable_granules(ls, ld, g, kind))
+        n = adoptable_granules(ls, ld, g, kind)
+        plan = TransferManager().compile_granules(ls, ld, g, g, kind, adopt_granules=n)
     else:
         assert variant == ""
         plan = TransferManager().compile(ls, ld, kind)

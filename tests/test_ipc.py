@@ -21,8 +21,8 @@ from elasticmegatron_amd.resharding.granules import GranuleBuffers
 from elasticmegatron_amd.resharding.model_spec import ModelSpec, llama2_7b, tiny_llama2
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from elasticmegatron_amd.transfer import ipc_manager as ipc
-from elasticmegatron_amd.transfer.transfer import (CompiledTensorPlan, TransferManager, adoptable_granules, held_granules,
-                                                   shares_params)
+from elasticmegatron_amd.transfer.transfer import (CompiledTensorPlan, TransferManager, adoptable_granules,
+                                                   held_granules, shares_params)
 from tests.helpers import small_llama2
 
 
