@@ -70,6 +70,52 @@ def test_captured_reshard_replays_bit_exact(gpu_device, per_tensor):
     assert bad == 0, first
 
 
+def test_captured_taken_over_group_zero_switch_replays_bit_exact(gpu_device):
+    """A Group-ZeRO scale-up between states in 64 KiB granules (hundreds of buffers a side, the
+    pointer-table path) whose new state holds the old one's instance 0: captured once, replayed
+    with the new state's own granules scrambled in between, and with the source refilled (which
+    also rewrites the taken-over head, the same memory)."""
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+    from elasticmegatron_amd.transfer.transfer import adoptable_granules
+
+    g = 1 << 16
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(PS(4, 1, 1)), space.layout(PS(8, 1, 1, num_distributed_optimizer_instances=2))
+    n = adoptable_granules(ls, ld, g, "backup_up")
+    tm = TransferManager()
+    plan = tm.compile_granules(ls, ld, g, g, "backup_up", adopt_granules=n)
+    a = SharedTrainingState.allocate(ls, gpu_device, g)
+    a.fill_synthetic(SEED)
+    b = SharedTrainingState.allocate(ld, gpu_device, g, param_granules=[a.tensors[x] for x in a.buffers.granules_of(3)],
+                                     adopted=a.leading_fp32_granules(n))
+    own = [b.tensors[x] for k in range(3) for x in b.buffers.granules_of(k)[n:]]
+    assert len(plan.dst) > 128
+
+    def run():
+        tm.execute_states(plan, a, b)
+
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    torch.cuda.synchronize()
+    for k in range(3):
+        print(f"case graph replay {k} (Group ZeRO, instance 0 taken over)", flush=True)
+        for t in own:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        bad, first = b.verify_synthetic(SEED)
+        assert bad == 0, (k, first)
+    a.fill_synthetic(SEED + 1)
+    graph.replay()
+    torch.cuda.synchronize()
+    bad, first = b.verify_synthetic(SEED + 1)
+    assert bad == 0, first
+
+
 def test_capture_refuses_calls_that_would_allocate(gpu_device):
     """A first call on the device (table upload) or a call whose base pointers differ from the
     plan's first call (its own pointer table) cannot be replayed from a graph: under capture it
