@@ -214,7 +214,7 @@ class ElasticMegatronManager:
         return t.elapsed
 
     def transfer_staged(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
-                        verify: bool = False):
+                        verify: bool = False, *, lost_ranks=()):
         """The switch in three launches, one optimizer kind at a time (see ``low_memory``).
 
         ``dst`` may start without fp32 arenas; each is allocated just before its stage.  With
@@ -222,11 +222,12 @@ class ElasticMegatronManager:
         it has been checked when ``verify`` is set.  ``src`` may be held in granules (a shared or
         received state).  Returns (ms of the stages' allocation, launch and release, summed;
         verification records or None); ``last_stage_ms`` has each stage's three times.
+        ``lost_ranks``: as for :meth:`reshard`.
         """
         if kind == "transfer" and src.layout.space is dst.layout.space:
             src.layout.space.register_reshard(src.parallel_strategy, dst.parallel_strategy)
         stages = self.transfer_manager.staged_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst),
-                                                         kind)
+                                                         kind, lost_ranks=lost_ranks)
         elapsed, stats, names = 0.0, None, None
         self.last_stage_ms = []
         for k, plan in enumerate(stages):
@@ -237,7 +238,7 @@ class ElasticMegatronManager:
             elapsed += ta.elapsed + te.elapsed
             self.last_stage_ms.append({"allocate": ta.elapsed, "execute": te.elapsed})
             if verify:
-                part, names = self.transfer_manager.verify_stats(src, dst, kind, stage=k)
+                part, names = self.transfer_manager.verify_stats(src, dst, kind, stage=k, lost_ranks=lost_ranks)
                 stats = merge_stats(stats, part)
                 if int(part["mismatches"].sum()):
                     # Stop before this stage's source is released; earlier stages were checked.
@@ -252,15 +253,15 @@ class ElasticMegatronManager:
         return elapsed, (stats, names) if verify else None
 
     def redundant_backup(self, src: TrainingState, dst: TrainingState, is_scale_up: bool,
-                         is_meta_device: bool = False) -> float:
+                         is_meta_device: bool = False, *, lost_ranks=()) -> float:
         """Group-ZeRO switch in the reference's argument order (elastic_manager.py:124-142);
         ``is_meta_device`` plans, caches and uploads the plan's tables without moving data.  The
         bf16 params stay where they are when ``dst`` shares ``src``'s, and are copied otherwise;
         the leading fp32 granules that ``dst`` holds in ``src``'s memory are left in place.
-        Returns the executor's ms."""
+        ``lost_ranks``: as for :meth:`reshard`.  Returns the executor's ms."""
         kind = backup_kind(is_scale_up, not shares_params(src, dst))
         plan = self.transfer_manager.plan_for_states(src.layout, dst.layout, _granule_of(src), _granule_of(dst), kind,
-                                                     adopt_granules=held_granules(src, dst))
+                                                     adopt_granules=held_granules(src, dst), lost_ranks=lost_ranks)
         if is_meta_device:
             self._prepare(plan, src)
         with Timer() as t:
@@ -268,11 +269,11 @@ class ElasticMegatronManager:
                 self.transfer_manager.execute_states(plan, src, dst)
         return t.elapsed
 
-    def _adoptable(self, src_state, dst_layout, kind: str, dst_granule_bytes, param) -> int:
+    def _adoptable(self, src_state, dst_layout, kind: str, dst_granule_bytes, param, lost_ranks=()) -> int:
         """Leading fp32 granules that the new state of a Group-ZeRO switch takes over from the old
         one: only from a shared state this process owns and the switch releases, into granules of
-        the same size, with the bf16 params shared too."""
-        if kind not in BACKUP_KINDS or param is None or not self.release_source:
+        the same size, with the bf16 params shared too, and with no rank's state lost."""
+        if kind not in BACKUP_KINDS or param is None or not self.release_source or lost_ranks:
             return 0
         if not isinstance(src_state, SharedTrainingState) or src_state.imported \
                 or src_state.granule_bytes != dst_granule_bytes:
@@ -325,7 +326,7 @@ class ElasticMegatronManager:
 
     def reshard(self, new_parallel_strategy: StrategyLike, logger: Optional[logging.Logger] = None,
                 is_meta_device: bool = False, save_ckpt: bool = False,
-                verify: bool = False) -> Optional[TrainingState]:
+                verify: bool = False, lost_ranks=None) -> Optional[TrainingState]:
         """Switch every rank's state to ``new_parallel_strategy``; returns the new state.
 
         ``is_meta_device=True`` builds and caches the plan, uploads its tables
@@ -338,6 +339,14 @@ class ElasticMegatronManager:
         before the old one is released (the reference's offline checkpoint
         comparison, tools/ckpt/compare_ckpt.py, done in place); the report is
         kept in ``last_verification`` and a mismatch raises RuntimeError.
+
+        ``lost_ranks`` (an extension; the reference has no recovery path): ranks of the current
+        world whose optimizer state is gone, such as a failed GPU's.  With more than one
+        distributed-optimizer instance every instance holds the whole fp32 state, so a
+        Group-ZeRO switch reads each shard of a lost rank from another instance's copy and reads
+        nothing from the lost ranks (their bf16 params are the model shard's, which every rank of
+        its DP group holds).  A shard whose every copy is lost, or any other kind of switch,
+        raises ValueError.
         """
         if is_meta_device and save_ckpt:
             raise AssertionError("Can't save checkpoint in meta device")
@@ -361,10 +370,12 @@ class ElasticMegatronManager:
         # (or are copied, when the new state cannot share them).
         param = self._carried_params(src_state, gd) if backup is not None else None
         kind = "transfer" if backup is None else backup_kind(backup, param is None)
+        lost = tuple(lost_ranks or ())
         # ... and instance 0's fp32 granules stay where they are when the new state can take them over.
-        adopt = self._adoptable(src_state, dst_layout, kind, gd, param)
-        plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind, adopt_granules=adopt)
-        stages = self.transfer_manager.staged_for_states(src_state.layout, dst_layout, gs, gd, kind) \
+        adopt = self._adoptable(src_state, dst_layout, kind, gd, param, lost)
+        plan = self.transfer_manager.plan_for_states(src_state.layout, dst_layout, gs, gd, kind, adopt_granules=adopt,
+                                                     lost_ranks=lost)
+        stages = self.transfer_manager.staged_for_states(src_state.layout, dst_layout, gs, gd, kind, lost_ranks=lost) \
             if self.low_memory else ()
         if is_meta_device:
             self._prepare(stages or plan, src_state)
@@ -373,7 +384,7 @@ class ElasticMegatronManager:
         if self.low_memory:
             dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),
                                                granule_bytes=ARENA_GRANULE_BYTES)
-            elapsed, checked = self.transfer_staged(src_state, dst_state, kind, verify)
+            elapsed, checked = self.transfer_staged(src_state, dst_state, kind, verify, lost_ranks=lost)
             if verify:
                 report = report_from_stats(*checked)
         else:
@@ -382,9 +393,9 @@ class ElasticMegatronManager:
             if backup is None:
                 elapsed = self.transfer_params(src_state, dst_state)
             else:
-                elapsed = self.redundant_backup(src_state, dst_state, backup)
+                elapsed = self.redundant_backup(src_state, dst_state, backup, lost_ranks=lost)
             if verify:
-                report = self.transfer_manager.verify(src_state, dst_state, kind)
+                report = self.transfer_manager.verify(src_state, dst_state, kind, lost_ranks=lost)
         self.last_transfer_ms = elapsed
         if verify:
             self.last_verification = report

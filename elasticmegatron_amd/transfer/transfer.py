@@ -64,17 +64,28 @@ def backup_kind(scale_up: bool, copy_bf16: bool = False) -> str:
 
 
 def _lower(src: StrategyLayout, dst: StrategyLayout, kind: str, include_bf16: bool, bf16_source: str,
-           with_groups: bool = False, in_place_below: int = 0):
+           with_groups: bool = False, in_place_below: int = 0, lost_ranks: Tuple[int, ...] = ()):
     """The segment table of a plan kind (with groups for verification)."""
     if kind == "transfer":
         if in_place_below:
             raise ValueError("only a Group-ZeRO switch can leave part of the new state in place")
+        if lost_ranks:
+            raise ValueError("only a Group-ZeRO switch has other optimizer instances to read a lost rank's state from")
         return lower_transfer(src, dst, include_bf16=include_bf16, bf16_source=bf16_source, with_groups=with_groups)
     if kind in BACKUP_KINDS:
         up, copy = BACKUP_KINDS[kind]
         return lower_redundant_backup(src, dst, scale_up=up, with_groups=with_groups, copy_bf16=copy,
-                                      in_place_below=in_place_below)
+                                      in_place_below=in_place_below, lost_ranks=lost_ranks)
     raise ValueError(kind)
+
+
+def _lost(lost_ranks) -> Tuple[int, ...]:
+    """Lost ranks as a sorted tuple without repeats (a plan-cache key part)."""
+    return tuple(sorted({int(r) for r in lost_ranks}))
+
+
+def _lost_key(lost: Tuple[int, ...]) -> Tuple:
+    return (("lost", lost),) if lost else ()
 
 
 def adoptable_granules(src: StrategyLayout, dst: StrategyLayout, granule_bytes: int, kind: str) -> int:
@@ -202,15 +213,18 @@ class TransferManager:
         return n
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                include_bf16: bool = True, in_place_below: int = 0) -> CompiledPlan:
-        """The arena plan of a switch; ``in_place_below``: see :func:`lower_redundant_backup`."""
+                include_bf16: bool = True, in_place_below: int = 0, *, lost_ranks=()) -> CompiledPlan:
+        """The arena plan of a switch; ``in_place_below`` and ``lost_ranks``: see
+        :func:`lower_redundant_backup`."""
+        lost = _lost(lost_ranks)
         key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16, self.bf16_source)
         if in_place_below:
             key += (("in-place", in_place_below),)
+        key += _lost_key(lost)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        table = _lower(src, dst, kind, include_bf16, self.bf16_source, in_place_below=in_place_below)
+        table = _lower(src, dst, kind, include_bf16, self.bf16_source, in_place_below=in_place_below, lost_ranks=lost)
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
         if kind == "transfer":
@@ -228,19 +242,20 @@ class TransferManager:
         return cp
 
     def compile_staged(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                       include_bf16: bool = True) -> Tuple[CompiledPlan, CompiledPlan, CompiledPlan]:
+                       include_bf16: bool = True, *, lost_ranks=()) -> Tuple[CompiledPlan, CompiledPlan, CompiledPlan]:
         """The switch as three launches, one per optimizer kind: ``main`` (with the bf16 params),
         ``exp_avg``, ``exp_avg_sq``.  Stage k reads source arena k only and writes destination arena
         k only (and the param arena), so a caller can allocate each destination arena just before its
         stage and release the source arena right after it, as the reference releases every
         optimizer tensor once it is sent (transfer.py:182-228, resharding_metadata.py:58-65).  The
         three together write exactly what :meth:`compile` writes."""
+        lost = _lost(lost_ranks)
         key = ("staged", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source)
+               self.bf16_source) + _lost_key(lost)
         stages = self._plans.get(key)
         if stages is not None:
             return stages
-        full = self.compile(src, dst, kind, include_bf16)
+        full = self.compile(src, dst, kind, include_bf16, lost_ranks=lost)
         out = []
         for k in range(3):
             t = _stage_rows(full.segments, k)
@@ -394,7 +409,7 @@ class TransferManager:
 
     def compile_granules(self, src: StrategyLayout, dst: StrategyLayout, src_granule_bytes: Optional[int],
                          dst_granule_bytes: Optional[int], kind: str = "transfer",
-                         include_bf16: bool = True, adopt_granules: int = 0) -> CompiledTensorPlan:
+                         include_bf16: bool = True, adopt_granules: int = 0, *, lost_ranks=()) -> CompiledTensorPlan:
         """The switch between states whose arenas are cut into granules (``SharedTrainingState``,
         handed between processes; ``None``: whole arenas, a ``TrainingState``).  ``plan.src`` /
         ``plan.dst`` are the :class:`~..resharding.granules.GranuleBuffers` of each side.
@@ -402,18 +417,21 @@ class TransferManager:
         ``adopt_granules``: a Group-ZeRO switch whose new state holds the old one's first
         ``adopt_granules`` granules of every fp32 arena (at most :func:`adoptable_granules`); the
         plan writes nothing there."""
+        lost = _lost(lost_ranks)
         key = ("granules", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source, src_granule_bytes, dst_granule_bytes, adopt_granules)
+               self.bf16_source, src_granule_bytes, dst_granule_bytes, adopt_granules) + _lost_key(lost)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
+        if adopt_granules and lost:
+            raise ValueError("a new state cannot take over granules that hold a lost rank's state")
         if adopt_granules:
             if src_granule_bytes is None or src_granule_bytes != dst_granule_bytes:
                 raise ValueError("adopting granules needs both states in granules of one size")
             if not 0 < adopt_granules <= self.adoptable(src, dst, src_granule_bytes, kind):
                 raise ValueError(f"the new state cannot take over {adopt_granules} granules of the old one")
         below = adopt_granules * src_granule_bytes // 4 if adopt_granules else 0
-        arena_plan = self.compile(src, dst, kind, include_bf16, in_place_below=below)
+        arena_plan = self.compile(src, dst, kind, include_bf16, in_place_below=below, lost_ranks=lost)
         sb, db = GranuleBuffers(src, src_granule_bytes), GranuleBuffers(dst, dst_granule_bytes)
         table = rebase_on_tensors(arena_plan.segments, sb, db)
         cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,
@@ -423,14 +441,16 @@ class TransferManager:
         return cp
 
     def staged_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
-                          dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True):
+                          dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True, *, lost_ranks=()):
         """The three plans of :meth:`compile_staged`, re-based onto granules when either side is held
         in them (a staged switch from a received state)."""
-        stages = self.compile_staged(src_layout, dst_layout, kind, include_bf16)
+        lost = _lost(lost_ranks)
+        stages = self.compile_staged(src_layout, dst_layout, kind, include_bf16, lost_ranks=lost)
         if src_granule_bytes is None and dst_granule_bytes is None:
             return stages
         key = ("staged-granules", src_layout.space.spec, src_layout.strategy, dst_layout.space.spec,
-               dst_layout.strategy, kind, include_bf16, self.bf16_source, src_granule_bytes, dst_granule_bytes)
+               dst_layout.strategy, kind, include_bf16, self.bf16_source, src_granule_bytes,
+               dst_granule_bytes) + _lost_key(lost)
         got = self._plans.get(key)
         if got is not None:
             return got
@@ -447,12 +467,12 @@ class TransferManager:
 
     def plan_for_states(self, src_layout: StrategyLayout, dst_layout: StrategyLayout, src_granule_bytes,
                         dst_granule_bytes, kind: str = "transfer", include_bf16: bool = True,
-                        adopt_granules: int = 0):
+                        adopt_granules: int = 0, *, lost_ranks=()):
         """The arena plan when both sides are whole arenas, else the granule plan."""
         if src_granule_bytes is None and dst_granule_bytes is None and not adopt_granules:
-            return self.compile(src_layout, dst_layout, kind, include_bf16)
+            return self.compile(src_layout, dst_layout, kind, include_bf16, lost_ranks=lost_ranks)
         return self.compile_granules(src_layout, dst_layout, src_granule_bytes, dst_granule_bytes, kind,
-                                     include_bf16, adopt_granules)
+                                     include_bf16, adopt_granules, lost_ranks=lost_ranks)
 
     def execute_states(self, plan, src, dst, stream: Optional[torch.cuda.Stream] = None) -> None:
         """Run ``plan`` (from :meth:`plan_for_states`) between two states of either kind."""
@@ -507,20 +527,22 @@ class TransferManager:
         self._comm_bytes += plan.reference_comm_bytes
 
     def verify(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
-               include_bf16: bool = True, stream: Optional[torch.cuda.Stream] = None) -> VerifyReport:
+               include_bf16: bool = True, stream: Optional[torch.cuda.Stream] = None, *,
+               lost_ranks=()) -> VerifyReport:
         """Check, on the device, that ``dst`` holds what the switch from ``src`` must produce.
 
         Replaces the reference's offline checkpoint comparison
         (tools/ckpt/compare_ckpt.py:17-76): per parameter and tensor kind, the
         bits that differ and compare_ckpt's max-abs / max-rel / RMS / relative
-        RMS.  ``src`` must still hold the state it was resharded from.
+        RMS.  ``src`` must still hold the state it was resharded from (with ``lost_ranks``, the
+        copies the switch read instead of theirs).
         """
-        stats, names = self.verify_stats(src, dst, kind, include_bf16, stream)
+        stats, names = self.verify_stats(src, dst, kind, include_bf16, stream, lost_ranks=lost_ranks)
         return report_from_stats(stats, names)
 
     def verify_stats(self, src: TrainingState, dst: TrainingState, kind: str = "transfer",
                      include_bf16: bool = True, stream: Optional[torch.cuda.Stream] = None,
-                     stage: Optional[int] = None):
+                     stage: Optional[int] = None, *, lost_ranks=()):
         """The records behind :meth:`verify` and the parameter names they index; with ``stage`` only
         what stage ``stage`` of :meth:`compile_staged` writes, so that a staged switch can check each
         stage before it releases that stage's source arena (:func:`.verify.merge_stats` adds them)."""
@@ -528,11 +550,13 @@ class TransferManager:
             raise RuntimeError("training states must live in GPU memory: verification has no CPU path")
         sl, dl = src.layout, dst.layout
         gs, gd = _granule_of(src), _granule_of(dst)
+        lost = _lost(lost_ranks)
         key = (sl.space.spec, sl.strategy, dl.space.spec, dl.strategy, kind, include_bf16, self.bf16_source, stage,
-               gs, gd)
+               gs, gd) + _lost_key(lost)
         vp = self._verify_plans.get(key)
         if vp is None:
-            table, groups, aux_groups = _lower(sl, dl, kind, include_bf16, self.bf16_source, with_groups=True)
+            table, groups, aux_groups = _lower(sl, dl, kind, include_bf16, self.bf16_source, with_groups=True,
+                                               lost_ranks=lost)
             if stage is not None:
                 m = _stage_mask(table, stage)
                 table, groups, aux_groups = table[m], groups[m], aux_groups[m]

@@ -113,7 +113,7 @@ def test_reshard_releases_the_source_state(monkeypatch):
 
     monkeypatch.setattr(TransferManager, "execute", lambda self, plan, src, dst, stream=None: None)
     monkeypatch.setattr(TransferManager, "verify", lambda self, src, dst, kind="transfer", include_bf16=True,
-                        stream=None: VerifyReport({}))
+                        stream=None, **kw: VerifyReport({}))
     monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
     mgr = ElasticMegatronManager(SEQ, tiny_llama2(), device="cpu")
     arenas = [weakref.ref(mgr.training_state.main)]

@@ -1,0 +1,123 @@
+"""GPU: a Group-ZeRO switch that reads a lost rank's optimizer state from another instance.
+
+With more than one distributed-optimizer instance every instance holds the
+whole fp32 state.  Here one source rank's fp32 state is poisoned with NaN, as
+a failed GPU's would be unreadable, and the switch is told that rank is lost:
+it must read that rank's shards from another instance's copy, so the new state
+holds the generator's values and the verification (which compares against the
+same copies) finds no difference.  Told nothing, the same switch copies the
+poison faithfully (its verification passes: it checks the copy) and the new
+state fails the generator check.  Whole switches over arenas and over
+granules, and staged switches.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy as PS
+from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+from elasticmegatron_amd.resharding.lowering import lower_redundant_backup
+from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from tests.helpers import SEED, small_llama2
+from tests.test_group_zero import _reads_from
+from tests.test_gpu_random_medium import _medium_spec
+from tests.test_random_switches import _random_strategy
+
+pytestmark = pytest.mark.gpu
+
+
+def _poison(state, rank):
+    """NaN over ``rank``'s region of the three fp32 arenas (arenas or granules)."""
+    lo, hi = state.layout.rank_fp32_slice(rank)
+    if not isinstance(state, SharedTrainingState):
+        for t in (state.main, state.exp_avg, state.exp_avg_sq):
+            t[lo:hi].fill_(float("nan"))
+        return
+    for k in range(3):
+        for b in state.buffers.granules_of(k):
+            g0 = state.buffers.offset[b]
+            a, z = max(lo, g0), min(hi, g0 + state.buffers.numel[b])
+            if a < z:
+                state.tensors[b][a - g0:z - g0].fill_(float("nan"))
+
+
+MODES = [pytest.param({}, id="arenas"), pytest.param({"share_granule_bytes": 1 << 16}, id="granules"),
+         pytest.param({"low_memory": True}, id="staged")]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("src,dst,lost", [
+    pytest.param(PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), 1, id="2to1-rank1"),
+    pytest.param(PS(8, 1, 1, num_distributed_optimizer_instances=2),
+                 PS(16, 1, 1, num_distributed_optimizer_instances=4), 0, id="2to4-rank0"),
+])
+def test_switch_reads_a_lost_rank_from_another_instance(gpu_device, mode, src, dst, lost):
+    spec = small_llama2()
+    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device, **mode)
+    old = mgr.training_state
+    old.fill_synthetic(SEED)
+    _poison(old, lost)
+    torch.cuda.synchronize()
+    print(f"case lost rank {lost}, {src} -> {dst}, {mode}: told nothing", flush=True)
+    blind = ElasticMegatronManager([src, dst], spec, device=gpu_device, training_state=old, release_source=False,
+                                   **mode)
+    copied = blind.reshard(dst, verify=True)
+    torch.cuda.synchronize()
+    assert blind.last_verification.bit_exact and copied.verify_synthetic(SEED)[0] > 0
+    del copied, blind
+    print(f"case lost rank {lost}, {src} -> {dst}, {mode}: told", flush=True)
+    mgr.reshard(dst, is_meta_device=True, lost_ranks=[lost])
+    new = mgr.reshard(dst, verify=True, lost_ranks=[lost])
+    torch.cuda.synchronize()
+    assert mgr.last_verification.bit_exact
+    bad, first = new.verify_synthetic(SEED)
+    assert bad == 0, first
+
+
+def _random_cases(n=6):
+    out = []
+    for k in range(8000, 8400):
+        rng = np.random.default_rng(k)
+        spec = _medium_spec(rng, k)
+        if spec.num_experts:
+            continue
+        base = _random_strategy(rng, spec)
+        inst, cp, up = int(rng.choice([2, 3])), int(rng.choice([1, 2])), len(out) % 2 == 1
+        tp, pp = base.tensor_model_parallel_size, base.pipeline_model_parallel_size
+        try:
+            src = PS(base.world_size * cp * inst, tp, pp, context_parallel_size=cp,
+                     num_distributed_optimizer_instances=inst)
+            dst = PS(base.world_size * cp * (2 * inst if up else 1), tp, pp, context_parallel_size=cp,
+                     num_distributed_optimizer_instances=2 * inst if up else 1)
+            for s in (src, dst):
+                s.validate_for(spec.num_layers, spec.num_experts)
+        except (ValueError, AssertionError, RuntimeError):
+            continue
+        # A rank the switch reads when nothing is lost (instance 0 on a scale-up, the kept instance on
+        # a scale-down), so that its loss reroutes reads.
+        space = build_virtual_model(spec)
+        ls, ld = space.layout(src), space.layout(dst)
+        plain = lower_redundant_backup(ls, ld, up)
+        read = [g for g in range(src.world_size) if _reads_from(plain, ls, g)]
+        lost = int(rng.choice(read))
+        out.append(pytest.param(spec, src, dst, lost, id=f"{k}-tp{tp}pp{pp}cp{cp}-{src.world_size}x{inst}-"
+                                f"{dst.world_size}x{dst.num_distributed_optimizer_instances}-lost{lost}"))
+        if len(out) == n:
+            break
+    return out
+
+
+@pytest.mark.parametrize("spec,src,dst,lost", _random_cases())
+def test_random_switch_with_a_lost_rank(gpu_device, spec, src, dst, lost):
+    """Seeded medium models (TP 1-4, PP 1-2, CP 1-2, 2 or 3 instances, up or down), one random
+    source rank lost and poisoned."""
+    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device)
+    mgr.training_state.fill_synthetic(SEED)
+    _poison(mgr.training_state, lost)
+    print(f"case {spec.name} {spec.num_params()} params: {src} -> {dst}, rank {lost} lost", flush=True)
+    new = mgr.reshard(dst, verify=True, lost_ranks=[lost])
+    torch.cuda.synchronize()
+    assert mgr.last_verification.bit_exact
+    bad, first = new.verify_synthetic(SEED)
+    assert bad == 0, first

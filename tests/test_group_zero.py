@@ -14,9 +14,10 @@ from hypothesis import HealthCheck, assume, given, settings
 from hypothesis import strategies as st
 
 from elasticmegatron_amd import ParallelStrategy as PS
-from elasticmegatron_amd.resharding.layout import SEG_DUP
+from elasticmegatron_amd.resharding.layout import SEG_DUP, SEG_ZERO_FILL
 from elasticmegatron_amd.resharding.lowering import in_place_prefix, lower_redundant_backup, payload_bytes, read_bytes
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+from elasticmegatron_amd.transfer.transfer import TransferManager
 from oracle import model
 from oracle import transfer as oracle1
 from tests.helpers import SEED, compare, compare_numpy, execute_numpy, extract, new_arenas, piece_fill_numpy, small_llama2, strat
@@ -229,3 +230,104 @@ def test_random_in_place_head_leaves_what_the_full_plan_leaves(sw):
     w, _ = extract(ld, want)
     h, _ = extract(ld, got)
     assert compare(h, {}, w, {}) == []
+
+
+LOST_CASES = [
+    ("2to1", PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), False),
+    ("3to1_tp2", PS(12, 2, 1, num_distributed_optimizer_instances=3), PS(4, 2, 1), False),
+    ("2to1_pp2", PS(8, 1, 2, num_distributed_optimizer_instances=2), PS(4, 1, 2), False),
+    ("2to4", PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(16, 1, 1, num_distributed_optimizer_instances=4),
+     True),
+]
+
+
+def _reads_from(table, layout, rank):
+    """fp32 elements the table reads from ``rank``'s region of the source arenas."""
+    lo, hi = layout.rank_fp32_slice(rank)
+    t = table[(table["src_buf"] < 3) & ((table["flags"] & SEG_ZERO_FILL) == 0)]
+    a, b = t["src_off"].astype(np.int64), (t["src_off"] + t["len"] * t["rows"]).astype(np.int64)
+    return int(np.clip(np.minimum(b, hi) - np.maximum(a, lo), 0, None).sum())
+
+
+@pytest.mark.parametrize("name,src,dst,up", LOST_CASES, ids=[c[0] for c in LOST_CASES])
+def test_lost_rank_is_read_from_another_instance(name, src, dst, up):
+    """Every instance holds the whole fp32 state, so with any one source rank lost the switch reads
+    that rank's shards from another instance's copy: it reads nothing from the lost rank, and with
+    the lost rank's memory poisoned the new state is still the oracle's."""
+    spec = small_llama2()
+    inv = model.inventory(spec)
+    S, D = strat(src), strat(dst)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, oracle1.build_src_world(inv, spec, S, SEED), up))
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    plain = lower_redundant_backup(ls, ld, up)
+    # Ranks the switch reads without a loss: instance 0 on a scale-up, the kept instances on a
+    # scale-down.  Losing one of them is what reroutes reads.
+    read = [g for g in range(src.world_size) if _reads_from(plain, ls, g)]
+    assert read
+    for g in range(src.world_size):
+        table = lower_redundant_backup(ls, ld, up, lost_ranks=[g])
+        assert _reads_from(table, ls, g) == 0, g
+        assert (g in read) == (not np.array_equal(table, plain)), g
+        assert payload_bytes(table) == payload_bytes(plain)
+        poisoned = [x.copy() for x in a]
+        lo, hi = ls.rank_fp32_slice(g)
+        for k in range(3):
+            poisoned[k][lo:hi] = 0x7FC00001
+        b = new_arenas(ld)
+        execute_numpy(table, poisoned, b)
+        got, _ = extract(ld, b)
+        assert compare(got, {}, want, {}) == [], g
+
+
+def test_lost_ranks_without_a_surviving_copy_are_refused():
+    space = build_virtual_model(small_llama2())
+    two, one = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1)
+    l2, l1 = space.layout(two), space.layout(one)
+    # Rank 1 of instance 0 and rank 5, its counterpart in instance 1, hold the same shards.
+    with pytest.raises(ValueError, match="every optimizer instance's copy"):
+        lower_redundant_backup(l2, l1, False, lost_ranks=[1, 5])
+    lower_redundant_backup(l2, l1, False, lost_ranks=[1, 6])     # different shards: both recoverable
+    with pytest.raises(ValueError, match="every optimizer instance's copy"):
+        lower_redundant_backup(l1, l2, True, lost_ranks=[2])     # one instance: no other copy
+    with pytest.raises(ValueError, match="ranks of the source world"):
+        lower_redundant_backup(l2, l1, False, lost_ranks=[8])
+    with pytest.raises(ValueError, match="only a Group-ZeRO switch"):
+        TransferManager().compile(space.layout(PS(8, 2, 1)), space.layout(PS(8, 1, 1)), lost_ranks=[0])
+
+
+@pytest.mark.parametrize("strategy", [PS(8, 1, 1, num_distributed_optimizer_instances=2),
+                                      PS(12, 2, 1, num_distributed_optimizer_instances=3),
+                                      PS(8, 1, 2, num_distributed_optimizer_instances=2),
+                                      PS(8, 2, 1, context_parallel_size=2, num_distributed_optimizer_instances=2)],
+                         ids=["w8g2", "w12tp2g3", "w8pp2g2", "w8cp2tp2g2"])
+def test_every_shard_has_a_copy_on_another_rank(strategy):
+    """With more than one optimizer instance, every fp32 run of every parameter is held by at least
+    one other rank, in another instance: the loss of any one rank loses no optimizer state."""
+    space = build_virtual_model(small_llama2())
+    lay = space.layout(strategy)
+    for vp in space.all_virtual_params:
+        if not lay.has_param(vp):
+            continue
+        holders = lay.fp32_holders(vp)
+        for h in holders:
+            copies = [x for x in holders if (x.tp_rank, x.lo, x.hi) == (h.tp_rank, h.lo, h.hi) and x.rank != h.rank]
+            assert copies and all(x.instance != h.instance for x in copies), (vp.name, h)
+
+
+def test_manager_plans_a_switch_with_lost_ranks():
+    """reshard(lost_ranks=...) plans the rerouted Group-ZeRO switch (its own cache entry, beside the
+    plain one) and refuses lost ranks for any other switch before allocating anything."""
+    from elasticmegatron_amd import ElasticMegatronManager
+
+    two, one = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1)
+    mgr = ElasticMegatronManager([two, one], small_llama2(), device="cpu")
+    assert mgr.reshard(one, is_meta_device=True) is None
+    assert mgr.reshard(one, is_meta_device=True, lost_ranks=[1]) is None
+    keys = list(mgr.transfer_manager._plans)
+    assert len(keys) == 2 and keys[1][-1] == ("lost", (1,)) and "lost" not in str(keys[0])
+    plain = ElasticMegatronManager([PS(8, 2, 1), PS(8, 1, 1)], small_llama2(), device="cpu")
+    with pytest.raises(ValueError, match="only a Group-ZeRO switch"):
+        plain.reshard(PS(8, 1, 1), is_meta_device=True, lost_ranks=[0])
