@@ -331,3 +331,46 @@ def test_manager_plans_a_switch_with_lost_ranks():
     plain = ElasticMegatronManager([PS(8, 2, 1), PS(8, 1, 1)], small_llama2(), device="cpu")
     with pytest.raises(ValueError, match="only a Group-ZeRO switch"):
         plain.reshard(PS(8, 1, 1), is_meta_device=True, lost_ranks=[0])
+
+
+def test_world_shrink_departing_ranks_only_send():
+    """A world shrink 8 -> 6: ranks 6 and 7 leave, yet their shards are read (they take part in the
+    transfer as senders only, through the union world group, megatron_state.py:180-189); no
+    destination rank 6 or 7 exists to receive."""
+    from elasticmegatron_amd.resharding.lowering import lower_transfer
+
+    space = build_virtual_model(small_llama2())
+    src, dst = PS(8, 1, 1), PS(6, 1, 1)
+    space.register_reshard(src, dst)
+    ls, ld = space.layout(src), space.layout(dst)
+    table = lower_transfer(ls, ld)
+    assert all(_reads_from(table, ls, g) > 0 for g in (6, 7))
+    assert ld.strategy.world_size == 6 and len(ld.rank_base) == 6
+
+
+@pytest.mark.parametrize("name,small,big", CASES, ids=[c[0] for c in CASES])
+def test_group_zero_replicas_equal_the_primary(name, small, big):
+    """After a scale-up every new instance's copy of a shard equals instance 0's (the primary) bit for
+    bit, even where every source rank's shard was made distinct first: the copies come from the
+    primary, not from the generator."""
+    space = build_virtual_model(small_llama2())
+    ls, ld = space.layout(small), space.layout(big)
+    table = lower_redundant_backup(ls, ld, True)
+    a, b = new_arenas(ls), new_arenas(ld)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    for g in range(small.world_size):         # every source rank's shard distinct
+        lo, hi = ls.rank_fp32_slice(g)
+        for k in range(3):
+            a[k][lo:hi] ^= np.uint32((g * 3 + k + 1) & 0x7F)
+    execute_numpy(table, a, b)
+    for vp in space.all_virtual_params:
+        if not ld.has_param(vp):
+            continue
+        hs = ld.fp32_holders(vp)
+        for h in hs:
+            if h.instance == 0:
+                continue
+            p = next(x for x in hs if x.instance == 0 and (x.tp_rank, x.lo, x.hi) == (h.tp_rank, h.lo, h.hi))
+            n = h.hi - h.lo
+            for k in range(3):
+                assert np.array_equal(b[k][h.offset:h.offset + n], b[k][p.offset:p.offset + n]), (vp.name, h)
