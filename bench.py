@@ -68,6 +68,8 @@ def workloads():
                                     PS(6, 1, 1)),
         "tiny-llama2-groupzero-1-2": ("tiny LLaMA-2 (2L h512) Group ZeRO instances 1 -> 2 (world 4 -> 8), fp32 only",
                                       ms.tiny_llama2, PS(4, 1, 1), PS(8, 1, 1, num_distributed_optimizer_instances=2)),
+        "tiny-llama2-groupzero-2-1": ("tiny LLaMA-2 (2L h512) Group ZeRO instances 2 -> 1 (world 8 -> 4), fp32 only",
+                                      ms.tiny_llama2, PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1)),
         # 182 GB per state: only a staged switch (--low-memory) fits it on one GPU.
         "llama2-13b-tp1dp8-tp4dp2": ("Llama-2-13B TP1PP1DP8 -> TP4PP1DP2, world 8, 40M buckets",
                                      ms.llama2_13b, PS(8, 1, 1), PS(8, 4, 1)),
@@ -164,6 +166,9 @@ def parse():
                     help="the switch from another process's state: a child exports the source in granules "
                          "(--ipc-granule-bytes), this process maps them and reshards into its own arenas")
     ap.add_argument("--ipc-granule-bytes", type=int, default=1 << 30)
+    ap.add_argument("--lost-ranks", type=lambda t: tuple(int(x) for x in t.split(",") if x), default=(),
+                    help="Group-ZeRO workloads: time the switch with these source ranks' fp32 state poisoned and "
+                         "read from another optimizer instance, beside the plain switch")
     ap.add_argument("--adopt", action="store_true",
                     help="Group-ZeRO workloads: time the switch between shared states (granules of "
                          "--ipc-granule-bytes) with instance 0 copied and with the new state taking it over, launch "
@@ -292,6 +297,8 @@ def main():
         return bench_ipc(args, desc, spec_fn, src, dst, dev, stream)
     if args.adopt:
         return bench_adopt(args, desc, spec_fn, src, dst, dev, stream)
+    if args.lost_ranks:
+        return bench_lost_ranks(args, desc, spec_fn, src, dst, dev, stream)
     repad = bool(opt and opt[0])
     backup = ParallelStrategy.is_redundant_backup(src, dst)
     spec = spec_fn()
@@ -818,6 +825,66 @@ def bench_adopt(args, desc, spec_fn, src, dst, dev, stream):
         "roofline": {"bound": "hbm", "achieved": t["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4),
                      "traffic": committed_traffic(f"{args.workload}.taken_over", None, t["traffic_bytes"])},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_lost_ranks(args, desc, spec_fn, src, dst, dev, stream):
+    """A Group-ZeRO switch timed twice on the same arenas: plain, then with the ``--lost-ranks``
+    source ranks' fp32 state poisoned with NaN and each of their shards read from another
+    optimizer instance.  Both results are checked against the generator, the second also by the
+    plan's comparison against the copies it read."""
+    import torch
+
+    from elasticmegatron_amd.megatron_manager.parallel_strategy import ParallelStrategy
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
+    from elasticmegatron_amd.transfer.transfer import TransferManager, backup_kind
+
+    backup = ParallelStrategy.is_redundant_backup(src, dst)
+    if backup is None:
+        print("--lost-ranks times a Group-ZeRO workload: other switches have no second copy to read", file=sys.stderr)
+        return 2
+    kind, lost = backup_kind(backup), args.lost_ranks
+    spec = spec_fn()
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(bf16_source=args.bf16_source)
+    plans = {"plain": tm.compile(ls, ld, kind), "lost": tm.compile(ls, ld, kind, lost_ranks=lost)}
+    a = TrainingState.allocate(ls, dev)
+    a.fill_synthetic(SEED)
+    b = TrainingState.allocate(ld, dev, param=a.param)
+    res = {}
+    for name, plan in plans.items():
+        if name == "lost":
+            for g in lost:
+                lo, hi = ls.rank_fp32_slice(g)
+                for t in (a.main, a.exp_avg, a.exp_avg_sq):
+                    t[lo:hi].fill_(float("nan"))
+        for t in (b.main, b.exp_avg, b.exp_avg_sq):
+            t.fill_(float("nan"))
+        tm.prepare(plan, dev)
+        step_ms = timed_launches(lambda: tm.execute(plan, a, b, stream), args.steps, args.warmup, stream)
+        bad, first = b.verify_synthetic(SEED, bf16=False)
+        exact = bad == 0 and tm.verify(a, b, kind, lost_ranks=lost if name == "lost" else ()).bit_exact
+        if not exact:
+            print(f"[bench] {name}: verification FAILED: {bad} elements, first {first}", file=sys.stderr)
+            return 3
+        ms = sum(step_ms) / len(step_ms)
+        res[name] = {"ms": round(ms, 3), "min_ms": round(min(step_ms), 3), "traffic_bytes": plan.traffic_bytes,
+                     "traffic_gbps": round(plan.traffic_bytes / ms / 1e6, 1), "verified_bit_exact": exact}
+        print(f"[bench] {name}: {ms:.2f} ms", file=sys.stderr, flush=True)
+    t = res["lost"]
+    out = {
+        "metric": f"Group-ZeRO switch with lost ranks read from another instance: ms per launch, {desc}, 1 GPU",
+        "value": t["ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t["ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (bitwise copy)", "data": "synthetic (seeded); the lost ranks' fp32 state poisoned with NaN",
+        "config": {"workload": desc, "params": spec.num_params(), "lost_ranks": list(lost), **res,
+                   "launch": launch_shape()},
+        "roofline": {"bound": "hbm", "achieved": t["traffic_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(t["traffic_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
     }
     print(json.dumps(out), flush=True)
     return 0

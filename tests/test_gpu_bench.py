@@ -106,3 +106,14 @@ def test_adopt_line(gpu_device):
     assert abs(c["taken_over"]["traffic_bytes"] / c["copied"]["traffic_bytes"] - 2 / 3) < 0.01
     assert c["taken_over"]["new_state_allocated_bytes"] < c["copied"]["new_state_allocated_bytes"]
     assert c["taken_over"]["both_states_allocated_bytes"] < c["copied"]["both_states_allocated_bytes"]
+
+
+@pytest.mark.gpu
+def test_lost_ranks_line(gpu_device):
+    """--lost-ranks: the Group-ZeRO switch plain and with rank 1's state poisoned and read from the
+    other instance, both checked, moving the same bytes."""
+    d = _bench("--workload", "tiny-llama2-groupzero-2-1", "--lost-ranks", "1", "--steps", "2", "--warmup", "1")
+    c = d["config"]
+    assert c["lost_ranks"] == [1]
+    assert c["plain"]["verified_bit_exact"] is True and c["lost"]["verified_bit_exact"] is True
+    assert c["plain"]["traffic_bytes"] == c["lost"]["traffic_bytes"]
