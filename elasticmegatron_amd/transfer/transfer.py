@@ -283,19 +283,21 @@ class TransferManager:
                 p.native.prepare(st.cuda_stream)
 
     def compile_shares(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                       include_bf16: bool = True) -> Tuple[Tuple[CompiledPlan, ...], CompiledPlan]:
+                       include_bf16: bool = True, *, lost_ranks=()) -> Tuple[Tuple[CompiledPlan, ...], CompiledPlan]:
         """The switch split by destination rank (``resharding.shares``): plan g writes rank g's
         fp32 shard, with the bf16 image of its ``main`` pieces, and nothing else; the last plan
         holds the segments whose primary destination is the bf16 param arena (none when the bf16
         params are cast).  With one rank per GPU, plan g is what GPU g would run, its sources then
         partly on peers.  Run in any order on the same arenas, they write what :meth:`compile`
-        writes."""
+        writes.  ``lost_ranks``: as for :func:`lower_redundant_backup`; no share then pulls from
+        them."""
+        lost = _lost(lost_ranks)
         key = ("shares", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source)
+               self.bf16_source) + _lost_key(lost)
         got = self._plans.get(key)
         if got is not None:
             return got
-        full = self.compile(src, dst, kind, include_bf16)
+        full = self.compile(src, dst, kind, include_bf16, lost_ranks=lost)
         per_rank, bf16 = destination_rank_shares(full.segments, dst)
 
         def plan_of(t):
@@ -327,19 +329,21 @@ class TransferManager:
         return cp
 
     def compile_share_tensors(self, src: StrategyLayout, dst: StrategyLayout, rank: int, kind: str = "transfer",
-                              include_bf16: bool = True) -> CompiledTensorPlan:
+                              include_bf16: bool = True, *, lost_ranks=()) -> CompiledTensorPlan:
         """Destination rank ``rank``'s share of the switch (:meth:`compile_shares`) over one buffer
         per stored tensor (:meth:`compile_tensors`).  It reads and writes only some of the tensors:
         ``plan.src_refs`` / ``plan.dst_refs``, the rest may be passed as None to
         :meth:`execute_tensors`.  With one rank per GPU, those are what GPU ``rank`` runs its part
         of the switch on: its own optimizer tensors, its part of its model shard's bf16 params, and
-        the source tensors it pulls, which in a multi-GPU job other GPUs hold."""
+        the source tensors it pulls, which in a multi-GPU job other GPUs hold.  With ``lost_ranks``
+        none of those is a lost rank's."""
+        lost = _lost(lost_ranks)
         key = ("share-tensors", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source, rank)
+               self.bf16_source, rank) + _lost_key(lost)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        per_rank, _ = self.compile_shares(src, dst, kind, include_bf16)
+        per_rank, _ = self.compile_shares(src, dst, kind, include_bf16, lost_ranks=lost)
         if not 0 <= rank < len(per_rank):
             raise ValueError(f"rank {rank} is not a destination rank (world {len(per_rank)})")
         sb, db = TensorBuffers(src), TensorBuffers(dst)

@@ -263,3 +263,34 @@ def test_partial_execution_checks_the_tensors_it_touches():
     src[i] = torch.empty(plan.src.numel[i] + 1, dtype=src[i].dtype)
     with pytest.raises(ValueError, match="does not match"):
         tm.execute_tensors(plan, src, dst)
+
+
+def test_shares_with_a_lost_rank_never_touch_its_tensors():
+    """With one rank per GPU and a GPU lost, each surviving rank's share of a Group-ZeRO switch pulls
+    the lost rank's shards from another instance: no share references a tensor of the lost rank
+    (they may all be None), and the shares together write what the plain switch writes."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    src, dst, lost = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), 1
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager()
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    whole = new_arenas(ld)
+    execute_numpy(lower_redundant_backup(ls, ld, False), a, whole)
+    got = new_arenas(ld)
+    for g in range(dst.world_size):
+        plan = tm.compile_share_tensors(ls, ld, g, "backup_down", lost_ranks=[lost])
+        sb, db = plan.src, plan.dst
+        assert all(sb.keys[i][1] != lost for i in plan.src_refs), g
+        src_bufs = [a[sb.arena[i]][sb.offset[i]:sb.offset[i] + sb.numel[i]].copy() if i in plan.src_refs else None
+                    for i in range(len(sb))]
+        dst_bufs = [np.zeros(db.numel[i], dtype=whole[db.arena[i]].dtype) if i in plan.dst_refs else None
+                    for i in range(len(db))]
+        execute_numpy(plan.segments, src_bufs, dst_bufs)
+        for i in plan.dst_refs:
+            got[db.arena[i]][db.offset[i]:db.offset[i] + db.numel[i]] = dst_bufs[i]
+    for k in range(3):
+        stored = whole[k] != 0xFFFFFFFF
+        assert np.array_equal(got[k][stored], whole[k][stored])
