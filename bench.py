@@ -173,6 +173,9 @@ def parse():
                     help="Group-ZeRO workloads: time the switch between shared states (granules of "
                          "--ipc-granule-bytes) with instance 0 copied and with the new state taking it over, launch "
                          "and ElasticMegatronManager.reshard end to end")
+    ap.add_argument("--shared-states", action="store_true",
+                    help="with --low-memory: every state held in granules of --ipc-granule-bytes, as a state another "
+                         "process can map")
     ap.add_argument("--low-memory", action="store_true",
                     help="time staged switches through ElasticMegatronManager(low_memory=True), alternating "
                          "directions: one optimizer kind per launch, arenas allocated and released as it goes")
@@ -500,7 +503,8 @@ def bench_low_memory(args, desc, spec_fn, src, dst, dev):
     quiet.addHandler(logging.NullHandler())
     quiet.propagate = False
     spec = spec_fn()
-    mgr = ElasticMegatronManager([src, dst], spec, device=dev, low_memory=True)
+    share = args.ipc_granule_bytes if args.shared_states else None
+    mgr = ElasticMegatronManager([src, dst], spec, device=dev, low_memory=True, share_granule_bytes=share)
     lay = {s: mgr.space_for(s).layout(s) for s in (src, dst)}
     plans = {(a, b): mgr.transfer_manager.compile(lay[a], lay[b]) for a, b in ((src, dst), (dst, src))}
     mgr.training_state.fill_synthetic(SEED)
@@ -543,7 +547,8 @@ def bench_low_memory(args, desc, spec_fn, src, dst, dev):
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16+fp32 (bitwise copy)",
         "data": "synthetic (seeded; bf16 ~N(0,0.02), main = upcast, exp_avg ~N(0,1e-3), exp_avg_sq = |N(0,1e-6)|)",
-        "config": {"workload": desc + ", staged: one optimizer kind per launch, arenas allocated and released as it goes",
+        "config": {"workload": desc + ", staged: one optimizer kind per launch, arenas allocated and released as it goes"
+                   + (f", states in {share}-byte granules" if share else ""),
                    "params": spec.num_params(), "payload_bytes_per_switch": int(sum(payload) / len(payload)),
                    "launch_ms_per_switch": round(launch_ms, 4), "last_switch_stages_ms": stages,
                    "peak_allocated_bytes": int(peak), "both_whole_states_bytes": int(both),

@@ -82,7 +82,10 @@ class ElasticMegatronManager:
         (``release_source``) leaves instance 0 where it is: the new state takes over the old one's
         leading granules of every fp32 arena (all of instance 0 with PP = 1) instead of copying
         them, so a scale-up to two instances moves two thirds of the bytes, a scale-down almost
-        none, and the peak memory drops by the granules taken over.
+        none, and the peak memory drops by the granules taken over.  With ``low_memory`` too, each
+        switch is staged between such states: a destination arena's granules are allocated just
+        before its stage, from the source granules the previous stage released (nothing is taken
+        over in a staged switch).
         """
         if not parallel_strategy_list:
             raise ValueError("parallel_strategy_list is empty")
@@ -108,8 +111,6 @@ class ElasticMegatronManager:
         self.release_source = release_source
         self.low_memory = low_memory
         self.share_granule_bytes = share_granule_bytes
-        if low_memory and share_granule_bytes is not None:
-            raise NotImplementedError("staged switches write TrainingState arenas, not shared granules")
         self.last_stage_ms: List[Dict[str, float]] = []   # staged switches: per stage, allocate / execute ms
         self.last_transfer_ms = 0.0
         self.last_verification = None
@@ -273,7 +274,7 @@ class ElasticMegatronManager:
         """Leading fp32 granules that the new state of a Group-ZeRO switch takes over from the old
         one: only from a shared state this process owns and the switch releases, into granules of
         the same size, with the bf16 params shared too, and with no rank's state lost."""
-        if kind not in BACKUP_KINDS or param is None or not self.release_source or lost_ranks:
+        if kind not in BACKUP_KINDS or param is None or not self.release_source or lost_ranks or self.low_memory:
             return 0
         if not isinstance(src_state, SharedTrainingState) or src_state.imported \
                 or src_state.granule_bytes != dst_granule_bytes:
@@ -382,8 +383,12 @@ class ElasticMegatronManager:
             return None
         report = None
         if self.low_memory:
-            dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),
-                                               granule_bytes=ARENA_GRANULE_BYTES)
+            if self.share_granule_bytes is not None:
+                dst_state = SharedTrainingState.allocate(dst_layout, src_state.device, self.share_granule_bytes,
+                                                         param_granules=param, kinds=())
+            else:
+                dst_state = TrainingState.allocate(dst_layout, src_state.device, param=param, kinds=(),
+                                                   granule_bytes=ARENA_GRANULE_BYTES)
             elapsed, checked = self.transfer_staged(src_state, dst_state, kind, verify, lost_ranks=lost)
             if verify:
                 report = report_from_stats(*checked)

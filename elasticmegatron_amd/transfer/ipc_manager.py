@@ -81,14 +81,19 @@ class SharedTrainingState:
     @classmethod
     def allocate(cls, layout: StrategyLayout, device=None, granule_bytes: int = DEFAULT_GRANULE_BYTES,
                  param_granules: Optional[List[torch.Tensor]] = None,
-                 adopted: Optional[Sequence[Sequence[torch.Tensor]]] = None) -> "SharedTrainingState":
+                 adopted: Optional[Sequence[Sequence[torch.Tensor]]] = None,
+                 kinds: Tuple[int, ...] = (0, 1, 2)) -> "SharedTrainingState":
         """Uninitialised granules for ``layout``, one allocation each; ``param_granules`` may be the
         bf16 granules of another state of the same model-parallel layout, shared instead.
         ``adopted``: per fp32 arena (main, exp_avg, exp_avg_sq), the same number of granules of
         another state to hold as this state's leading granules of that arena instead of allocating
         them (a Group-ZeRO switch that leaves instance 0 in place; the other state then hands them
-        over, see :meth:`hand_over`)."""
+        over, see :meth:`hand_over`).  ``kinds``: the fp32 arenas whose granules are allocated now;
+        the others start without memory and are allocated with :meth:`allocate_kind`, as a staged
+        switch does."""
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if adopted is not None and tuple(kinds) != (0, 1, 2):
+            raise ValueError("a state that takes over granules allocates every fp32 arena at once")
         if dev.type != "cuda":
             raise RuntimeError("a shared state lives in GPU memory")
         bufs = GranuleBuffers(layout, granule_bytes)
@@ -115,9 +120,32 @@ class SharedTrainingState:
                 tensors.append(param_granules[b - keep[0]])
             elif b in held:
                 tensors.append(held[b])
-            else:
+            elif a == ARENA_PARAM or a in kinds:
                 tensors.append(torch.empty(n, dtype=_DTYPES[a], device=dev))
-        return cls(layout, bufs, [t.data_ptr() for t in tensors], dev, tensors)
+            else:
+                tensors.append(None)
+        st = cls(layout, bufs, [0 if t is None else t.data_ptr() for t in tensors], dev, tensors)
+        for a in range(3):
+            st._released[a] = a not in kinds
+        return st
+
+    def allocate_kind(self, kind: int) -> None:
+        """Allocate the granules of fp32 arena ``kind`` (0 main, 1 exp_avg, 2 exp_avg_sq) if it has
+        none: a staged switch allocates each destination arena just before its stage.  With the
+        source in granules of the same size, those are the granules its previous stage released,
+        straight from torch's cache."""
+        if self.imported:
+            raise RuntimeError("an imported state's granules belong to the exporting process")
+        if kind not in (0, 1, 2):
+            raise ValueError("allocate_kind takes an fp32 arena: 0 main, 1 exp_avg, 2 exp_avg_sq")
+        if not self._released[kind]:
+            return
+        for b in self.buffers.granules_of(kind):
+            t = torch.empty(self.buffers.numel[b], dtype=torch.float32, device=self._device)
+            self.tensors[b] = t
+            self._ptrs[b] = t.data_ptr()
+            self._handed_over.discard(b)
+        self._released[kind] = False
 
     def leading_fp32_granules(self, n: int) -> List[List[torch.Tensor]]:
         """The first ``n`` granules of every fp32 arena of an owned state, for another state to
@@ -191,7 +219,7 @@ class SharedTrainingState:
             return
         if not self.imported:
             for b in self.buffers.granules_of(kind):
-                if b not in self._handed_over:
+                if b not in self._handed_over and self.tensors[b] is not None:
                     self.tensors[b].untyped_storage().resize_(0)
             self._released[kind] = True
             return

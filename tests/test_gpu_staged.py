@@ -116,3 +116,36 @@ def test_random_staged_chain(gpu_device, spec, seq):
     torch.cuda.synchronize()
     bad, first = mgr.training_state.verify_synthetic(SEED)
     assert bad == 0, first
+
+
+@pytest.mark.parametrize("factory,seq", [
+    (small_llama2, [PS(8, 1, 1), PS(8, 4, 1), PS(8, 2, 2)]),
+    (small_llama2, [PS(6, 1, 1), PS(12, 1, 1, num_distributed_optimizer_instances=2), PS(6, 1, 1)]),
+], ids=["llama2-tp1-tp4-tp2pp2", "groupzero-1-2-1"])
+def test_staged_switch_between_shared_states(gpu_device, factory, seq):
+    """low_memory with share_granule_bytes: each destination arena's granules are allocated just
+    before its stage and each source arena's released right after it, so no more than one
+    destination fp32 arena (and the destination's bf16 params when they are new) sits beside the
+    source at any time; every switch verified, the last state against the generator."""
+    from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+
+    g = 1 << 20
+    mgr = ElasticMegatronManager(seq, factory(), device=gpu_device, low_memory=True, share_granule_bytes=g)
+    mgr.training_state.fill_synthetic(SEED)
+    for s in seq[1:]:
+        old = mgr.training_state
+        print(f"case staged shared {factory.__name__} -> {s}", flush=True)
+        torch.cuda.synchronize()
+        gc.collect()
+        base = torch.cuda.memory_allocated(gpu_device)
+        torch.cuda.reset_peak_memory_stats(gpu_device)
+        new = mgr.reshard(s, verify=True)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated(gpu_device)
+        assert isinstance(new, SharedTrainingState) and mgr.last_verification.bit_exact
+        assert all(old.buffer_bytes()[b] == 0 for a in range(3) for b in old.buffers.granules_of(a))
+        shared = new.tensors[new.buffers.granules_of(3)[0]] is old.tensors[old.buffers.granules_of(3)[0]]
+        bound = new.layout.fp32_numel * 4 + (0 if shared else new.layout.bf16_numel * 2) + (64 << 20)
+        assert peak - base <= bound, (peak - base, bound)
+    bad, first = mgr.training_state.verify_synthetic(SEED)
+    assert bad == 0, first

@@ -298,10 +298,24 @@ def test_manager_plans_the_adopting_switch_for_an_owned_shared_state():
         assert (keys[0][-1] == state.layout.fp32_numel * 4 // g) is want and (keys[0][-1] == 0) is not want
 
 
-def test_low_memory_refuses_to_allocate_shared_states():
-    with pytest.raises(NotImplementedError):
-        ElasticMegatronManager([PS(8, 1, 1)], small_llama2(), device="meta", low_memory=True,
-                               share_granule_bytes=1 << 20)
+def test_staged_manager_plans_between_shared_states():
+    """low_memory with share_granule_bytes: the three staged plans are re-based onto granules of one
+    size on both sides, and a released arena's granules are allocated again, one arena at a time."""
+    spec = small_llama2()
+    src, dst, g = PS(8, 2, 1), PS(8, 4, 1), 1 << 16
+    mgr = ElasticMegatronManager([src, dst], spec, device="meta", low_memory=True, share_granule_bytes=g)
+    state = _owned_cpu(mgr.virtual_param_space.layout(src), g)
+    mgr.attach_training_state(state)
+    assert mgr.reshard(dst, is_meta_device=True) is None
+    staged = [(k, p) for k, p in mgr.transfer_manager._plans.items() if k[0] == "staged-granules"]
+    assert len(staged) == 1 and staged[0][0][-2:] == (g, g) and len(staged[0][1]) == 3
+    before = state.buffer_bytes()
+    state.release_kind(1)
+    assert all(state.buffer_bytes()[b] == 0 for b in state.buffers.granules_of(1))
+    state.allocate_kind(1)
+    assert state.buffer_bytes() == before and all(state.buffer_ptrs()[b] for b in state.buffers.granules_of(1))
+    with pytest.raises(RuntimeError):
+        _fake_shared(state.layout, g).allocate_kind(0)       # another process's memory
 
 
 def test_arena_release_protocol():
