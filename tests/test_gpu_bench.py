@@ -117,3 +117,12 @@ def test_lost_ranks_line(gpu_device):
     assert c["lost_ranks"] == [1]
     assert c["plain"]["verified_bit_exact"] is True and c["lost"]["verified_bit_exact"] is True
     assert c["plain"]["traffic_bytes"] == c["lost"]["traffic_bytes"]
+
+
+@pytest.mark.gpu
+def test_low_memory_shared_states_line(gpu_device):
+    """--low-memory --shared-states: staged switches between states held in granules, checked."""
+    d = _bench("--low-memory", "--shared-states", "--ipc-granule-bytes", str(1 << 20), "--steps", "2", "--warmup", "1")
+    c = d["config"]
+    assert c["verified_bit_exact"] is True and "granules" in c["workload"]
+    assert [sorted(s) for s in c["last_switch_stages_ms"]] == [["allocate", "execute", "release"]] * 3
