@@ -273,13 +273,15 @@ class ElasticMegatronManager:
     def _adoptable(self, src_state, dst_layout, kind: str, dst_granule_bytes, param, lost_ranks=()) -> int:
         """Leading fp32 granules that the new state of a Group-ZeRO switch takes over from the old
         one: only from a shared state this process owns and the switch releases, into granules of
-        the same size, with the bf16 params shared too, and with no rank's state lost."""
-        if kind not in BACKUP_KINDS or param is None or not self.release_source or lost_ranks or self.low_memory:
+        the same size, with the bf16 params shared too, in a whole (not staged) switch, and only
+        granules that end before the first lost rank's state."""
+        if kind not in BACKUP_KINDS or param is None or not self.release_source or self.low_memory:
             return 0
         if not isinstance(src_state, SharedTrainingState) or src_state.imported \
                 or src_state.granule_bytes != dst_granule_bytes:
             return 0
-        return self.transfer_manager.adoptable(src_state.layout, dst_layout, dst_granule_bytes, kind)
+        return self.transfer_manager.adoptable(src_state.layout, dst_layout, dst_granule_bytes, kind,
+                                               lost_ranks=lost_ranks)
 
     @staticmethod
     def _carried_params(src_state, dst_granule_bytes):

@@ -88,15 +88,20 @@ def _lost_key(lost: Tuple[int, ...]) -> Tuple:
     return (("lost", lost),) if lost else ()
 
 
-def adoptable_granules(src: StrategyLayout, dst: StrategyLayout, granule_bytes: int, kind: str) -> int:
+def adoptable_granules(src: StrategyLayout, dst: StrategyLayout, granule_bytes: int, kind: str,
+                       lost_ranks=()) -> int:
     """Leading granules of each fp32 arena that the new state of a Group-ZeRO switch can take over
     from the old one instead of copying them, both held in granules of ``granule_bytes``: whole
     granules of the same size on both sides inside :func:`in_place_prefix`.  With PP = 1 that is
     all of instance 0, a third of a scale-up to two instances' traffic and nearly all of a
-    scale-down's.  0 for any other switch."""
+    scale-down's.  With ``lost_ranks``, only granules that end before the first lost rank's
+    state.  0 for any other switch."""
     if kind not in BACKUP_KINDS or granule_bytes is None:
         return 0
-    return in_place_prefix(src, dst, BACKUP_KINDS[kind][0]) * 4 // granule_bytes
+    end = in_place_prefix(src, dst, BACKUP_KINDS[kind][0])
+    for g in lost_ranks:
+        end = min(end, src.rank_fp32_slice(int(g))[0])
+    return end * 4 // granule_bytes
 
 
 def _fixed_padding_space(src: StrategyLayout, dst: StrategyLayout):
@@ -204,12 +209,14 @@ class TransferManager:
                            if not (strategy is None or any(x == strategy for x in k))}
         return n
 
-    def adoptable(self, src: StrategyLayout, dst: StrategyLayout, granule_bytes: Optional[int], kind: str) -> int:
+    def adoptable(self, src: StrategyLayout, dst: StrategyLayout, granule_bytes: Optional[int], kind: str, *,
+                  lost_ranks=()) -> int:
         """:func:`adoptable_granules`, kept per switch (it walks every parameter's runs)."""
-        key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, granule_bytes, kind)
+        lost = _lost(lost_ranks)
+        key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, granule_bytes, kind) + _lost_key(lost)
         n = self._adoptable.get(key)
         if n is None:
-            n = self._adoptable[key] = adoptable_granules(src, dst, granule_bytes, kind)
+            n = self._adoptable[key] = adoptable_granules(src, dst, granule_bytes, kind, lost)
         return n
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
@@ -427,12 +434,10 @@ class TransferManager:
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        if adopt_granules and lost:
-            raise ValueError("a new state cannot take over granules that hold a lost rank's state")
         if adopt_granules:
             if src_granule_bytes is None or src_granule_bytes != dst_granule_bytes:
                 raise ValueError("adopting granules needs both states in granules of one size")
-            if not 0 < adopt_granules <= self.adoptable(src, dst, src_granule_bytes, kind):
+            if not 0 < adopt_granules <= self.adoptable(src, dst, src_granule_bytes, kind, lost_ranks=lost):
                 raise ValueError(f"the new state cannot take over {adopt_granules} granules of the old one")
         below = adopt_granules * src_granule_bytes // 4 if adopt_granules else 0
         arena_plan = self.compile(src, dst, kind, include_bf16, in_place_below=below, lost_ranks=lost)

@@ -17,6 +17,7 @@ import torch
 
 from elasticmegatron_amd import ElasticMegatronManager, ParallelStrategy as PS
 from elasticmegatron_amd.transfer.ipc_manager import SharedTrainingState
+from elasticmegatron_amd.transfer.transfer import adoptable_granules, backup_kind
 from elasticmegatron_amd.resharding.lowering import lower_redundant_backup
 from elasticmegatron_amd.resharding.virtual_param import build_virtual_model
 from tests.helpers import SEED, small_llama2
@@ -67,12 +68,24 @@ def test_switch_reads_a_lost_rank_from_another_instance(gpu_device, mode, src, d
     assert blind.last_verification.bit_exact and copied.verify_synthetic(SEED)[0] > 0
     del copied, blind
     print(f"case lost rank {lost}, {src} -> {dst}, {mode}: told", flush=True)
+    heads = old.buffer_ptrs() if isinstance(old, SharedTrainingState) else None
     mgr.reshard(dst, is_meta_device=True, lost_ranks=[lost])
     new = mgr.reshard(dst, verify=True, lost_ranks=[lost])
     torch.cuda.synchronize()
     assert mgr.last_verification.bit_exact
     bad, first = new.verify_synthetic(SEED)
     assert bad == 0, first
+    if heads is not None and not mode.get("low_memory"):
+        # Granules below the lost rank's state were taken over; none at or past it.
+        g = mode["share_granule_bytes"]
+        n = adoptable_granules(old.layout, new.layout, g, backup_kind(src.num_distributed_optimizer_instances <
+                                                                     dst.num_distributed_optimizer_instances),
+                               [lost])
+        assert n == old.layout.rank_fp32_slice(lost)[0] * 4 // g
+        ptrs = new.buffer_ptrs()
+        for k in range(3):
+            ids_old, ids_new = old.buffers.granules_of(k), new.buffers.granules_of(k)
+            assert [ptrs[b] for b in ids_new[:n]] == [heads[b] for b in ids_old[:n]]
 
 
 def _random_cases(n=6):

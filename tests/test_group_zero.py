@@ -374,3 +374,39 @@ def test_group_zero_replicas_equal_the_primary(name, small, big):
             n = h.hi - h.lo
             for k in range(3):
                 assert np.array_equal(b[k][h.offset:h.offset + n], b[k][p.offset:p.offset + n]), (vp.name, h)
+
+
+@pytest.mark.parametrize("lost", [2, 5], ids=["lost-in-instance-0", "lost-in-instance-1"])
+def test_in_place_head_with_a_lost_rank(lost):
+    """Taking over the old state's head and reading a lost rank from another instance combine: the
+    head stops before the first lost rank's state (a lost rank of instance 1, which a scale-down
+    to one instance never reads, leaves it whole), and the new state is the oracle's with the lost
+    rank's memory poisoned."""
+    from elasticmegatron_amd.transfer.transfer import adoptable_granules
+
+    spec = small_llama2()
+    src, dst = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1)
+    inv = model.inventory(spec)
+    S, D = strat(src), strat(dst)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, oracle1.build_src_world(inv, spec, S, SEED), False))
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    g = 4096
+    n = adoptable_granules(ls, ld, g, "backup_down", [lost])
+    below = n * g // 4
+    assert 0 < below <= ls.rank_fp32_slice(lost)[0]
+    if lost >= src.world_size // 2:
+        assert n == adoptable_granules(ls, ld, g, "backup_down")
+    table = lower_redundant_backup(ls, ld, False, in_place_below=below, lost_ranks=[lost])
+    assert _reads_from(table, ls, lost) == 0 and not _writes_below(table, below)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    lo, hi = ls.rank_fp32_slice(lost)
+    for k in range(3):
+        a[k][lo:hi] = 0x7FC00001
+    b = new_arenas(ld)
+    for k in range(3):
+        b[k][:below] = a[k][:below]
+    execute_numpy(table, a, b)
+    got, _ = extract(ld, b)
+    assert compare(got, {}, want, {}) == []
