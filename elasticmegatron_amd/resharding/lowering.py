@@ -278,10 +278,12 @@ def lower_transfer(src: StrategyLayout, dst: StrategyLayout, include_fp32: bool 
     return _assemble(fp32.table(), bf16.table(), fp32.group_array(), bf16.group_array(), with_groups)
 
 
-def _backup_sources(src: StrategyLayout, dst: StrategyLayout, vp, scale_up: bool, lost=frozenset()):
+def _backup_sources(src: StrategyLayout, dst: StrategyLayout, vp, scale_up: bool, lost=frozenset(),
+                    source_instance: int = 0):
     """(source holder, destination holder) of every fp32 run of ``vp`` in a Group-ZeRO switch: a
-    new instance's shard comes from instance 0 on a scale-up and from the same instance on a
-    scale-down (transfer.py:343-388).  A shard whose rank is in ``lost`` is read from the first
+    new instance's shard comes from instance ``source_instance`` (the reference's ``group_src``,
+    0 unless given) on a scale-up and from the same instance on a scale-down
+    (transfer.py:343-388).  A shard whose rank is in ``lost`` is read from the first
     other optimizer instance that holds it on a rank not lost (every instance holds the whole
     optimizer state, partitioned alike)."""
     src_by, replicas = {}, {}
@@ -290,7 +292,7 @@ def _backup_sources(src: StrategyLayout, dst: StrategyLayout, vp, scale_up: bool
         replicas.setdefault((h.tp_rank, h.lo, h.hi), []).append(h)
     out = []
     for h in dst.fp32_holders(vp):
-        s = src_by.get((0 if scale_up else h.instance, h.tp_rank, h.lo))
+        s = src_by.get((source_instance if scale_up else h.instance, h.tp_rank, h.lo))
         if s is None or s.hi != h.hi:
             raise AssertionError(f"{vp.name}: no matching source shard for a Group-ZeRO copy")
         if s.rank in lost:
@@ -318,7 +320,8 @@ def in_place_prefix(src: StrategyLayout, dst: StrategyLayout, scale_up: bool) ->
 
 
 def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: bool, with_groups: bool = False,
-                           copy_bf16: bool = False, in_place_below: int = 0, lost_ranks: Sequence[int] = ()):
+                           copy_bf16: bool = False, in_place_below: int = 0, lost_ranks: Sequence[int] = (),
+                           source_instance: int = 0):
     """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
 
     On a scale-up every new instance of a shard is filled from instance 0's
@@ -347,11 +350,17 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     whose every copy is lost raises ValueError.  The bf16 params are the
     model shard's, held by every rank of its DP group, and are not affected.
 
+    ``source_instance``: on a scale-up, the optimizer instance whose copy fills
+    the new ones (the reference's ``group_src``, transfer.py:343-371).
+
     ``with_groups``: as for :func:`lower_transfer`.
     """
     space = src.space
     if src.strategy.optimizer_data_parallel_size != dst.strategy.optimizer_data_parallel_size:
         raise AssertionError("Group-ZeRO switch must keep the optimizer DP size")
+    if not 0 <= source_instance < src.strategy.num_distributed_optimizer_instances:
+        raise ValueError(f"source instance {source_instance} is not an optimizer instance of the source "
+                         f"({src.strategy.num_distributed_optimizer_instances} instances)")
     lost = frozenset(int(r) for r in lost_ranks)
     if any(not 0 <= r < src.strategy.world_size for r in lost):
         raise ValueError(f"lost ranks must be ranks of the source world (0..{src.strategy.world_size - 1})")
@@ -363,7 +372,7 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
         g = vp.global_index if with_groups else 0
         # Destinations per source shard, in destination order.
         fills: Dict[int, Tuple[Holder, List[Holder]]] = {}
-        for s, h in _backup_sources(src, dst, vp, scale_up, lost):
+        for s, h in _backup_sources(src, dst, vp, scale_up, lost, source_instance):
             if h.offset < in_place_below:
                 if s.offset != h.offset:
                     raise AssertionError(f"{vp.name}: a run below the in-place bound is not at its source's offset")

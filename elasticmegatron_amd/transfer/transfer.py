@@ -64,7 +64,8 @@ def backup_kind(scale_up: bool, copy_bf16: bool = False) -> str:
 
 
 def _lower(src: StrategyLayout, dst: StrategyLayout, kind: str, include_bf16: bool, bf16_source: str,
-           with_groups: bool = False, in_place_below: int = 0, lost_ranks: Tuple[int, ...] = ()):
+           with_groups: bool = False, in_place_below: int = 0, lost_ranks: Tuple[int, ...] = (),
+           source_instance: int = 0):
     """The segment table of a plan kind (with groups for verification)."""
     if kind == "transfer":
         if in_place_below:
@@ -75,7 +76,8 @@ def _lower(src: StrategyLayout, dst: StrategyLayout, kind: str, include_bf16: bo
     if kind in BACKUP_KINDS:
         up, copy = BACKUP_KINDS[kind]
         return lower_redundant_backup(src, dst, scale_up=up, with_groups=with_groups, copy_bf16=copy,
-                                      in_place_below=in_place_below, lost_ranks=lost_ranks)
+                                      in_place_below=in_place_below, lost_ranks=lost_ranks,
+                                      source_instance=source_instance)
     raise ValueError(kind)
 
 
@@ -220,18 +222,22 @@ class TransferManager:
         return n
 
     def compile(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                include_bf16: bool = True, in_place_below: int = 0, *, lost_ranks=()) -> CompiledPlan:
-        """The arena plan of a switch; ``in_place_below`` and ``lost_ranks``: see
-        :func:`lower_redundant_backup`."""
+                include_bf16: bool = True, in_place_below: int = 0, *, lost_ranks=(),
+                source_instance: int = 0) -> CompiledPlan:
+        """The arena plan of a switch; ``in_place_below``, ``lost_ranks`` and ``source_instance``:
+        see :func:`lower_redundant_backup`."""
         lost = _lost(lost_ranks)
         key = (src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16, self.bf16_source)
         if in_place_below:
             key += (("in-place", in_place_below),)
         key += _lost_key(lost)
+        if source_instance:
+            key += (("source-instance", source_instance),)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        table = _lower(src, dst, kind, include_bf16, self.bf16_source, in_place_below=in_place_below, lost_ranks=lost)
+        table = _lower(src, dst, kind, include_bf16, self.bf16_source, in_place_below=in_place_below, lost_ranks=lost,
+                       source_instance=source_instance)
         sb = [src.fp32_numel * 4] * 3 + [src.bf16_numel * 2]
         db = [dst.fp32_numel * 4] * 3 + [dst.bf16_numel * 2]
         if kind == "transfer":
@@ -610,12 +616,15 @@ class TransferManager:
         self.execute(plan, src, dst, stream)
         return plan
 
-    def redundant_backup(self, is_scale_up: bool, src: TrainingState, dst: TrainingState,
+    def redundant_backup(self, is_scale_up: bool, src: TrainingState, dst: TrainingState, group_src: int = 0,
                          stream=None) -> CompiledPlan:
         """Group-ZeRO switch (transfer.py:343-388): fp32 shards replicated or dropped.  As in the
         reference, only the optimizer tensors move; ``ElasticMegatronManager`` also copies the bf16
-        params when the new state cannot share them."""
-        plan = self.compile(src.layout, dst.layout, backup_kind(is_scale_up))
+        params when the new state cannot share them.  ``group_src``: on a scale-up, the optimizer
+        instance whose copy fills the new ones (the reference's broadcast root in the
+        inter-instance group)."""
+        plan = self.compile(src.layout, dst.layout, backup_kind(is_scale_up),
+                            source_instance=group_src if is_scale_up else 0)
         self.execute(plan, src, dst, stream)
         return plan
 

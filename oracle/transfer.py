@@ -281,11 +281,13 @@ def rebuild_bf16(inv, hp, dst, dst_world, plans, tp_of_dst):
     return out
 
 
-def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None, dist=None):
+def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None, dist=None, group_src=0):
     """Group-ZeRO switch (transfer.py:343-388): migrate on the master, broadcast to the instances.
 
     ``params``: the parameter ids to move (default: all); ``src_world`` must hold them.
-    ``dist``: the destination's DP distributions, when the caller has them already."""
+    ``dist``: the destination's DP distributions, when the caller has them already.
+    ``group_src``: on a scale-up, the master is the ``group_src``-th rank of each inter-instance
+    group (transfer.py:360-371), so instance ``group_src``'s shard is what every instance gets."""
     dist = dist if dist is not None else dp_distributions(inv, dst, hp)
     out = {}
     for p in inv:
@@ -298,7 +300,7 @@ def redundant_backup(inv, hp, src, dst, src_world, scale_up, params=None, dist=N
                 for inst in range(dst.inst):
                     s = stage(p, dst.pp, hp.num_layers)
                     g = s * (dst.dp * dst.cp * dst.tp) + (inst * dst.pdp + r) * dst.tp + t
-                    src_inst = 0 if scale_up else inst
+                    src_inst = group_src if scale_up else inst
                     gs = s * (src.dp * src.cp * src.tp) + (src_inst * src.pdp + r) * src.tp + t
                     info = src_world[pid][gs]
                     assert info.rng == (lo, hi)

@@ -57,3 +57,32 @@ def test_redundant_backup_matches_oracle1(gpu_device, name, small, big, scale_up
     # The model-parallel shards do not change under Group ZeRO: the bf16 arena is not written at all.
     assert bool((b.param.view(torch.int16) == CANARY16).all())
     assert padding_damage(b) == 0
+
+
+@pytest.mark.parametrize("group_src", [0, 1])
+def test_scale_up_from_a_chosen_source_instance(gpu_device, group_src):
+    """TransferManager.redundant_backup(is_scale_up, src, dst, group_src), the reference's broadcast
+    root (transfer.py:343-371): from two instances to four, every new instance holds instance
+    ``group_src``'s shard; each source rank's shard distinct, against Oracle-1."""
+    from elasticmegatron_amd import ParallelStrategy as PS
+
+    src, dst = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(16, 1, 1, num_distributed_optimizer_instances=4)
+    print(f"group-zero scale-up from instance {group_src}: {src} -> {dst}", flush=True)
+    spec = small_llama2()
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    perturb_per_rank(a)
+    b = TrainingState.allocate(ld, gpu_device)
+    fill_canaries(b)
+    TransferManager().redundant_backup(True, a, b, group_src)
+    torch.cuda.synchronize()
+    inv = model.inventory(spec)
+    world = oracle1.build_src_world(inv, spec, strat(src), SEED)
+    perturb_per_rank(world)
+    want = oracle1.flatten(oracle1.redundant_backup(inv, spec, strat(src), strat(dst), world, True,
+                                                    group_src=group_src))
+    got, _ = extract(ld, _host_arenas(b))
+    assert compare(got, {}, want, {}) == []
+    assert padding_damage(b) == 0

@@ -410,3 +410,42 @@ def test_in_place_head_with_a_lost_rank(lost):
     execute_numpy(table, a, b)
     got, _ = extract(ld, b)
     assert compare(got, {}, want, {}) == []
+
+
+def test_scale_up_from_another_source_instance_matches_oracle():
+    """TransferManager.redundant_backup(is_scale_up, src, dst, group_src) as the reference takes it
+    (transfer.py:343-371): on a scale-up from two instances to four, instance ``group_src``'s copy
+    fills every new instance.  With every source rank's shard made distinct, the product's plan
+    equals Oracle-1 for group_src 0 and 1, and the two differ."""
+    import inspect
+
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+    from tests.helpers import perturb_per_rank
+
+    params = list(inspect.signature(TransferManager.redundant_backup).parameters)
+    assert params[1:5] == ["is_scale_up", "src", "dst", "group_src"]
+    spec = small_llama2()
+    inv = model.inventory(spec)
+    src, dst = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(16, 1, 1, num_distributed_optimizer_instances=4)
+    S, D = strat(src), strat(dst)
+    space = build_virtual_model(spec)
+    ls, ld = space.layout(src), space.layout(dst)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    for g in range(src.world_size):
+        lo, hi = ls.rank_fp32_slice(g)
+        for k in range(3):
+            a[k][lo:hi] ^= np.uint32((g * 3 + k + 1) & 0x7F)
+    got_by = {}
+    for gs in (0, 1):
+        world = oracle1.build_src_world(inv, spec, S, SEED)
+        perturb_per_rank(world)
+        want = oracle1.flatten(oracle1.redundant_backup(inv, spec, S, D, world, True, group_src=gs))
+        b = new_arenas(ld)
+        execute_numpy(lower_redundant_backup(ls, ld, True, source_instance=gs), a, b)
+        got, _ = extract(ld, b)
+        assert compare(got, {}, want, {}) == [], gs
+        got_by[gs] = got
+    assert any(not np.array_equal(got_by[0][k]["main"], got_by[1][k]["main"]) for k in got_by[0])
+    with pytest.raises(ValueError, match="not an optimizer instance"):
+        lower_redundant_backup(ls, ld, True, source_instance=2)
