@@ -341,7 +341,11 @@ class ElasticMegatronManager:
         ``verify=True`` compares the new state with the old one on the device
         before the old one is released (the reference's offline checkpoint
         comparison, tools/ckpt/compare_ckpt.py, done in place); the report is
-        kept in ``last_verification`` and a mismatch raises RuntimeError.
+        kept in ``last_verification`` and a mismatch raises RuntimeError.  The
+        old state then stays the live state, whole, except after a staged
+        (``low_memory``) switch with ``release_source``: each stage's source arena
+        is released once that stage has been checked, so a mismatch in a later
+        stage leaves the old state without the arenas of the stages before it.
 
         ``lost_ranks`` (an extension; the reference has no recovery path): ranks of the current
         world whose optimizer state is gone, such as a failed GPU's.  With more than one
