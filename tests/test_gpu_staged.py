@@ -149,3 +149,29 @@ def test_staged_switch_between_shared_states(gpu_device, factory, seq):
         assert peak - base <= bound, (peak - base, bound)
     bad, first = mgr.training_state.verify_synthetic(SEED)
     assert bad == 0, first
+
+
+def test_failed_stage_stops_before_its_source_is_released(gpu_device, monkeypatch):
+    """A mismatch found in stage 1 (exp_avg) raises before that stage's source arena is released:
+    the old state keeps exp_avg and exp_avg_sq, having released main after stage 0 passed."""
+    spec = small_llama2()
+    src, dst = PS(8, 1, 1), PS(8, 4, 1)
+    mgr = ElasticMegatronManager([src, dst], spec, device=gpu_device, low_memory=True)
+    old = mgr.training_state
+    old.fill_synthetic(SEED)
+    real, calls = mgr.transfer_manager.execute_states, []
+
+    def corrupting(plan, s, d, stream=None):
+        real(plan, s, d, stream)
+        calls.append(plan)
+        if len(calls) == 2:                      # stage 1 writes exp_avg
+            d.exp_avg.view(torch.int32)[d.layout.rank_fp32_slice(0)[0]] ^= 1
+
+    monkeypatch.setattr(mgr.transfer_manager, "execute_states", corrupting)
+    print("case staged switch with a planted mismatch in stage 1", flush=True)
+    with pytest.raises(RuntimeError, match="stage 1"):
+        mgr.reshard(dst, verify=True)
+    assert mgr.training_state is old
+    assert old.main.numel() == 0 and old.exp_avg.numel() > 0 and old.exp_avg_sq.numel() > 0
+    bad, first = old.verify_synthetic(SEED, params=None, bf16=True, fp32=False)
+    assert bad == 0, first
