@@ -134,3 +134,37 @@ def test_random_switch_with_a_lost_rank(gpu_device, spec, src, dst, lost):
     assert mgr.last_verification.bit_exact
     bad, first = new.verify_synthetic(SEED)
     assert bad == 0, first
+
+
+def test_full_size_switch_with_a_lost_rank(gpu_device):
+    """Llama-2-7B Group ZeRO 2 -> 1 instances (world 12 -> 6) with rank 3's state poisoned and read
+    from instance 1: every fp32 element of the new state holds the generator's value, and the
+    plan's comparison against the copies it read finds no difference."""
+    import gc
+
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.resharding import model_spec as ms
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    gc.collect()
+    torch.cuda.empty_cache()
+    src, dst, lost = PS(12, 1, 1, num_distributed_optimizer_instances=2), PS(6, 1, 1), 3
+    space = build_virtual_model(ms.llama2_7b())
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(check_disjoint=True)
+    plan = tm.compile(ls, ld, "backup_down", lost_ranks=[lost])
+    print(f"case full-size Llama-2-7B {src} -> {dst}, rank {lost} lost: {plan.segments.shape[0]} segments", flush=True)
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    _poison(a, lost)
+    b = TrainingState.allocate(ld, gpu_device, param=a.param)
+    try:
+        tm.execute(plan, a, b)
+        torch.cuda.synchronize()
+        bad, first = b.verify_synthetic(SEED, bf16=False)
+        assert bad == 0, first
+        assert tm.verify(a, b, "backup_down", lost_ranks=[lost]).bit_exact
+    finally:
+        del a, b
+        gc.collect()
+        torch.cuda.empty_cache()
