@@ -325,7 +325,7 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     """fp32 segments of a Group-ZeRO switch (instances change, shards do not).
 
     On a scale-up every new instance of a shard is filled from instance 0's
-    copy (transfer.py:343-388).  The destinations of one source shard are
+    copy, or instance ``source_instance``'s (transfer.py:343-388).  The destinations of one source shard are
     taken in pairs, each pair as one duplicating segment: the shard is read
     once per two copies written.
 
@@ -346,9 +346,9 @@ def lower_redundant_backup(src: StrategyLayout, dst: StrategyLayout, scale_up: b
     ``lost_ranks``: source ranks whose fp32 state is gone (a failed GPU).  Every
     shard they held is read from another optimizer instance's copy instead,
     so nothing is read from them (an extension: the reference migrates each
-    instance from itself).  A shard
-    whose every copy is lost raises ValueError.  The bf16 params are the
-    model shard's, held by every rank of its DP group, and are not affected.
+    instance from itself).  A shard whose every copy is lost raises
+    ValueError.  The bf16 params are the model shard's, held by every rank of
+    its DP group, and are not affected.
 
     ``source_instance``: on a scale-up, the optimizer instance whose copy fills
     the new ones (the reference's ``group_src``, transfer.py:343-371).
