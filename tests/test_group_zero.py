@@ -449,3 +449,44 @@ def test_scale_up_from_another_source_instance_matches_oracle():
     assert any(not np.array_equal(got_by[0][k]["main"], got_by[1][k]["main"]) for k in got_by[0])
     with pytest.raises(ValueError, match="not an optimizer instance"):
         lower_redundant_backup(ls, ld, True, source_instance=2)
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.filter_too_much, HealthCheck.too_slow])
+@given(_group_zero_switches(), st.data())
+def test_random_lost_ranks_leave_what_the_plain_switch_leaves(sw, data):
+    """Random models, instance counts, PP and CP sizes and directions, with a random set of lost
+    source ranks: when every shard keeps a copy on a surviving rank, the rerouted plan reads
+    nothing from the lost ranks and, with their memory poisoned, leaves what the plain switch
+    leaves; otherwise it is refused."""
+    spec, small, big, up, _ = sw
+    src, dst = (small, big) if up else (big, small)
+    space = build_virtual_model(spec)
+    try:
+        ls, ld = space.layout(src), space.layout(dst)
+    except (AssertionError, RuntimeError, ValueError):
+        assume(False)
+    lost = data.draw(st.sets(st.integers(0, src.world_size - 1), min_size=1, max_size=3))
+    # A shard survives when some rank of another instance holding it is not lost.
+    survives = all(any(x.rank not in lost for x in ls.fp32_holders(vp) if (x.tp_rank, x.lo, x.hi) ==
+                       (h.tp_rank, h.lo, h.hi)) for vp in space.all_virtual_params if ls.has_param(vp)
+                   for h in ls.fp32_holders(vp))
+    if not survives:
+        with pytest.raises(ValueError, match="every optimizer instance's copy"):
+            lower_redundant_backup(ls, ld, up, lost_ranks=sorted(lost))
+        return
+    plain = lower_redundant_backup(ls, ld, up)
+    table = lower_redundant_backup(ls, ld, up, lost_ranks=sorted(lost))
+    assert all(_reads_from(table, ls, g) == 0 for g in lost)
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    want = new_arenas(ld)
+    execute_numpy(plain, a, want)
+    for g in lost:
+        lo, hi = ls.rank_fp32_slice(g)
+        for k in range(3):
+            a[k][lo:hi] = 0x7FC00001
+    got = new_arenas(ld)
+    execute_numpy(table, a, got)
+    w, _ = extract(ld, want)
+    h, _ = extract(ld, got)
+    assert compare(h, {}, w, {}) == []
