@@ -168,3 +168,53 @@ def test_full_size_switch_with_a_lost_rank(gpu_device):
         del a, b
         gc.collect()
         torch.cuda.empty_cache()
+
+
+def _zero_raw(base, numel, off, n, device):
+    """Zero fp32 elements [off, off + n) of a mapped buffer of ``numel`` elements, by a one-segment
+    zero-fill plan (another process's memory has no torch tensor here)."""
+    from elasticmegatron_amd import _native
+    from elasticmegatron_amd.resharding.layout import SEG_ZERO_FILL, SEGMENT_DTYPE
+
+    assert 0 <= off and off + n <= numel
+    t = np.zeros(1, dtype=SEGMENT_DTYPE)
+    t[0] = (0, 0, 4, SEG_ZERO_FILL, 0, off, n, 1, 0, 0, 0, 0, 0, 0)
+    plan = _native.Plan(t, [16], [numel * 4])
+    with torch.cuda.device(device):
+        plan.execute([0], [base], torch.cuda.current_stream(device).cuda_stream)
+        torch.cuda.synchronize(device)
+
+
+def test_received_state_with_a_lost_rank(gpu_device):
+    """A two-instance state exported by another process, one of its ranks then lost (its mapped
+    memory poisoned here): the new process switches to one instance reading that rank's shards
+    from the other instance, copying the bf16 params since the exporter frees its memory."""
+    from elasticmegatron_amd.transfer import ipc_manager as ipc
+    from tests.test_gpu_ipc import _finish, _payload_line, _spawn_exporter
+
+    spec = small_llama2()
+    src, dst, lost = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), 2
+    child = _spawn_exporter(spec, src, (1 << 20) + 256 * 3)
+    state = None
+    try:
+        mgr = ElasticMegatronManager([src, dst], spec, device="meta")
+        line = _payload_line(child, 240)
+        state, _ = ipc.receive_training_state(line, gpu_device, space=mgr.virtual_param_space)
+        print(f"case received {src} with rank {lost} lost -> {dst}", flush=True)
+        lo, hi = state.layout.rank_fp32_slice(lost)
+        for k in range(3):
+            for b in state.buffers.granules_of(k):
+                g0, n = state.buffers.offset[b], state.buffers.numel[b]
+                a, z = max(lo, g0), min(hi, g0 + n)
+                if a < z:
+                    _zero_raw(state.buffer_ptrs()[b], n, a - g0, z - a, gpu_device)
+        assert state.verify_synthetic(SEED, bf16=False)[0] > 0      # the poison landed
+        mgr.attach_training_state(state)
+        new = mgr.reshard(dst, verify=True, lost_ranks=[lost])
+        torch.cuda.synchronize()
+        state = None
+        assert mgr.last_verification.bit_exact
+        bad, first = new.verify_synthetic(SEED)
+        assert bad == 0, first
+    finally:
+        _finish(child, state)
