@@ -126,3 +126,12 @@ def test_low_memory_shared_states_line(gpu_device):
     c = d["config"]
     assert c["verified_bit_exact"] is True and "granules" in c["workload"]
     assert [sorted(s) for s in c["last_switch_stages_ms"]] == [["allocate", "execute", "release"]] * 3
+
+
+@pytest.mark.gpu
+def test_lost_ranks_refuses_a_switch_without_a_second_copy(gpu_device):
+    """--lost-ranks on a switch that is not Group ZeRO exits 2 with a message: there is no other
+    optimizer instance to read a lost rank's state from."""
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--workload", TINY, "--lost-ranks", "1",
+                        "--steps", "1", "--warmup", "0"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "Group-ZeRO" in r.stderr and r.stdout.strip() == ""
