@@ -323,17 +323,19 @@ class TransferManager:
         return got
 
     def compile_tensors(self, src: StrategyLayout, dst: StrategyLayout, kind: str = "transfer",
-                        include_bf16: bool = True) -> CompiledTensorPlan:
+                        include_bf16: bool = True, *, lost_ranks=()) -> CompiledTensorPlan:
         """The switch over one buffer per stored tensor, as the reference holds them: the
         ``OptimizerTensorInfo`` tensors of every (rank, parameter) and the bf16 parameter of every
         model-parallel shard.  ``plan.src.keys`` / ``plan.dst.keys`` name the tensors in buffer
-        order."""
+        order.  ``lost_ranks``: as for :func:`lower_redundant_backup`; the lost ranks' tensors are
+        then not referenced and may be None."""
+        lost = _lost(lost_ranks)
         key = ("tensors", src.space.spec, src.strategy, dst.space.spec, dst.strategy, kind, include_bf16,
-               self.bf16_source)
+               self.bf16_source) + _lost_key(lost)
         cp = self._plans.get(key)
         if cp is not None:
             return cp
-        arena_plan = self.compile(src, dst, kind, include_bf16)
+        arena_plan = self.compile(src, dst, kind, include_bf16, lost_ranks=lost)
         sb, db = TensorBuffers(src), TensorBuffers(dst)
         table = rebase_on_tensors(arena_plan.segments, sb, db)
         cp = CompiledTensorPlan(table, _native.Plan(table, sb.nbytes(), db.nbytes(), self.check_disjoint), sb, db,

@@ -294,3 +294,27 @@ def test_shares_with_a_lost_rank_never_touch_its_tensors():
     for k in range(3):
         stored = whole[k] != 0xFFFFFFFF
         assert np.array_equal(got[k][stored], whole[k][stored])
+
+
+def test_tensor_plan_with_a_lost_rank_never_references_its_tensors():
+    """Over one buffer per stored tensor, a Group-ZeRO switch with a lost rank references none of
+    the lost rank's tensors (they may be None) and writes what the plain switch writes."""
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    src, dst, lost = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), 2
+    ls, ld = space.layout(src), space.layout(dst)
+    plan = TransferManager().compile_tensors(ls, ld, "backup_down", lost_ranks=[lost])
+    sb, db = plan.src, plan.dst
+    assert all(sb.keys[i][1] != lost for i in plan.src_refs)
+    assert any(sb.keys[i][1] == lost for i in range(len(sb)) if sb.arena[i] < 3)   # it has tensors to avoid
+    a = new_arenas(ls)
+    piece_fill_numpy(ls.pieces(), a, SEED)
+    whole = new_arenas(ld)
+    execute_numpy(lower_redundant_backup(ls, ld, False), a, whole)
+    src_bufs = [a[sb.arena[i]][sb.offset[i]:sb.offset[i] + sb.numel[i]].copy() if i in plan.src_refs else None
+                for i in range(len(sb))]
+    dst_bufs = [np.zeros(db.numel[i], dtype=whole[db.arena[i]].dtype) for i in range(len(db))]
+    execute_numpy(plan.segments, src_bufs, dst_bufs)
+    for i in plan.dst_refs:
+        assert np.array_equal(dst_bufs[i], whole[db.arena[i]][db.offset[i]:db.offset[i] + db.numel[i]]), db.keys[i]
