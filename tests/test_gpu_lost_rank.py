@@ -218,3 +218,27 @@ def test_received_state_with_a_lost_rank(gpu_device):
         assert bad == 0, first
     finally:
         _finish(child, state)
+
+
+def test_tensor_plan_with_a_lost_rank_runs_with_its_tensors_absent(gpu_device):
+    """Over one buffer per stored tensor, the lost rank's source tensors are passed as None (a
+    lost GPU's memory has no address): the switch runs and the new state holds the generator's
+    values."""
+    from elasticmegatron_amd.megatron_manager.training_state import TrainingState
+    from elasticmegatron_amd.transfer.transfer import TransferManager
+
+    space = build_virtual_model(small_llama2())
+    src, dst, lost = PS(8, 1, 1, num_distributed_optimizer_instances=2), PS(4, 1, 1), 2
+    ls, ld = space.layout(src), space.layout(dst)
+    tm = TransferManager(check_disjoint=True)
+    plan = tm.compile_tensors(ls, ld, "backup_down", lost_ranks=[lost])
+    a = TrainingState.allocate(ls, gpu_device)
+    a.fill_synthetic(SEED)
+    b = TrainingState.allocate(ld, gpu_device, param=a.param)
+    src_views = [None if plan.src.arena[i] < 3 and plan.src.keys[i][1] == lost else v
+                 for i, v in enumerate(plan.src.views(a))]
+    print(f"case per-tensor switch, rank {lost}'s {sum(v is None for v in src_views)} tensors absent", flush=True)
+    tm.execute_tensors(plan, src_views, plan.dst.views(b))
+    torch.cuda.synchronize()
+    bad, first = b.verify_synthetic(SEED, bf16=False)
+    assert bad == 0, first
